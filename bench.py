@@ -1,0 +1,241 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Headline (BASELINE.json `metric`, configs[1]): Q4_K decode GEMV at
+14336x4096, reported as achieved HBM GB/s = algorithmic bytes per call
+(W + x + y, the reference's formula, GEMVTests.swift:1438-1440) / average
+launch duration.  One step = one GEMV call over one of >= 768 MB of distinct
+weight copies (rotated so every call misses the 256 MB Infinity Cache), with
+x and y resident in HBM.  Timing uses HIP events on the launch stream around
+exactly `--steps` launches after `--warmup` untimed ones.
+
+Also reported in `results`: the other BASELINE GEMV shapes (Q8_0 3072x1024 and
+14336x4096, Q4_K 4096x14336, Q6_K 151936x1024 and 128256x4096).
+
+The cpu_baseline leg times the CPU oracle (a C restatement of the reference's
+Swift CPU dequant+dot loop, oracle/er_oracle.c) on a bounded sample of the
+same workload on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "quant GEMV achieved HBM GB/s (% of 8 TB/s) at 14336x4096; prefill GEMM TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 768 << 20
+
+BLOCK = {"q8_0": (34, 32), "q4_k": (144, 256), "q6_k": (210, 256)}
+ENCODE = {"q8_0": "encodeQ8_0Weights", "q4_k": "encodeQ4KWeights", "q6_k": "encodeQ6KWeights"}
+KERNEL_PREFIX = {"q8_0": "er_gemv_q8_0", "q4_k": "er_gemv_q4k", "q6_k": "er_gemv_q6k"}
+DSCALE = {"q8_0": {"dscale": 0.02}, "q4_k": {"dscale": 0.01, "dminscale": 0.01},
+          "q6_k": {"dscale": 0.005}}
+
+# (name, fmt, M, K, BASELINE config index)
+GEMV_WORKLOADS = [
+    ("q4_k_gemv_14336x4096", "q4_k", 14336, 4096, 2),
+    ("q4_k_gemv_4096x14336", "q4_k", 4096, 14336, 2),
+    ("q8_0_gemv_14336x4096", "q8_0", 14336, 4096, 1),
+    ("q8_0_gemv_3072x1024", "q8_0", 3072, 1024, 1),
+    ("q6_k_gemv_151936x1024", "q6_k", 151936, 1024, 3),
+    ("q6_k_gemv_128256x4096", "q6_k", 128256, 4096, 3),
+]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def weight_bytes(fmt: str, M: int, K: int) -> int:
+    bb, bw = BLOCK[fmt]
+    return M * (K // bw) * bb
+
+
+def algorithmic_bytes(fmt: str, M: int, K: int) -> int:
+    return weight_bytes(fmt, M, K) + 4 * K + 4 * M
+
+
+def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
+    import edgerunner_amd.synth as synth
+    from edgerunner_amd import GEMVKernel
+
+    gemv = GEMVKernel(ctx)
+    W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
+    x = synth.normal_f32(synth.seed(cfg, 1), K)
+    copies = max(2, -(-ROTATE_BYTES // W.nbytes))
+    stream = ctx.stream()
+    wbufs = [ctx.upload(W, stream) for _ in range(copies)]
+    xb = ctx.upload(x, stream)
+    yb = ctx.alloc(4 * M)
+    enc = getattr(gemv, ENCODE[fmt])
+    for i in range(warmup):
+        enc(stream, wbufs[i % copies], xb, yb, M, K)
+    stream.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record(stream)
+    for i in range(steps):
+        enc(stream, wbufs[i % copies], xb, yb, M, K)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1)
+    avg_us = ms * 1000.0 / steps
+    # per-launch event pairs: launch-gap-free kernel duration (diagnostic)
+    evs = [(ctx.event(), ctx.event()) for _ in range(min(steps, 64))]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        enc(stream, wbufs[i % copies], xb, yb, M, K)
+        b.record(stream)
+    stream.synchronize()
+    per = sorted(a.elapsed_ms(b) * 1000.0 for a, b in evs)
+    med_us = per[len(per) // 2]
+    for a, b in evs:
+        a.destroy()
+        b.destroy()
+    nbytes = algorithmic_bytes(fmt, M, K)
+    y = yb.download(np.float32, stream=stream)
+    for b in wbufs:
+        b.free()
+    xb.free()
+    yb.free()
+    e0.destroy()
+    e1.destroy()
+    stream.destroy()
+    return {
+        "fmt": fmt, "M": M, "K": K, "copies": copies, "bytes_per_call": nbytes,
+        "us_per_call": avg_us, "GBps": nbytes / (avg_us * 1e-6) / 1e9,
+        "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "us_per_call_event_pair_median": med_us,
+        "GBps_event_pair": nbytes / (med_us * 1e-6) / 1e9,
+        "ms_total": ms, "y_finite": bool(np.all(np.isfinite(y))),
+    }
+
+
+def cpu_baseline(fmt: str, M: int, K: int, cfg: int, budget_s: float) -> dict:
+    """Times the CPU oracle (oracle/er_oracle.c, the reference's Swift CPU
+    loop restated in C) on the same synthetic workload, all rows of the matrix,
+    repeated until `budget_s` seconds have passed."""
+    import edgerunner_amd.synth as synth
+    from oracle import ref
+
+    W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
+    x = synth.normal_f32(synth.seed(cfg, 1), K)
+    threads = min(16, os.cpu_count() or 1, ref.max_threads())
+    ref.gemv(fmt, W, x, M, K, threads=threads)  # warm
+    calls = 0
+    t0 = time.perf_counter()
+    while True:
+        ref.gemv(fmt, W, x, M, K, threads=threads)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    per_call = el / calls
+    nbytes = algorithmic_bytes(fmt, M, K)
+    return {
+        "value": nbytes / per_call / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"{calls} full {fmt.upper()} GEMV calls {M}x{K} in {el:.1f} s "
+                  f"({per_call * 1e3:.2f} ms/call, OpenMP rows split over {threads} threads)",
+        "us_per_call": per_call * 1e6,
+    }
+
+
+def load_traffic(name: str):
+    p = ROOT / "profiles" / "traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get(name)
+        except Exception:
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workloads", default="all",
+                    help="comma list of workload names, or 'all' / 'headline'")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is a design note, not built)"}))
+        return 2
+
+    from edgerunner_amd import Context
+    ctx = Context(0)
+    log(f"device {ctx.info.name.decode()} arch={ctx.arch} CUs={ctx.compute_units}")
+
+    head = GEMV_WORKLOADS[0]
+    if args.workloads == "all":
+        todo = GEMV_WORKLOADS
+    elif args.workloads == "headline":
+        todo = [head]
+    else:
+        names = set(args.workloads.split(","))
+        todo = [w for w in GEMV_WORKLOADS if w[0] in names]
+        if head not in todo:
+            todo = [head] + todo
+    results = {}
+    for name, fmt, M, K, cfg in todo:
+        log(f"{name}: running")
+        r = bench_gemv(ctx, fmt, M, K, cfg, args.steps, args.warmup)
+        results[name] = r
+        log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
+            f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s); event-pair median "
+            f"{r['us_per_call_event_pair_median']:.2f} us")
+
+    h = results[head[0]]
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline: running")
+        cpu = cpu_baseline(head[1], head[2], head[3], head[4], args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+
+    traffic = load_traffic(head[0])
+    out = {
+        "metric": METRIC,
+        "value": round(h["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": h["us_per_call"] / 1000.0,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded xoshiro256**, BASELINE.json config distributions)",
+        "config": {"workload": "Q4_K decode GEMV, W 14336x4096 (BASELINE configs[1]), x fp32, "
+                               "y fp32, 24 rotating weight copies",
+                   "M": head[2], "K": head[3], "format": "Q4_K"},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(h["GBps"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(h["frac_of_hbm_peak"], 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": ({k: (round(v, 3) if isinstance(v, float) else v)
+                          for k, v in cpu.items() if k != "us_per_call"} if cpu else None),
+        "results": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                         for kk, vv in v.items()} for k, v in results.items()},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

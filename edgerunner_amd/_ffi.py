@@ -1,0 +1,125 @@
+"""ctypes declarations of the C ABI in include/er_hip.h.
+
+The library is loaded from this package directory (it is built in-tree by
+``python -m edgerunner_amd.build``).  A missing library is an error: there is
+no CPU fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libedgerunner_hip.so"
+
+ER_OK = 0
+STATUS_NAMES = {
+    0: "ok",
+    1: "libraryNotFound",
+    2: "functionNotFound",
+    3: "encodingFailed",
+    4: "invalidMatrixShape",
+    5: "invalidVectorShape",
+    6: "invalidBlockDataCount",
+    7: "allocationFailed",
+    8: "invalidArgument",
+    9: "deviceError",
+}
+
+
+class er_buffer(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("length", C.c_uint64)]
+
+
+class er_tensor_storage(C.Structure):
+    _fields_ = [
+        ("buffer", er_buffer),
+        ("byte_offset", C.c_uint64),
+        ("data_type", C.c_uint32),
+        ("ndim", C.c_uint32),
+        ("shape", C.c_uint64 * 4),
+    ]
+
+
+class er_device_info(C.Structure):
+    _fields_ = [
+        ("device", C.c_int),
+        ("compute_units", C.c_int),
+        ("clock_khz", C.c_int),
+        ("memory_clock_khz", C.c_int),
+        ("memory_bus_width", C.c_int),
+        ("total_memory", C.c_uint64),
+        ("name", C.c_char * 64),
+        ("arch", C.c_char * 64),
+    ]
+
+
+_ctx_p = C.c_void_p
+_stream = C.c_void_p
+_event = C.c_void_p
+_u32 = C.c_uint32
+_u64 = C.c_uint64
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "er_hip_abi_version": (C.c_int, []),
+    "er_hip_create": (C.c_int, [C.c_int, C.POINTER(_ctx_p)]),
+    "er_hip_destroy": (None, [_ctx_p]),
+    "er_hip_get_device_info": (C.c_int, [_ctx_p, C.POINTER(er_device_info)]),
+    "er_hip_last_error": (C.c_char_p, []),
+    "er_status_string": (C.c_char_p, [C.c_int]),
+    "er_hip_alloc": (C.c_int, [_ctx_p, _u64, C.POINTER(er_buffer)]),
+    "er_hip_free": (C.c_int, [_ctx_p, er_buffer]),
+    "er_hip_upload": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, C.c_void_p, _u64]),
+    "er_hip_download": (C.c_int, [_ctx_p, _stream, C.c_void_p, er_buffer, _u64, _u64]),
+    "er_hip_stream_create": (C.c_int, [_ctx_p, C.POINTER(_stream)]),
+    "er_hip_stream_destroy": (C.c_int, [_ctx_p, _stream]),
+    "er_hip_synchronize": (C.c_int, [_ctx_p, _stream]),
+    "er_hip_event_create": (C.c_int, [_ctx_p, C.POINTER(_event)]),
+    "er_hip_event_destroy": (C.c_int, [_ctx_p, _event]),
+    "er_hip_event_record": (C.c_int, [_ctx_p, _event, _stream]),
+    "er_hip_event_elapsed_ms": (C.c_int, [_ctx_p, _event, _event, C.POINTER(C.c_float)]),
+    "er_hip_dequant_q8_0": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, er_buffer]),
+    "er_hip_dequant_q4_k": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, er_buffer]),
+    "er_hip_dequant_q6_k": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, er_buffer]),
+    "er_hip_encode_q4k_weights": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q6k_weights": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q8_0_weights": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_batched_q4k_weights": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
+    "er_hip_encode_batched_q6k_weights": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
+    "er_hip_encode_batched_q8_0_weights": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
+    "er_hip_encode_projection": (
+        C.c_int, [_ctx_p, _stream, C.POINTER(er_tensor_storage), er_buffer, er_buffer, _u32]),
+}
+
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def load() -> C.CDLL:
+    """Load libedgerunner_hip.so and bind every declared entry point."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise LibraryMissing(
+            f"{LIB_PATH} is not built; run `python -m edgerunner_amd.build` "
+            "(the HIP library is required, there is no CPU fallback)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load().er_hip_last_error()
+    return msg.decode() if msg else ""

@@ -1,0 +1,95 @@
+"""Build the gfx950 code object and the host libraries in-tree.
+
+Produces (next to this file, so they travel with the source tree):
+  libedgerunner_hip.so -- the C-ABI library (include/er_hip.h) with the gfx950
+                          code object embedded
+  liber_synth.so       -- seeded synthetic workload generator (host only)
+
+Usage: python -m edgerunner_amd.build
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = ROOT / "_build"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = str(ROCM / "bin" / "hipcc")
+
+# Device flags.  Packed-FP32 instruction selection is disabled for every
+# kernel (the hardware's packed fp32 forms are not used by this library).
+DEVICE_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-munsafe-fp-atomics",
+]
+
+LIB = PKG / "libedgerunner_hip.so"
+SYNTH = PKG / "liber_synth.so"
+CODE_OBJECT = BUILD / "er_kernels.hsaco"
+
+
+def _run(cmd: list[str]) -> None:
+    print("+", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build_code_object(extra: list[str] | None = None) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    _run([HIPCC, *DEVICE_FLAGS, *(extra or []), "--genco", "-I", str(CSRC),
+          str(CSRC / "er_kernels.hip"), "-o", str(CODE_OBJECT)])
+    return CODE_OBJECT
+
+
+def build_host_library(code_object: Path = CODE_OBJECT, out: Path = LIB) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    blob = BUILD / "er_blob.S"
+    blob.write_text(
+        "    .section .rodata\n"
+        "    .balign 4096\n"
+        "    .globl er_kernels_blob\n"
+        "er_kernels_blob:\n"
+        f"    .incbin \"{code_object}\"\n"
+        "    .globl er_kernels_blob_end\n"
+        "er_kernels_blob_end:\n"
+        "    .byte 0\n"
+        "    .section .note.GNU-stack,\"\",@progbits\n"
+    )
+    blob_o = BUILD / "er_blob.o"
+    host_o = BUILD / "er_hip.o"
+    _run(["gcc", "-c", str(blob), "-o", str(blob_o)])
+    _run(["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+          "-I", str(ROCM / "include"), "-I", str(ROOT / "include"),
+          "-c", str(CSRC / "er_hip.cpp"), "-o", str(host_o)])
+    tmp = out.with_suffix(".so.tmp")
+    _run(["g++", "-shared", "-o", str(tmp), str(host_o), str(blob_o),
+          "-L", str(ROCM / "lib"), "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
+          "-Wl,--version-script=" + str(CSRC / "er_hip.map")])
+    os.replace(tmp, out)
+    return out
+
+
+def build_synth() -> Path:
+    tmp = SYNTH.with_suffix(".so.tmp")
+    _run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-Wall", "-Wextra",
+          str(CSRC / "er_synth.c"), "-o", str(tmp), "-lm"])
+    os.replace(tmp, SYNTH)
+    return SYNTH
+
+
+def build_all() -> None:
+    build_code_object()
+    build_host_library()
+    build_synth()
+
+
+if __name__ == "__main__":
+    build_all()
+    sys.exit(0)

@@ -1,0 +1,100 @@
+// er_common.h -- device helpers shared by the gfx950 kernels.
+//
+// Raw GGUF block layouts handled here (byte offsets inside one block):
+//   Q8_0  34 B / 32 w : [0,2) d fp16, [2,34) q int8
+//   Q4_K 144 B / 256 w: [0,2) d, [2,4) dmin, [4,16) 12 packed 6-bit scales/mins,
+//                       [16,144) qs (byte 32*(j/2)+l holds sub-block j, low nibble
+//                       for even j, high nibble for odd j)
+//   Q6_K 210 B / 256 w: [0,128) ql, [128,192) qh, [192,208) int8 scales, [208,210) d
+// Q8_0 and Q6_K blocks are only 2-byte aligned inside a row, so their fields
+// are fetched with dword loads from the enclosing 4-byte-aligned window and
+// realigned with v_alignbyte_b32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// Same vectors with only dword alignment guaranteed: gfx950 global loads of
+// 2/4 dwords need 4-byte alignment only.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+#define ER_DEV static __device__ __forceinline__
+
+ER_DEV float f16_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// Byte n of a dword, widened exactly (v_cvt_f32_ubyte{0..3}).
+ER_DEV float ub0(uint32_t v) { return (float)(v & 0xffu); }
+ER_DEV float ub1(uint32_t v) { return (float)((v >> 8) & 0xffu); }
+ER_DEV float ub2(uint32_t v) { return (float)((v >> 16) & 0xffu); }
+ER_DEV float ub3(uint32_t v) { return (float)(v >> 24); }
+
+ER_DEV float sb(uint32_t v, uint32_t n) { return (float)(int8_t)((v >> (8u * n)) & 0xffu); }
+
+ER_DEV uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t sh) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+
+ER_DEV u32x4 ld16_a16(const uint8_t *p) { return *(const u32x4 *)p; }
+ER_DEV u32x4 ld16_a4(const uint8_t *p) {
+    u32x4_a4 v = *(const u32x4_a4 *)p;
+    return u32x4{v.x, v.y, v.z, v.w};
+}
+ER_DEV uint32_t ld4_a4(const uint8_t *p) { return *(const uint32_t *)p; }
+ER_DEV uint32_t ld2(const uint8_t *p) { return (uint32_t)(*(const uint16_t *)p); }
+
+// 16 bytes at a 2-byte-aligned address p inside a 4-byte-aligned buffer.
+// Reads the window [p & ~3, p + 18) when p % 4 == 2 and exactly [p, p + 16)
+// when p % 4 == 0, so callers keep p + 18 inside the buffer for the former.
+ER_DEV u32x4 ld16_a2(const uint8_t *p) {
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
+    const uint32_t *q = (const uint32_t *)((uintptr_t)p & ~(uintptr_t)3);
+    u32x4_a4 v = *(const u32x4_a4 *)q;
+    const uint32_t v4 = q[sh ? 4 : 3];
+    return u32x4{alignbyte(v.y, v.x, sh), alignbyte(v.z, v.y, sh), alignbyte(v.w, v.z, sh),
+                 alignbyte(v4, v.w, sh)};
+}
+
+// 8 bytes at a 2-byte-aligned address, same window rule as ld16_a2.
+ER_DEV u32x2 ld8_a2(const uint8_t *p) {
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
+    const uint32_t *q = (const uint32_t *)((uintptr_t)p & ~(uintptr_t)3);
+    u32x2_a4 v = *(const u32x2_a4 *)q;
+    const uint32_t v2 = q[sh ? 2 : 1];
+    return u32x2{alignbyte(v.y, v.x, sh), alignbyte(v2, v.y, sh)};
+}
+
+// 4 bytes at a 2-byte-aligned address (two 16-bit loads, never over-reads).
+ER_DEV uint32_t ld4_a2(const uint8_t *p) { return ld2(p) | (ld2(p + 2) << 16); }
+
+// Sum over the lanes of an aligned group of W lanes (W a power of two <= 64).
+template <int W>
+ER_DEV float group_sum(float v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Q4_K 6-bit scale/min unpack for the two sub-blocks j = 2p and 2p+1 that
+// share qs bytes [32p, 32p+32).  hy, hz, hw are the block's bytes [4,8),
+// [8,12), [12,16).  Returns scales in bytes 0/1 of *sc2 and mins in bytes
+// 0/1 of *m2 (sub-block 2p in byte 0).
+//   j < 4 : sc = s[j] & 63,                  m = s[j+4] & 63
+//   j >= 4: sc = (s[j+4] & 15) | (s[j-4]>>6)<<4, m = (s[j+4]>>4) | (s[j]>>6)<<4
+ER_DEV void q4k_scales_pair(uint32_t hy, uint32_t hz, uint32_t hw, uint32_t p, uint32_t *sc2,
+                            uint32_t *m2) {
+    const uint32_t sh = (p & 1u) << 4;
+    const uint32_t A = (hy >> sh) & 0xffffu;  // s[q], s[q+1]
+    const uint32_t B = (hz >> sh) & 0xffffu;  // s[q+4], s[q+5]
+    const uint32_t C = (hw >> sh) & 0xffffu;  // s[q+8], s[q+9]
+    const uint32_t scLo = A & 0x3f3fu;
+    const uint32_t mLo = B & 0x3f3fu;
+    const uint32_t scHi = (C & 0x0f0fu) | ((A >> 2) & 0x3030u);
+    const uint32_t mHi = ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u);
+    *sc2 = p < 2 ? scLo : scHi;
+    *m2 = p < 2 ? mLo : mHi;
+}

@@ -1,0 +1,409 @@
+// er_gemv.hip -- decode GEMV y[M] = W[M,K] . x[K] over raw GGUF blocks.
+//
+// Replaces q4_k_gemv_f32 (Dequant_Q4_K_M.metal:70-139), q6_k_gemv_f32
+// (Dequant_Q6_K.metal:60-127), dequant_q8_0_gemv (Dequant_Q8_0.metal:86-141)
+// and their token-batched forms (Dequant_Q4_K_M.metal:141-214,
+// Dequant_Q8_0.metal:143-197).  Bandwidth-bound: no MFMA.
+//
+// Work decomposition (all formats):
+//   * A row is cut into "slots" of 16 raw bytes of quantised weights
+//     (Q4_K: 8 slots per super-block, 32 weights each; Q6_K: 4 slots per
+//     super-block, 64 weights each; Q8_0: one slot per pair of blocks,
+//     68 bytes / 64 weights).
+//   * A wave64 is split into G = 64/LPR lane groups of LPR lanes; each group
+//     owns R consecutive rows and its lanes stride over the row's slots.
+//     The x values of a slot are read once from LDS and reused for all R rows
+//     of the group, and the raw loads for the R rows are issued back to back
+//     so each lane keeps R independent HBM requests in flight.
+//   * Partial sums are reduced across the LPR lanes with cross-lane
+//     shuffles; lane 0 of each group writes the R outputs.
+//   * The workgroup (4 waves) first stages x (K fp32) in LDS; when K*4 bytes
+//     exceeds the LDS budget (XG = true) x is read from global memory
+//     instead.
+//   * gridDim.y is the token count of the batched form: token t reads
+//     x + t*K and writes y + t*M (the reference's grid-y = token layout).
+//
+// Scale factoring: per sub-block the kernel accumulates sum(q*x) and uses the
+// precomputed sum(x) of the same 16/32 positions, i.e.
+//   Q4_K: (d*sc)*sum(q*x) - (dmin*m)*sum(x)
+//   Q6_K: (d*sc)*(sum(q6*x) - 32*sum(x))
+//   Q8_0: d*(sum((q+128)*x) - 128*sum(x))
+// which is the reference's sum of dequantised-weight * x products in a
+// different association; fp32 accumulation keeps the result within 1e-3
+// relative L2 of the CPU oracle.
+#include "er_common.h"
+
+#ifndef ER_Q4K_ROWS
+#define ER_Q4K_ROWS 4
+#endif
+#ifndef ER_Q6K_ROWS
+#define ER_Q6K_ROWS 2
+#endif
+#ifndef ER_Q8_0_ROWS
+#define ER_Q8_0_ROWS 2
+#endif
+
+#define ER_GEMV_THREADS 256
+
+// Stages x[0..K) in LDS; returns the pointer the slot loop reads x from.
+template <bool XG>
+ER_DEV const float *stage_x(const float *__restrict__ x, float *xs, uint32_t K) {
+    if (XG) return x;
+    const uint32_t K4 = K >> 2;
+    const float4 *xg = (const float4 *)x;
+    float4 *xs4 = (float4 *)xs;
+    for (uint32_t i = threadIdx.x; i < K4; i += blockDim.x) xs4[i] = xg[i];
+    __syncthreads();
+    return xs;
+}
+
+ER_DEV void ld_x16(const float *p, float v[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 f = ((const float4 *)p)[i];
+        v[4 * i + 0] = f.x;
+        v[4 * i + 1] = f.y;
+        v[4 * i + 2] = f.z;
+        v[4 * i + 3] = f.w;
+    }
+}
+
+ER_DEV float sum16(const float v[16]) {
+    float s0 = (v[0] + v[1]) + (v[2] + v[3]);
+    float s1 = (v[4] + v[5]) + (v[6] + v[7]);
+    float s2 = (v[8] + v[9]) + (v[10] + v[11]);
+    float s3 = (v[12] + v[13]) + (v[14] + v[15]);
+    return (s0 + s1) + (s2 + s3);
+}
+
+// sum over 4 packed bytes of u (as unsigned) times x[0..4)
+ER_DEV float dot4u(uint32_t u, const float *x, float acc) {
+    acc = __builtin_fmaf(ub0(u), x[0], acc);
+    acc = __builtin_fmaf(ub1(u), x[1], acc);
+    acc = __builtin_fmaf(ub2(u), x[2], acc);
+    acc = __builtin_fmaf(ub3(u), x[3], acc);
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K: slot s of a row -> super-block b = s/8, qs bytes [16i, 16i+16) with
+// i = s%8, i.e. pair p = i/2 and positions l in [16(i&1), 16(i&1)+16) of
+// sub-blocks 2p (low nibbles) and 2p+1 (high nibbles).
+// ---------------------------------------------------------------------------
+template <int LPR, int R, bool XG>
+ER_DEV void gemv_q4k(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                     float *__restrict__ y, uint32_t M, uint32_t K) {
+    extern __shared__ float xs_dyn[];
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    const float *xv = stage_x<XG>(x, xs_dyn, K);
+
+    constexpr int G = 64 / LPR;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR, li = lane % LPR;
+    const uint32_t nb = K >> 8, S = nb << 3;
+    const size_t rowBytes = (size_t)nb * 144u;
+    const uint32_t row0 =
+        ((blockIdx.x * (ER_GEMV_THREADS / 64) + wave) * G + g) * (uint32_t)R;
+
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = min(row0 + (uint32_t)r, M - 1u);
+        rowp[r] = W + (size_t)row * rowBytes;
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+    for (uint32_t s = li; s < S; s += LPR) {
+        const uint32_t b = s >> 3, i = s & 7u, p = i >> 1;
+        const uint32_t blkOff = b * 144u;
+        u32x4 hdr[R], qv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            hdr[r] = ld16_a16(rowp[r] + blkOff);
+            qv[r] = ld16_a16(rowp[r] + blkOff + 16u + (i << 4));
+        }
+        const float *xa = xv + (b << 8) + (p << 6) + ((i & 1u) << 4);
+        float xlo[16], xhi[16];
+        ld_x16(xa, xlo);
+        ld_x16(xa + 32, xhi);
+        const float sLo = sum16(xlo), sHi = sum16(xhi);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float d = f16_to_f32(hdr[r].x & 0xffffu);
+            const float dmin = f16_to_f32(hdr[r].x >> 16);
+            uint32_t sc2, m2;
+            q4k_scales_pair(hdr[r].y, hdr[r].z, hdr[r].w, p, &sc2, &m2);
+            float fLo = 0.0f, fHi = 0.0f;
+            const uint32_t qw[4] = {qv[r].x, qv[r].y, qv[r].z, qv[r].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = qw[k] & 0x0f0f0f0fu;
+                const uint32_t hi = (qw[k] >> 4) & 0x0f0f0f0fu;
+                fLo = dot4u(lo, xlo + 4 * k, fLo);
+                fHi = dot4u(hi, xhi + 4 * k, fHi);
+            }
+            float a = acc[r];
+            a = __builtin_fmaf(d * ub0(sc2), fLo, a);
+            a = __builtin_fmaf(-(dmin * ub0(m2)), sLo, a);
+            a = __builtin_fmaf(d * ub1(sc2), fHi, a);
+            a = __builtin_fmaf(-(dmin * ub1(m2)), sHi, a);
+            acc[r] = a;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K: slot s -> super-block b = s/4, half h = (s/2)&1, lane chunk
+// c = s&1 covering l in [16c, 16c+16): ql bytes [64h+16c, +16) (q1 low, q3
+// high nibbles), [64h+32+16c, +16) (q2, q4), qh bytes [128+32h+16c, +16),
+// scales sc[8h+c+{0,2,4,6}].  Blocks are 2-byte aligned: ld16_a2/ld8_a2.
+// ---------------------------------------------------------------------------
+template <int LPR, int R, bool XG>
+ER_DEV void gemv_q6k(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                     float *__restrict__ y, uint32_t M, uint32_t K) {
+    extern __shared__ float xs_dyn[];
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    const float *xv = stage_x<XG>(x, xs_dyn, K);
+
+    constexpr int G = 64 / LPR;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR, li = lane % LPR;
+    const uint32_t nb = K >> 8, S = nb << 2;
+    const size_t rowBytes = (size_t)nb * 210u;
+    const uint32_t row0 =
+        ((blockIdx.x * (ER_GEMV_THREADS / 64) + wave) * G + g) * (uint32_t)R;
+
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = min(row0 + (uint32_t)r, M - 1u);
+        rowp[r] = W + (size_t)row * rowBytes;
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+    for (uint32_t s = li; s < S; s += LPR) {
+        const uint32_t b = s >> 2, h = (s >> 1) & 1u, c = s & 1u;
+        const uint32_t blkOff = b * 210u;
+        u32x4 qa[R], qb[R], qh[R];
+        u32x2 sc[R];
+        uint32_t dbits[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = rowp[r] + blkOff;
+            qa[r] = ld16_a2(blk + 64u * h + 16u * c);
+            qb[r] = ld16_a2(blk + 64u * h + 32u + 16u * c);
+            qh[r] = ld16_a2(blk + 128u + 32u * h + 16u * c);
+            sc[r] = ld8_a2(blk + 192u + 8u * h);
+            dbits[r] = ld2(blk + 208u);
+        }
+        const float *xb = xv + (b << 8) + (h << 7) + (c << 4);
+        float x1[16], x2[16], x3[16], x4[16];
+        ld_x16(xb, x1);
+        ld_x16(xb + 32, x2);
+        ld_x16(xb + 64, x3);
+        ld_x16(xb + 96, x4);
+        const float X1 = 32.0f * sum16(x1), X2 = 32.0f * sum16(x2);
+        const float X3 = 32.0f * sum16(x3), X4 = 32.0f * sum16(x4);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t A[4] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w};
+            const uint32_t B[4] = {qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+            const uint32_t H[4] = {qh[r].x, qh[r].y, qh[r].z, qh[r].w};
+            float f1 = 0.0f, f2 = 0.0f, f3 = 0.0f, f4 = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q1 = (A[k] & 0x0f0f0f0fu) | ((H[k] << 4) & 0x30303030u);
+                const uint32_t q2 = (B[k] & 0x0f0f0f0fu) | ((H[k] << 2) & 0x30303030u);
+                const uint32_t q3 = ((A[k] >> 4) & 0x0f0f0f0fu) | (H[k] & 0x30303030u);
+                const uint32_t q4 = ((B[k] >> 4) & 0x0f0f0f0fu) | ((H[k] >> 2) & 0x30303030u);
+                f1 = dot4u(q1, x1 + 4 * k, f1);
+                f2 = dot4u(q2, x2 + 4 * k, f2);
+                f3 = dot4u(q3, x3 + 4 * k, f3);
+                f4 = dot4u(q4, x4 + 4 * k, f4);
+            }
+            const float d = f16_to_f32(dbits[r]);
+            float t = sb(sc[r].x, c) * (f1 - X1);
+            t = __builtin_fmaf(sb(sc[r].x, c + 2u), f2 - X2, t);
+            t = __builtin_fmaf(sb(sc[r].y, c), f3 - X3, t);
+            t = __builtin_fmaf(sb(sc[r].y, c + 2u), f4 - X4, t);
+            acc[r] = __builtin_fmaf(d, t, acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0, K % 64 == 0: slot s -> blocks 2s and 2s+1 = bytes [68s, 68s+68) of
+// the row, 4-byte aligned because rows are 68*(K/64) bytes.
+//   dwords v0..v16: block A d = v0[15:0], qs = bytes 2..33 (realigned by 2),
+//                   block B d = v8[31:16], qs = v9..v16.
+// ---------------------------------------------------------------------------
+template <int LPR, int R, bool XG>
+ER_DEV void gemv_q8_0(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                      float *__restrict__ y, uint32_t M, uint32_t K) {
+    extern __shared__ float xs_dyn[];
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    const float *xv = stage_x<XG>(x, xs_dyn, K);
+
+    constexpr int G = 64 / LPR;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR, li = lane % LPR;
+    const uint32_t S = K >> 6;
+    const size_t rowBytes = (size_t)S * 68u;
+    const uint32_t row0 =
+        ((blockIdx.x * (ER_GEMV_THREADS / 64) + wave) * G + g) * (uint32_t)R;
+
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = min(row0 + (uint32_t)r, M - 1u);
+        rowp[r] = W + (size_t)row * rowBytes;
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+    for (uint32_t s = li; s < S; s += LPR) {
+        uint32_t v[R][17];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *p = rowp[r] + (size_t)s * 68u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x4 t = ld16_a4(p + 16 * j);
+                v[r][4 * j + 0] = t.x;
+                v[r][4 * j + 1] = t.y;
+                v[r][4 * j + 2] = t.z;
+                v[r][4 * j + 3] = t.w;
+            }
+            v[r][16] = ld4_a4(p + 64);
+        }
+        const float *xb = xv + (s << 6);
+        float xa[32], xc[32];
+        ld_x16(xb, xa);
+        ld_x16(xb + 16, xa + 16);
+        ld_x16(xb + 32, xc);
+        ld_x16(xb + 48, xc + 16);
+        const float XA = 128.0f * (sum16(xa) + sum16(xa + 16));
+        const float XC = 128.0f * (sum16(xc) + sum16(xc + 16));
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float fa = 0.0f, fc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t qa = alignbyte(v[r][k + 1], v[r][k], 2) ^ 0x80808080u;
+                const uint32_t qc = v[r][9 + k] ^ 0x80808080u;
+                fa = dot4u(qa, xa + 4 * k, fa);
+                fc = dot4u(qc, xc + 4 * k, fc);
+            }
+            const float dA = f16_to_f32(v[r][0] & 0xffffu);
+            const float dC = f16_to_f32(v[r][8] >> 16);
+            float a = __builtin_fmaf(dA, fa - XA, acc[r]);
+            acc[r] = __builtin_fmaf(dC, fc - XC, a);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+    }
+}
+
+// Q8_0 for any K % 32 == 0 (rows only 2-byte aligned when K/32 is odd): one
+// lane group per row, one block per lane step, 16-bit loads.  Not used at the
+// BASELINE shapes; kept for the reference's full shape contract.
+template <int R>
+ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                          float *__restrict__ y, uint32_t M, uint32_t K) {
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t nb = K >> 5;
+    const size_t rowBytes = (size_t)nb * 34u;
+    const uint32_t row0 = (blockIdx.x * (ER_GEMV_THREADS / 64) + wave) * (uint32_t)R;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (uint32_t b = lane; b < nb; b += 64) {
+        const float *xb = x + (b << 5);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = min(row0 + (uint32_t)r, M - 1u);
+            const uint8_t *p = W + (size_t)row * rowBytes + (size_t)b * 34u;
+            const float d = f16_to_f32(ld2(p));
+            float f = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t q = ld4_a2(p + 2 + 4 * k);
+                f = __builtin_fmaf(sb(q, 0), xb[4 * k + 0], f);
+                f = __builtin_fmaf(sb(q, 1), xb[4 * k + 1], f);
+                f = __builtin_fmaf(sb(q, 2), xb[4 * k + 2], f);
+                f = __builtin_fmaf(sb(q, 3), xb[4 * k + 3], f);
+            }
+            acc[r] = __builtin_fmaf(d, f, acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<64>(acc[r]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Entry points (extern "C" so hipModuleGetFunction resolves them by name).
+// Naming: er_gemv_<fmt>_l<LPR>_<x source: s = LDS, g = global>.
+// ---------------------------------------------------------------------------
+#define ER_GEMV_ENTRY(fmt, impl, rows, lpr, xg, tag)                                       \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                        \
+        er_gemv_##fmt##_l##lpr##_##tag(const uint8_t *__restrict__ W,                     \
+                                         const float *__restrict__ x, float *__restrict__ y, \
+                                         uint32_t M, uint32_t K) {                        \
+        impl<lpr, rows, xg>(W, x, y, M, K);                                              \
+    }
+
+#define ER_GEMV_FAMILY(fmt, impl, rows)        \
+    ER_GEMV_ENTRY(fmt, impl, rows, 64, false, s) \
+    ER_GEMV_ENTRY(fmt, impl, rows, 32, false, s) \
+    ER_GEMV_ENTRY(fmt, impl, rows, 16, false, s) \
+    ER_GEMV_ENTRY(fmt, impl, rows, 8, false, s)  \
+    ER_GEMV_ENTRY(fmt, impl, rows, 4, false, s)  \
+    ER_GEMV_ENTRY(fmt, impl, rows, 64, true, g)  \
+    ER_GEMV_ENTRY(fmt, impl, rows, 32, true, g)  \
+    ER_GEMV_ENTRY(fmt, impl, rows, 16, true, g)  \
+    ER_GEMV_ENTRY(fmt, impl, rows, 8, true, g)   \
+    ER_GEMV_ENTRY(fmt, impl, rows, 4, true, g)
+
+ER_GEMV_FAMILY(q4k, gemv_q4k, ER_Q4K_ROWS)
+ER_GEMV_FAMILY(q6k, gemv_q6k, ER_Q6K_ROWS)
+ER_GEMV_FAMILY(q8_0, gemv_q8_0, ER_Q8_0_ROWS)
+
+extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)
+er_gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                 float *__restrict__ y, uint32_t M, uint32_t K) {
+    gemv_q8_0_any<2>(W, x, y, M, K);
+}

@@ -1,0 +1,564 @@
+// er_hip.cpp -- host side of the EdgeRunnerHIP C ABI (include/er_hip.h).
+//
+// The gfx950 code object is embedded in this library at build time
+// (er_blob.S) and loaded with hipModuleLoadData; kernels are resolved by name
+// once per context (the KernelRegistry.pipeline(for:) analogue,
+// Sources/EdgeRunnerMetal/KernelRegistry.swift:38-49) and launched with
+// hipModuleLaunchKernel on the caller's stream.  Shape validation reproduces
+// GEMVKernel.validateKQuantInputShape / encodeKQuantWeights
+// (Sources/EdgeRunnerMetal/GEMVKernel.swift:1276-1300, 1415-1432) and the
+// Dequant*Kernel.dequantise checks (Sources/EdgeRunnerIO/DequantQ4KMKernel.swift:23-29).
+#include "er_hip.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+
+extern "C" const unsigned char er_kernels_blob[];
+extern "C" const unsigned char er_kernels_blob_end[];
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+er_status fail(er_status st, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return st;
+}
+
+// Kernel table: every kernel the library launches, resolved at create time.
+#define ER_KERNEL_LIST(X)                                                              \
+    X(DEQUANT_Q8_0, "er_dequant_q8_0")                                                 \
+    X(DEQUANT_Q4_K, "er_dequant_q4_k")                                                 \
+    X(DEQUANT_Q6_K, "er_dequant_q6_k")                                                 \
+    X(GEMV_Q4K_L64_S, "er_gemv_q4k_l64_s")                                             \
+    X(GEMV_Q4K_L32_S, "er_gemv_q4k_l32_s")                                             \
+    X(GEMV_Q4K_L16_S, "er_gemv_q4k_l16_s")                                             \
+    X(GEMV_Q4K_L8_S, "er_gemv_q4k_l8_s")                                               \
+    X(GEMV_Q4K_L4_S, "er_gemv_q4k_l4_s")                                               \
+    X(GEMV_Q4K_L64_G, "er_gemv_q4k_l64_g")                                             \
+    X(GEMV_Q4K_L32_G, "er_gemv_q4k_l32_g")                                             \
+    X(GEMV_Q4K_L16_G, "er_gemv_q4k_l16_g")                                             \
+    X(GEMV_Q4K_L8_G, "er_gemv_q4k_l8_g")                                               \
+    X(GEMV_Q4K_L4_G, "er_gemv_q4k_l4_g")                                               \
+    X(GEMV_Q6K_L64_S, "er_gemv_q6k_l64_s")                                             \
+    X(GEMV_Q6K_L32_S, "er_gemv_q6k_l32_s")                                             \
+    X(GEMV_Q6K_L16_S, "er_gemv_q6k_l16_s")                                             \
+    X(GEMV_Q6K_L8_S, "er_gemv_q6k_l8_s")                                               \
+    X(GEMV_Q6K_L4_S, "er_gemv_q6k_l4_s")                                               \
+    X(GEMV_Q6K_L64_G, "er_gemv_q6k_l64_g")                                             \
+    X(GEMV_Q6K_L32_G, "er_gemv_q6k_l32_g")                                             \
+    X(GEMV_Q6K_L16_G, "er_gemv_q6k_l16_g")                                             \
+    X(GEMV_Q6K_L8_G, "er_gemv_q6k_l8_g")                                               \
+    X(GEMV_Q6K_L4_G, "er_gemv_q6k_l4_g")                                               \
+    X(GEMV_Q8_0_L64_S, "er_gemv_q8_0_l64_s")                                           \
+    X(GEMV_Q8_0_L32_S, "er_gemv_q8_0_l32_s")                                           \
+    X(GEMV_Q8_0_L16_S, "er_gemv_q8_0_l16_s")                                           \
+    X(GEMV_Q8_0_L8_S, "er_gemv_q8_0_l8_s")                                             \
+    X(GEMV_Q8_0_L4_S, "er_gemv_q8_0_l4_s")                                             \
+    X(GEMV_Q8_0_L64_G, "er_gemv_q8_0_l64_g")                                           \
+    X(GEMV_Q8_0_L32_G, "er_gemv_q8_0_l32_g")                                           \
+    X(GEMV_Q8_0_L16_G, "er_gemv_q8_0_l16_g")                                           \
+    X(GEMV_Q8_0_L8_G, "er_gemv_q8_0_l8_g")                                             \
+    X(GEMV_Q8_0_L4_G, "er_gemv_q8_0_l4_g")                                             \
+    X(GEMV_Q8_0_ANY, "er_gemv_q8_0_any")
+
+enum KernelId {
+#define ER_ENUM(id, name) K_##id,
+    ER_KERNEL_LIST(ER_ENUM)
+#undef ER_ENUM
+        K_COUNT
+};
+
+const char *const kKernelNames[K_COUNT] = {
+#define ER_NAME(id, name) name,
+    ER_KERNEL_LIST(ER_NAME)
+#undef ER_NAME
+};
+
+// Rows per lane group of each GEMV family; must match ER_*_ROWS in er_gemv.hip.
+constexpr uint32_t kQ4KRows = 4;
+constexpr uint32_t kQ6KRows = 2;
+constexpr uint32_t kQ8_0Rows = 2;
+constexpr uint32_t kGemvThreads = 256;
+constexpr uint64_t kLdsXLimit = 64u * 1024u;  // bytes of x staged in LDS
+
+}  // namespace
+
+struct er_hip_ctx {
+    int device = 0;
+    hipModule_t module = nullptr;
+    hipFunction_t fn[K_COUNT] = {};
+    int cu_count = 0;
+    er_device_info info{};
+};
+
+namespace {
+
+er_status check_ctx(const er_hip_ctx *ctx) {
+    if (!ctx) return fail(ER_ERR_INVALID_ARGUMENT, "null er_hip_ctx");
+    return ER_OK;
+}
+
+er_status bind_device(const er_hip_ctx *ctx) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess || cur != ctx->device) {
+        hipError_t e = hipSetDevice(ctx->device);
+        if (e != hipSuccess)
+            return fail(ER_ERR_DEVICE, "hipSetDevice(%d): %s", ctx->device, hipGetErrorString(e));
+    }
+    return ER_OK;
+}
+
+er_status launch(const er_hip_ctx *ctx, KernelId k, dim3 grid, dim3 block, uint32_t lds,
+                 er_stream stream, void **args) {
+    hipError_t e = hipModuleLaunchKernel(ctx->fn[k], grid.x, grid.y, grid.z, block.x, block.y,
+                                         block.z, lds, (hipStream_t)stream, args, nullptr);
+    if (e != hipSuccess)
+        return fail(ER_ERR_ENCODING_FAILED, "hipModuleLaunchKernel(%s): %s", kKernelNames[k],
+                    hipGetErrorString(e));
+    return ER_OK;
+}
+
+bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// Largest power of two in [4, 64] dividing the slot count (4 when none does).
+uint32_t lanes_per_row(uint32_t slots) {
+    uint32_t l = 64;
+    while (l > 4 && (slots % l) != 0) l >>= 1;
+    return l;
+}
+
+int lpr_index(uint32_t lpr) {
+    switch (lpr) {
+        case 64: return 0;
+        case 32: return 1;
+        case 16: return 2;
+        case 8: return 3;
+        default: return 4;
+    }
+}
+
+enum class Fmt { Q8_0, Q4_K, Q6_K };
+
+uint32_t block_bytes(Fmt f) {
+    return f == Fmt::Q8_0 ? ER_Q8_0_BLOCK_BYTES
+                          : (f == Fmt::Q4_K ? ER_Q4_K_BLOCK_BYTES : ER_Q6_K_BLOCK_BYTES);
+}
+uint32_t block_weights(Fmt f) {
+    return f == Fmt::Q8_0 ? ER_Q8_0_BLOCK_WEIGHTS : ER_K_BLOCK_WEIGHTS;
+}
+const char *fmt_name(Fmt f) {
+    return f == Fmt::Q8_0 ? "Q8_0" : (f == Fmt::Q4_K ? "Q4_K" : "Q6_K");
+}
+
+// validateKQuantInputShape (GEMVKernel.swift:1415-1432) plus the buffer-length
+// guard of encodeKQuantWeights / encodeBatchedKQuantWeights (:1296-1300, :1339-1344).
+er_status validate_gemv(Fmt f, er_buffer W, er_buffer x, er_buffer y, uint32_t batch, uint32_t M,
+                        uint32_t K) {
+    const uint32_t bw = block_weights(f);
+    if (K == 0 || K % bw != 0)
+        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s GEMV: K=%u must be a positive multiple of %u",
+                    fmt_name(f), K, bw);
+    const uint64_t expected = (uint64_t)M * (K / bw) * block_bytes(f);
+    if (W.length < expected)
+        return fail(ER_ERR_INVALID_MATRIX_SHAPE,
+                    "%s GEMV: weight buffer holds %llu bytes, M=%u K=%u needs %llu", fmt_name(f),
+                    (unsigned long long)W.length, M, K, (unsigned long long)expected);
+    if (batch == 0) return fail(ER_ERR_ENCODING_FAILED, "%s GEMV: batchSeq must be > 0", fmt_name(f));
+    if (x.length < (uint64_t)batch * K * 4u || y.length < (uint64_t)batch * M * 4u)
+        return fail(ER_ERR_ENCODING_FAILED,
+                    "%s GEMV: input %llu B / output %llu B too small for batch=%u M=%u K=%u",
+                    fmt_name(f), (unsigned long long)x.length, (unsigned long long)y.length, batch, M,
+                    K);
+    if (M == 0) return ER_OK;
+    if (!W.data || !x.data || !y.data)
+        return fail(ER_ERR_INVALID_ARGUMENT, "%s GEMV: null buffer", fmt_name(f));
+    if (!aligned(W.data, 16))
+        return fail(ER_ERR_INVALID_ARGUMENT, "%s GEMV: weight pointer must be 16-byte aligned",
+                    fmt_name(f));
+    if (!aligned(x.data, 16) || !aligned(y.data, 4))
+        return fail(ER_ERR_INVALID_ARGUMENT,
+                    "%s GEMV: input must be 16-byte and output 4-byte aligned", fmt_name(f));
+    return ER_OK;
+}
+
+er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_buffer x,
+                      er_buffer y, uint32_t batch, uint32_t M, uint32_t K) {
+    // shape validation first (it needs no device), then the context
+    er_status st = validate_gemv(f, W, x, y, batch, M, K);
+    if (st != ER_OK) return st;
+    st = check_ctx(ctx);
+    if (st != ER_OK || M == 0) return st;
+    if (batch > 65535u)
+        return fail(ER_ERR_ENCODING_FAILED, "GEMV: batchSeq %u exceeds the grid limit 65535", batch);
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+
+    const bool xg = (uint64_t)K * 4u > kLdsXLimit;
+    const uint32_t lds = xg ? 0u : K * 4u;
+    KernelId k;
+    uint32_t rows, slots;
+    if (f == Fmt::Q4_K) {
+        slots = (K / 256u) * 8u;
+        rows = kQ4KRows;
+        k = (KernelId)(K_GEMV_Q4K_L64_S + lpr_index(lanes_per_row(slots)) + (xg ? 5 : 0));
+    } else if (f == Fmt::Q6_K) {
+        slots = (K / 256u) * 4u;
+        rows = kQ6KRows;
+        k = (KernelId)(K_GEMV_Q6K_L64_S + lpr_index(lanes_per_row(slots)) + (xg ? 5 : 0));
+    } else if (K % 64u == 0) {
+        slots = K / 64u;
+        rows = kQ8_0Rows;
+        k = (KernelId)(K_GEMV_Q8_0_L64_S + lpr_index(lanes_per_row(slots)) + (xg ? 5 : 0));
+    } else {
+        // odd number of Q8_0 blocks per row: generic kernel, one row group per wave
+        uint32_t rowsPerBlock = (kGemvThreads / 64u) * 2u;
+        dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
+        void *args[] = {&W.data, &x.data, &y.data, &M, &K};
+        return launch(ctx, K_GEMV_Q8_0_ANY, grid, dim3(kGemvThreads, 1, 1), 0, stream, args);
+    }
+    const uint32_t lpr = lanes_per_row(slots);
+    const uint32_t rowsPerBlock = (kGemvThreads / 64u) * (64u / lpr) * rows;
+    dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
+    void *args[] = {&W.data, &x.data, &y.data, &M, &K};
+    return launch(ctx, k, grid, dim3(kGemvThreads, 1, 1), lds, stream, args);
+}
+
+er_status encode_dequant(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer blocks,
+                         uint64_t count, er_buffer out) {
+    const uint64_t need = count * block_bytes(f);
+    if (blocks.length < need)
+        return fail(ER_ERR_INVALID_BLOCK_DATA_COUNT,
+                    "%s dequant: expected %llu block bytes, buffer holds %llu", fmt_name(f),
+                    (unsigned long long)need, (unsigned long long)blocks.length);
+    const uint64_t outBytes = count * block_weights(f) * 4u;
+    if (out.length < outBytes)
+        return fail(ER_ERR_ALLOCATION_FAILED, "%s dequant: output needs %llu bytes, has %llu",
+                    fmt_name(f), (unsigned long long)outBytes, (unsigned long long)out.length);
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK || count == 0) return st;
+    if (!blocks.data || !out.data) return fail(ER_ERR_INVALID_ARGUMENT, "dequant: null buffer");
+    if (!aligned(blocks.data, f == Fmt::Q4_K ? 16 : 4) || !aligned(out.data, 16))
+        return fail(ER_ERR_INVALID_ARGUMENT,
+                    "dequant: blocks must be %d-byte and output 16-byte aligned",
+                    f == Fmt::Q4_K ? 16 : 4);
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    const uint64_t perBlock = f == Fmt::Q8_0 ? 8u : (f == Fmt::Q4_K ? 32u : 16u);
+    const uint64_t threads = count * perBlock;
+    const uint64_t maxBlocks = (uint64_t)ctx->cu_count * 64u;
+    uint64_t nb = (threads + 255u) / 256u;
+    if (nb > maxBlocks) nb = maxBlocks;
+    KernelId k = f == Fmt::Q8_0 ? K_DEQUANT_Q8_0 : (f == Fmt::Q4_K ? K_DEQUANT_Q4_K : K_DEQUANT_Q6_K);
+    void *args[] = {&blocks.data, &out.data, &count};
+    return launch(ctx, k, dim3((uint32_t)nb, 1, 1), dim3(256, 1, 1), 0, stream, args);
+}
+
+}  // namespace
+
+extern "C" {
+
+int er_hip_abi_version(void) { return ER_HIP_ABI_VERSION; }
+
+const char *er_hip_last_error(void) { return g_last_error; }
+
+const char *er_status_string(er_status s) {
+    switch (s) {
+        case ER_OK: return "ok";
+        case ER_ERR_LIBRARY_NOT_FOUND: return "libraryNotFound";
+        case ER_ERR_FUNCTION_NOT_FOUND: return "functionNotFound";
+        case ER_ERR_ENCODING_FAILED: return "encodingFailed";
+        case ER_ERR_INVALID_MATRIX_SHAPE: return "invalidMatrixShape";
+        case ER_ERR_INVALID_VECTOR_SHAPE: return "invalidVectorShape";
+        case ER_ERR_INVALID_BLOCK_DATA_COUNT: return "invalidBlockDataCount";
+        case ER_ERR_ALLOCATION_FAILED: return "allocationFailed";
+        case ER_ERR_INVALID_ARGUMENT: return "invalidArgument";
+        case ER_ERR_DEVICE: return "deviceError";
+    }
+    return "unknown";
+}
+
+er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
+    if (!out_ctx) return fail(ER_ERR_INVALID_ARGUMENT, "null out_ctx");
+    *out_ctx = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0)
+        return fail(ER_ERR_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+    if (device < 0 || device >= count)
+        return fail(ER_ERR_INVALID_ARGUMENT, "device %d out of range (%d devices)", device, count);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipSetDevice: %s", hipGetErrorString(e));
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess)
+        return fail(ER_ERR_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(ER_ERR_LIBRARY_NOT_FOUND, "device %d is %s; this library carries gfx950 code only",
+                    device, prop.gcnArchName);
+    er_hip_ctx *ctx = new (std::nothrow) er_hip_ctx();
+    if (!ctx) return fail(ER_ERR_ALLOCATION_FAILED, "context allocation");
+    ctx->device = device;
+    ctx->cu_count = prop.multiProcessorCount;
+    e = hipModuleLoadData(&ctx->module, er_kernels_blob);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail(ER_ERR_LIBRARY_NOT_FOUND, "hipModuleLoadData(gfx950 code object, %zu bytes): %s",
+                    (size_t)(er_kernels_blob_end - er_kernels_blob), hipGetErrorString(e));
+    }
+    for (int i = 0; i < K_COUNT; ++i) {
+        e = hipModuleGetFunction(&ctx->fn[i], ctx->module, kKernelNames[i]);
+        if (e != hipSuccess) {
+            (void)hipModuleUnload(ctx->module);
+            delete ctx;
+            return fail(ER_ERR_FUNCTION_NOT_FOUND, "functionNotFound(%s): %s", kKernelNames[i],
+                        hipGetErrorString(e));
+        }
+    }
+    er_device_info &info = ctx->info;
+    info.device = device;
+    info.compute_units = prop.multiProcessorCount;
+    info.clock_khz = prop.clockRate;
+    info.memory_clock_khz = prop.memoryClockRate;
+    info.memory_bus_width = prop.memoryBusWidth;
+    info.total_memory = prop.totalGlobalMem;
+    std::snprintf(info.name, sizeof(info.name), "%.63s", prop.name);
+    std::snprintf(info.arch, sizeof(info.arch), "%.63s", prop.gcnArchName);
+    *out_ctx = ctx;
+    return ER_OK;
+}
+
+void er_hip_destroy(er_hip_ctx *ctx) {
+    if (!ctx) return;
+    if (bind_device(ctx) == ER_OK && ctx->module) (void)hipModuleUnload(ctx->module);
+    delete ctx;
+}
+
+er_status er_hip_get_device_info(const er_hip_ctx *ctx, er_device_info *out) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!out) return fail(ER_ERR_INVALID_ARGUMENT, "null out");
+    *out = ctx->info;
+    return ER_OK;
+}
+
+er_status er_hip_alloc(er_hip_ctx *ctx, uint64_t bytes, er_buffer *out) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!out) return fail(ER_ERR_INVALID_ARGUMENT, "null out");
+    out->data = nullptr;
+    out->length = 0;
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess)
+        return fail(ER_ERR_ALLOCATION_FAILED, "allocationFailed(byteCount: %llu): %s",
+                    (unsigned long long)bytes, hipGetErrorString(e));
+    out->data = p;
+    out->length = bytes;
+    return ER_OK;
+}
+
+er_status er_hip_free(er_hip_ctx *ctx, er_buffer buf) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!buf.data) return ER_OK;
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipError_t e = hipFree(buf.data);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipFree: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_upload(er_hip_ctx *ctx, er_stream stream, er_buffer dst, uint64_t dst_offset,
+                        const void *src, uint64_t bytes) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (dst_offset > dst.length || bytes > dst.length - dst_offset)
+        return fail(ER_ERR_INVALID_ARGUMENT, "upload of %llu bytes at %llu overruns %llu-byte buffer",
+                    (unsigned long long)bytes, (unsigned long long)dst_offset,
+                    (unsigned long long)dst.length);
+    if (bytes == 0) return ER_OK;
+    if (!src || !dst.data) return fail(ER_ERR_INVALID_ARGUMENT, "upload: null pointer");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipError_t e = hipMemcpyAsync((char *)dst.data + dst_offset, src, bytes, hipMemcpyHostToDevice,
+                                  (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "upload: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_download(er_hip_ctx *ctx, er_stream stream, void *dst, er_buffer src,
+                          uint64_t src_offset, uint64_t bytes) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (src_offset > src.length || bytes > src.length - src_offset)
+        return fail(ER_ERR_INVALID_ARGUMENT,
+                    "download of %llu bytes at %llu overruns %llu-byte buffer",
+                    (unsigned long long)bytes, (unsigned long long)src_offset,
+                    (unsigned long long)src.length);
+    if (bytes == 0) return ER_OK;
+    if (!dst || !src.data) return fail(ER_ERR_INVALID_ARGUMENT, "download: null pointer");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipError_t e = hipMemcpyAsync(dst, (const char *)src.data + src_offset, bytes,
+                                  hipMemcpyDeviceToHost, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "download: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_stream_create(er_hip_ctx *ctx, er_stream *out) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!out) return fail(ER_ERR_INVALID_ARGUMENT, "null out");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipStreamCreate: %s", hipGetErrorString(e));
+    *out = (er_stream)s;
+    return ER_OK;
+}
+
+er_status er_hip_stream_destroy(er_hip_ctx *ctx, er_stream stream) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!stream) return ER_OK;
+    hipError_t e = hipStreamDestroy((hipStream_t)stream);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipStreamDestroy: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_synchronize(er_hip_ctx *ctx, er_stream stream) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipStreamSynchronize: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_event_create(er_hip_ctx *ctx, er_event *out) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!out) return fail(ER_ERR_INVALID_ARGUMENT, "null out");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreate(&ev);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipEventCreate: %s", hipGetErrorString(e));
+    *out = (er_event)ev;
+    return ER_OK;
+}
+
+er_status er_hip_event_destroy(er_hip_ctx *ctx, er_event ev) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!ev) return ER_OK;
+    hipError_t e = hipEventDestroy((hipEvent_t)ev);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipEventDestroy: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_event_record(er_hip_ctx *ctx, er_event ev, er_stream stream) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!ev) return fail(ER_ERR_INVALID_ARGUMENT, "null event");
+    hipError_t e = hipEventRecord((hipEvent_t)ev, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipEventRecord: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_event_elapsed_ms(er_hip_ctx *ctx, er_event start, er_event end, float *ms) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!start || !end || !ms) return fail(ER_ERR_INVALID_ARGUMENT, "null event/out");
+    hipError_t e = hipEventSynchronize((hipEvent_t)end);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipEventElapsedTime: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_dequant_q8_0(er_hip_ctx *ctx, er_stream stream, er_buffer blocks,
+                              uint64_t block_count, er_buffer out) {
+    return encode_dequant(ctx, stream, Fmt::Q8_0, blocks, block_count, out);
+}
+
+er_status er_hip_dequant_q4_k(er_hip_ctx *ctx, er_stream stream, er_buffer blocks,
+                              uint64_t super_block_count, er_buffer out) {
+    return encode_dequant(ctx, stream, Fmt::Q4_K, blocks, super_block_count, out);
+}
+
+er_status er_hip_dequant_q6_k(er_hip_ctx *ctx, er_stream stream, er_buffer blocks,
+                              uint64_t super_block_count, er_buffer out) {
+    return encode_dequant(ctx, stream, Fmt::Q6_K, blocks, super_block_count, out);
+}
+
+er_status er_hip_encode_q4k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                    er_buffer input, er_buffer output, uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q4_K, weight, input, output, 1, M, K);
+}
+
+er_status er_hip_encode_q6k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                    er_buffer input, er_buffer output, uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q6_K, weight, input, output, 1, M, K);
+}
+
+er_status er_hip_encode_q8_0_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                     er_buffer input, er_buffer output, uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q8_0, weight, input, output, 1, M, K);
+}
+
+er_status er_hip_encode_batched_q4k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                            er_buffer input, er_buffer output, uint32_t batch_seq,
+                                            uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q4_K, weight, input, output, batch_seq, M, K);
+}
+
+er_status er_hip_encode_batched_q6k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                            er_buffer input, er_buffer output, uint32_t batch_seq,
+                                            uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q6_K, weight, input, output, batch_seq, M, K);
+}
+
+er_status er_hip_encode_batched_q8_0_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                             er_buffer input, er_buffer output, uint32_t batch_seq,
+                                             uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q8_0, weight, input, output, batch_seq, M, K);
+}
+
+er_status er_hip_encode_projection(er_hip_ctx *ctx, er_stream stream,
+                                   const er_tensor_storage *tensor, er_buffer input,
+                                   er_buffer output, uint32_t tokens) {
+    if (!tensor) return fail(ER_ERR_INVALID_ARGUMENT, "null tensor");
+    if (tensor->ndim != 2 || tensor->shape[0] > 0xffffffffu || tensor->shape[1] > 0xffffffffu)
+        return fail(ER_ERR_INVALID_MATRIX_SHAPE, "projection tensor must be 2-D [K, M]");
+    if (tensor->byte_offset > tensor->buffer.length)
+        return fail(ER_ERR_INVALID_MATRIX_SHAPE, "byteOffset beyond the tensor buffer");
+    er_buffer W{(char *)tensor->buffer.data + tensor->byte_offset,
+                tensor->buffer.length - tensor->byte_offset};
+    const uint32_t K = (uint32_t)tensor->shape[0], M = (uint32_t)tensor->shape[1];
+    switch (tensor->data_type) {
+        case ER_TYPE_Q8_0: return encode_gemv(ctx, stream, Fmt::Q8_0, W, input, output, tokens, M, K);
+        case ER_TYPE_Q4_K: return encode_gemv(ctx, stream, Fmt::Q4_K, W, input, output, tokens, M, K);
+        case ER_TYPE_Q6_K: return encode_gemv(ctx, stream, Fmt::Q6_K, W, input, output, tokens, M, K);
+        default:
+            return fail(ER_ERR_INVALID_ARGUMENT,
+                        "projection data type %u is not supported by the quantized GEMV path",
+                        tensor->data_type);
+    }
+}
+
+}  // extern "C"

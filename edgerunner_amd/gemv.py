@@ -1,0 +1,203 @@
+"""GEMVKernel / Dequant*Kernel: the reference's Swift dispatch protocol on HIP.
+
+Method names and argument meaning follow
+Sources/EdgeRunnerMetal/GEMVKernel.swift (encode* append to the caller's
+stream and never allocate; execute* allocate, run, wait and copy out) and
+Sources/EdgeRunnerIO/Dequant{Q8_0,Q4KM,Q6K}Kernel.swift (dequantise).
+Validation errors are raised as the same Swift error cases.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+
+from . import _ffi
+from .runtime import (Buffer, Context, InvalidBlockDataCount, InvalidVectorShape, Stream, check,
+                      default_context)
+
+Q8_0_BLOCK_BYTES = 34
+Q4_K_BLOCK_BYTES = 144
+Q6_K_BLOCK_BYTES = 210
+
+TYPE_Q8_0 = 8
+TYPE_Q4_K = 12
+TYPE_Q6_K = 14
+
+
+def _sh(stream: Optional[Stream]):
+    return stream.handle if stream is not None else None
+
+
+def _u8(raw) -> np.ndarray:
+    if isinstance(raw, (bytes, bytearray, memoryview)):
+        return np.frombuffer(raw, dtype=np.uint8)
+    return np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+
+
+class GEMVKernel:
+    """Quantized GEMV dispatch (GEMVKernel.swift:6-1433, K-quant + Q8_0 part)."""
+
+    def __init__(self, ctx: Optional[Context] = None):
+        self.ctx = ctx or default_context()
+        self.lib = self.ctx.lib
+
+    # ---------------------------------------------------------------- encode
+    def encodeQ4KWeights(self, stream: Optional[Stream], weightBuffer: Buffer, inputBuffer: Buffer,
+                         outputBuffer: Buffer, M: int, K: int) -> None:
+        check(self.lib.er_hip_encode_q4k_weights(self.ctx.handle, _sh(stream), weightBuffer.raw,
+                                                 inputBuffer.raw, outputBuffer.raw, M, K))
+
+    def encodeQ6KWeights(self, stream: Optional[Stream], weightBuffer: Buffer, inputBuffer: Buffer,
+                         outputBuffer: Buffer, M: int, K: int) -> None:
+        check(self.lib.er_hip_encode_q6k_weights(self.ctx.handle, _sh(stream), weightBuffer.raw,
+                                                 inputBuffer.raw, outputBuffer.raw, M, K))
+
+    def encodeQ8_0Weights(self, stream: Optional[Stream], weightBuffer: Buffer,
+                          inputBuffer: Buffer, outputBuffer: Buffer, M: int, K: int) -> None:
+        check(self.lib.er_hip_encode_q8_0_weights(self.ctx.handle, _sh(stream), weightBuffer.raw,
+                                                  inputBuffer.raw, outputBuffer.raw, M, K))
+
+    def encodeBatchedQ4KWeights(self, stream: Optional[Stream], weightBuffer: Buffer,
+                                inputBuffer: Buffer, outputBuffer: Buffer, batchSeq: int, M: int,
+                                K: int) -> None:
+        check(self.lib.er_hip_encode_batched_q4k_weights(
+            self.ctx.handle, _sh(stream), weightBuffer.raw, inputBuffer.raw, outputBuffer.raw,
+            batchSeq, M, K))
+
+    def encodeBatchedQ6KWeights(self, stream: Optional[Stream], weightBuffer: Buffer,
+                                inputBuffer: Buffer, outputBuffer: Buffer, batchSeq: int, M: int,
+                                K: int) -> None:
+        check(self.lib.er_hip_encode_batched_q6k_weights(
+            self.ctx.handle, _sh(stream), weightBuffer.raw, inputBuffer.raw, outputBuffer.raw,
+            batchSeq, M, K))
+
+    def encodeBatchedQ8_0Weights(self, stream: Optional[Stream], weightBuffer: Buffer,
+                                 inputBuffer: Buffer, outputBuffer: Buffer, batchSeq: int, M: int,
+                                 K: int) -> None:
+        check(self.lib.er_hip_encode_batched_q8_0_weights(
+            self.ctx.handle, _sh(stream), weightBuffer.raw, inputBuffer.raw, outputBuffer.raw,
+            batchSeq, M, K))
+
+    def encodeProjection(self, stream: Optional[Stream], weightBuffer: Buffer, dataType: int,
+                         inputBuffer: Buffer, outputBuffer: Buffer, M: int, K: int,
+                         tokens: int = 1, byteOffset: int = 0) -> None:
+        """Gemma4LanguageModel.encodeProjection (Gemma4LanguageModel.swift:4207-4285)."""
+        t = _ffi.er_tensor_storage()
+        t.buffer = weightBuffer.raw
+        t.byte_offset = byteOffset
+        t.data_type = dataType
+        t.ndim = 2
+        t.shape[0] = K
+        t.shape[1] = M
+        import ctypes as C
+        check(self.lib.er_hip_encode_projection(self.ctx.handle, _sh(stream), C.byref(t),
+                                                inputBuffer.raw, outputBuffer.raw, tokens))
+
+    # ---------------------------------------------------------------- execute
+    def _execute(self, encode, block_bytes: int, rawWeights, x, M: int, K: int,
+                 batchSeq: Optional[int] = None) -> np.ndarray:
+        w = _u8(rawWeights)
+        xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        per = 32 if block_bytes == Q8_0_BLOCK_BYTES else 256
+        tokens = 1 if batchSeq is None else batchSeq
+        # validateKQuantInputShape(vectorCount: x.count) (GEMVKernel.swift:1415-1432)
+        if batchSeq is None and xv.size != K:
+            raise InvalidVectorShape(f"x.count {xv.size} != K {K}")
+        if batchSeq is not None and (batchSeq <= 0 or xv.size != batchSeq * K):
+            raise InvalidVectorShape(f"x.count {xv.size} != batchSeq*K {tokens * K}")
+        if K <= 0 or K % per != 0:
+            raise InvalidVectorShape(f"K={K} must be a positive multiple of {per}")
+        ctx = self.ctx
+        wb = ctx.upload(w) if w.size else ctx.alloc(0)
+        xb = ctx.upload(xv)
+        yb = ctx.alloc(tokens * M * 4)
+        try:
+            if batchSeq is None:
+                encode(None, wb, xb, yb, M, K)
+            else:
+                encode(None, wb, xb, yb, batchSeq, M, K)
+            ctx.synchronize()
+            return yb.download(np.float32, tokens * M)
+        finally:
+            wb.free()
+            xb.free()
+            yb.free()
+
+    def executeQ4KWeights(self, rawWeights, x, M: int, K: int) -> np.ndarray:
+        return self._execute(self.encodeQ4KWeights, Q4_K_BLOCK_BYTES, rawWeights, x, M, K)
+
+    def executeQ6KWeights(self, rawWeights, x, M: int, K: int) -> np.ndarray:
+        return self._execute(self.encodeQ6KWeights, Q6_K_BLOCK_BYTES, rawWeights, x, M, K)
+
+    def executeQ8_0Weights(self, rawWeights, x, M: int, K: int) -> np.ndarray:
+        return self._execute(self.encodeQ8_0Weights, Q8_0_BLOCK_BYTES, rawWeights, x, M, K)
+
+    def executeBatchedQ4KWeights(self, rawWeights, x, batchSeq: int, M: int, K: int) -> np.ndarray:
+        return self._execute(self.encodeBatchedQ4KWeights, Q4_K_BLOCK_BYTES, rawWeights, x, M, K,
+                             batchSeq)
+
+    def executeBatchedQ6KWeights(self, rawWeights, x, batchSeq: int, M: int, K: int) -> np.ndarray:
+        return self._execute(self.encodeBatchedQ6KWeights, Q6_K_BLOCK_BYTES, rawWeights, x, M, K,
+                             batchSeq)
+
+    def executeBatchedQ8_0Weights(self, rawWeights, x, batchSeq: int, M: int,
+                                  K: int) -> np.ndarray:
+        return self._execute(self.encodeBatchedQ8_0Weights, Q8_0_BLOCK_BYTES, rawWeights, x, M, K,
+                             batchSeq)
+
+
+class _DequantKernel:
+    block_bytes = 0
+    weights_per_block = 0
+    entry = ""
+
+    def __init__(self, ctx: Optional[Context] = None):
+        self.ctx = ctx or default_context()
+
+    def encode(self, stream: Optional[Stream], blocks: Buffer, count: int, out: Buffer) -> None:
+        check(getattr(self.ctx.lib, self.entry)(self.ctx.handle, _sh(stream), blocks.raw, count,
+                                                out.raw))
+
+    def dequantise(self, blockData, count: int) -> np.ndarray:
+        """dequantise(blockData:blockCount:) -- exact byte count required
+        (DequantQ8_0Kernel.swift:23-29)."""
+        data = _u8(blockData)
+        expected = count * self.block_bytes
+        if data.size != expected:
+            raise InvalidBlockDataCount(
+                f"invalidBlockDataCount(expected: {expected}, actual: {data.size})",
+                expected=expected, actual=int(data.size))
+        ctx = self.ctx
+        if count == 0:
+            return np.zeros(0, dtype=np.float32)
+        ib = ctx.upload(data)
+        ob = ctx.alloc(count * self.weights_per_block * 4)
+        try:
+            self.encode(None, ib, count, ob)
+            ctx.synchronize()
+            return ob.download(np.float32, count * self.weights_per_block)
+        finally:
+            ib.free()
+            ob.free()
+
+
+class DequantQ8_0Kernel(_DequantKernel):
+    """Sources/EdgeRunnerIO/DequantQ8_0Kernel.swift:18-78."""
+    block_bytes = Q8_0_BLOCK_BYTES
+    weights_per_block = 32
+    entry = "er_hip_dequant_q8_0"
+
+
+class DequantQ4KMKernel(_DequantKernel):
+    """Sources/EdgeRunnerIO/DequantQ4KMKernel.swift:18-78."""
+    block_bytes = Q4_K_BLOCK_BYTES
+    weights_per_block = 256
+    entry = "er_hip_dequant_q4_k"
+
+
+class DequantQ6KKernel(_DequantKernel):
+    """Sources/EdgeRunnerIO/DequantQ6KKernel.swift:18-78."""
+    block_bytes = Q6_K_BLOCK_BYTES
+    weights_per_block = 256
+    entry = "er_hip_dequant_q6_k"

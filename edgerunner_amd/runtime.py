@@ -1,0 +1,242 @@
+"""Python host layer over the EdgeRunnerHIP C ABI.
+
+Mirrors the Swift host objects the Metal path is driven by:
+  - ``Context``     : the device + loaded code object (MetalBackend/KernelRegistry)
+  - ``Buffer``      : device memory with a length (MTLBuffer)
+  - ``Stream``      : the ordered work queue encodes go to (MTLCommandBuffer)
+  - ``Event``       : GPU timestamps (commandBuffer.gpuStartTime/gpuEndTime)
+  - ``GEMVError`` / ``DequantKernelError`` : the reference's Swift error enums
+    (Sources/EdgeRunnerMetal/GEMVKernel.swift:1435-1441,
+     Sources/EdgeRunnerIO/DequantKernel.swift:19-25).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import numpy as np
+
+from . import _ffi
+
+
+# --------------------------------------------------------------------------- errors
+class EdgeRunnerHIPError(Exception):
+    status = -1
+
+    def __init__(self, message: str = ""):
+        super().__init__(message)
+        self.message = message
+
+
+class GEMVError(EdgeRunnerHIPError):
+    """GEMVError (GEMVKernel.swift:1435-1441)."""
+
+
+class LibraryNotFound(GEMVError):
+    status = 1
+
+
+class FunctionNotFound(GEMVError):
+    status = 2
+
+
+class EncodingFailed(GEMVError):
+    status = 3
+
+
+class InvalidMatrixShape(GEMVError):
+    status = 4
+
+
+class InvalidVectorShape(GEMVError):
+    status = 5
+
+
+class DequantKernelError(EdgeRunnerHIPError):
+    """DequantKernelError (DequantKernel.swift:19-25)."""
+
+
+class InvalidBlockDataCount(DequantKernelError):
+    status = 6
+
+    def __init__(self, message: str = "", expected: Optional[int] = None,
+                 actual: Optional[int] = None):
+        super().__init__(message)
+        self.expected = expected
+        self.actual = actual
+
+
+class AllocationFailed(DequantKernelError):
+    status = 7
+
+
+class InvalidArgument(EdgeRunnerHIPError):
+    status = 8
+
+
+class DeviceError(EdgeRunnerHIPError):
+    status = 9
+
+
+_BY_STATUS = {cls.status: cls for cls in (
+    LibraryNotFound, FunctionNotFound, EncodingFailed, InvalidMatrixShape, InvalidVectorShape,
+    InvalidBlockDataCount, AllocationFailed, InvalidArgument, DeviceError)}
+
+
+def check(status: int) -> None:
+    if status == _ffi.ER_OK:
+        return
+    cls = _BY_STATUS.get(status, EdgeRunnerHIPError)
+    raise cls(f"{_ffi.STATUS_NAMES.get(status, status)}: {_ffi.last_error()}")
+
+
+# --------------------------------------------------------------------------- objects
+class Buffer:
+    """Device memory plus its byte length (the MTLBuffer analogue)."""
+
+    def __init__(self, ctx: "Context", raw: _ffi.er_buffer, owned: bool = True):
+        self.ctx = ctx
+        self.raw = raw
+        self.owned = owned
+
+    @property
+    def length(self) -> int:
+        return int(self.raw.length)
+
+    @property
+    def ptr(self) -> int:
+        return int(self.raw.data or 0)
+
+    def view(self, offset: int = 0, length: Optional[int] = None) -> "Buffer":
+        """A non-owning sub-range (for byteOffset-style tensor views)."""
+        if length is None:
+            length = self.length - offset
+        if offset < 0 or length < 0 or offset + length > self.length:
+            raise InvalidArgument("view out of range")
+        return Buffer(self.ctx, _ffi.er_buffer(self.ptr + offset, length), owned=False)
+
+    def upload(self, host: np.ndarray, offset: int = 0, stream: "Optional[Stream]" = None) -> None:
+        a = np.ascontiguousarray(host)
+        check(self.ctx.lib.er_hip_upload(self.ctx.handle, _sh(stream), self.raw, offset,
+                                         a.ctypes.data_as(C.c_void_p), a.nbytes))
+
+    def download(self, dtype, count: Optional[int] = None, offset: int = 0,
+                 stream: "Optional[Stream]" = None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.length - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        check(self.ctx.lib.er_hip_download(self.ctx.handle, _sh(stream),
+                                           out.ctypes.data_as(C.c_void_p), self.raw, offset,
+                                           out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.owned and self.raw.data:
+            check(self.ctx.lib.er_hip_free(self.ctx.handle, self.raw))
+        self.raw = _ffi.er_buffer(None, 0)
+
+    def __del__(self):
+        try:
+            if self.owned and self.raw.data and self.ctx.handle:
+                self.ctx.lib.er_hip_free(self.ctx.handle, self.raw)
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self, ctx: "Context"):
+        self.ctx = ctx
+        h = C.c_void_p()
+        check(ctx.lib.er_hip_stream_create(ctx.handle, C.byref(h)))
+        self.handle = h
+
+    def synchronize(self) -> None:
+        check(self.ctx.lib.er_hip_synchronize(self.ctx.handle, self.handle))
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(self.ctx.lib.er_hip_stream_destroy(self.ctx.handle, self.handle))
+            self.handle = C.c_void_p()
+
+
+class Event:
+    def __init__(self, ctx: "Context"):
+        self.ctx = ctx
+        h = C.c_void_p()
+        check(ctx.lib.er_hip_event_create(ctx.handle, C.byref(h)))
+        self.handle = h
+
+    def record(self, stream: "Optional[Stream]" = None) -> None:
+        check(self.ctx.lib.er_hip_event_record(self.ctx.handle, self.handle, _sh(stream)))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        check(self.ctx.lib.er_hip_event_elapsed_ms(self.ctx.handle, self.handle, end.handle,
+                                                   C.byref(ms)))
+        return float(ms.value)
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(self.ctx.lib.er_hip_event_destroy(self.ctx.handle, self.handle))
+            self.handle = C.c_void_p()
+
+
+def _sh(stream: Optional[Stream]):
+    return stream.handle if stream is not None else None
+
+
+class Context:
+    """One GPU with the gfx950 code object loaded and every kernel resolved."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _ffi.load()
+        h = C.c_void_p()
+        check(self.lib.er_hip_create(device, C.byref(h)))
+        self.handle = h
+        info = _ffi.er_device_info()
+        check(self.lib.er_hip_get_device_info(self.handle, C.byref(info)))
+        self.info = info
+
+    @property
+    def compute_units(self) -> int:
+        return int(self.info.compute_units)
+
+    @property
+    def arch(self) -> str:
+        return self.info.arch.decode()
+
+    def alloc(self, nbytes: int) -> Buffer:
+        raw = _ffi.er_buffer()
+        check(self.lib.er_hip_alloc(self.handle, nbytes, C.byref(raw)))
+        return Buffer(self, raw)
+
+    def upload(self, host: np.ndarray, stream: Optional[Stream] = None) -> Buffer:
+        a = np.ascontiguousarray(host)
+        buf = self.alloc(a.nbytes)
+        buf.upload(a, stream=stream)
+        return buf
+
+    def stream(self) -> Stream:
+        return Stream(self)
+
+    def event(self) -> Event:
+        return Event(self)
+
+    def synchronize(self, stream: Optional[Stream] = None) -> None:
+        check(self.lib.er_hip_synchronize(self.handle, _sh(stream)))
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.er_hip_destroy(self.handle)
+            self.handle = C.c_void_p()
+
+
+_default: Optional[Context] = None
+
+
+def default_context() -> Context:
+    global _default
+    if _default is None:
+        _default = Context(0)
+    return _default

@@ -1,0 +1,194 @@
+/*
+ * er_hip.h -- C ABI of EdgeRunnerHIP: the MI355X (gfx950) quantized-matmul
+ * backend for EdgeRunner's GGUF Q8_0 / Q4_K / Q6_K weights.
+ *
+ * The entry points replace the Metal kernel path behind
+ * EdgeRunnerMetal.GEMVKernel (Sources/EdgeRunnerMetal/GEMVKernel.swift),
+ * the Q8_0 pipelines fetched by name from KernelRegistry
+ * (Sources/EdgeRunnerMetal/KernelRegistry.swift:38-49, used at
+ * Sources/EdgeRunner/Models/LlamaLanguageModel.swift:260-275, 2519-2535) and
+ * the Dequant*Kernel.dequantise wrappers (Sources/EdgeRunnerIO/Dequant*.swift).
+ * Paths are relative to the EdgeRunner source tree.
+ *
+ * Conventions (mirroring the Metal protocol):
+ *   - Weights are the raw GGUF blocks, row-major, each row made of K/32 (Q8_0)
+ *     or K/256 (Q4_K, Q6_K) contiguous blocks; GGUF shape [K, M].
+ *   - "encode" calls only enqueue work on the caller's stream (the
+ *     MTLCommandBuffer analogue) and never allocate; ordering is the stream's.
+ *   - A buffer is device memory plus its byte length (the MTLBuffer analogue),
+ *     so the reference's buffer-length validation is reproduced exactly.
+ *   - Every call returns an er_status; er_hip_last_error() gives the message of
+ *     the calling thread's last failure.
+ *   - A context is immutable after er_hip_create; calls on distinct streams may
+ *     run concurrently from several threads.
+ */
+#ifndef ER_HIP_H
+#define ER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ER_HIP_ABI_VERSION 1
+
+/* Status codes.  Each maps 1:1 onto a Swift error case of the reference:
+ * GEMVError (GEMVKernel.swift:1435-1441) and DequantKernelError
+ * (Sources/EdgeRunnerIO/DequantKernel.swift:19-25). */
+typedef enum er_status {
+    ER_OK = 0,
+    ER_ERR_LIBRARY_NOT_FOUND = 1,        /* GEMVError.libraryNotFound: code object missing/unloadable */
+    ER_ERR_FUNCTION_NOT_FOUND = 2,       /* GEMVError.functionNotFound(name) */
+    ER_ERR_ENCODING_FAILED = 3,          /* GEMVError.encodingFailed / DequantKernelError.encodingFailed */
+    ER_ERR_INVALID_MATRIX_SHAPE = 4,     /* GEMVError.invalidMatrixShape */
+    ER_ERR_INVALID_VECTOR_SHAPE = 5,     /* GEMVError.invalidVectorShape */
+    ER_ERR_INVALID_BLOCK_DATA_COUNT = 6, /* DequantKernelError.invalidBlockDataCount(expected:actual:) */
+    ER_ERR_ALLOCATION_FAILED = 7,        /* DequantKernelError.allocationFailed(byteCount:) */
+    ER_ERR_INVALID_ARGUMENT = 8,         /* null context/pointer, misaligned device pointer */
+    ER_ERR_DEVICE = 9                    /* HIP runtime error (commandBuffer.error analogue) */
+} er_status;
+
+/* TensorDataType raw values (Sources/EdgeRunnerIO/WeightMap.swift:69-91). */
+typedef enum er_tensor_type {
+    ER_TYPE_F32 = 0,
+    ER_TYPE_F16 = 1,
+    ER_TYPE_Q8_0 = 8,
+    ER_TYPE_Q4_K = 12,
+    ER_TYPE_Q6_K = 14,
+    ER_TYPE_BF16 = 30
+} er_tensor_type;
+
+/* Block geometry (GGUFLoader.tensorByteCount, Sources/EdgeRunnerIO/GGUF/GGUFLoader.swift:125-179). */
+#define ER_Q8_0_BLOCK_BYTES 34
+#define ER_Q8_0_BLOCK_WEIGHTS 32
+#define ER_Q4_K_BLOCK_BYTES 144
+#define ER_Q6_K_BLOCK_BYTES 210
+#define ER_K_BLOCK_WEIGHTS 256
+
+/* Device memory plus its byte length: the MTLBuffer analogue.  The weight
+ * buffer's data pointer must be 16-byte aligned (GGUF tensor data is 32-byte
+ * aligned); activations and outputs must be 4-byte aligned. */
+typedef struct er_buffer {
+    void *data;
+    uint64_t length;
+} er_buffer;
+
+/* TensorStorage (WeightMap.swift:93-127): buffer + byteOffset + dataType +
+ * GGUF shape [K, M] (shape[0] = K = columns, shape[1] = M = rows). */
+typedef struct er_tensor_storage {
+    er_buffer buffer;
+    uint64_t byte_offset;
+    uint32_t data_type; /* er_tensor_type */
+    uint32_t ndim;
+    uint64_t shape[4];
+} er_tensor_storage;
+
+typedef struct er_hip_ctx er_hip_ctx;
+typedef void *er_stream; /* hipStream_t; NULL = the device's null stream */
+typedef void *er_event;  /* hipEvent_t */
+
+typedef struct er_device_info {
+    int device;
+    int compute_units;
+    int clock_khz;
+    int memory_clock_khz;
+    int memory_bus_width;
+    uint64_t total_memory;
+    char name[64];
+    char arch[64];
+} er_device_info;
+
+/* ---- lifecycle (GEMVKernel.init: pipelines resolved once, GEMVKernel.swift:54-76) ---- */
+
+/* Loads the embedded gfx950 code object on `device` (hipModuleLoadData) and
+ * resolves every kernel by name (the KernelRegistry analogue). */
+er_status er_hip_create(int device, er_hip_ctx **out_ctx);
+void er_hip_destroy(er_hip_ctx *ctx);
+er_status er_hip_get_device_info(const er_hip_ctx *ctx, er_device_info *out);
+const char *er_hip_last_error(void);
+const char *er_status_string(er_status status);
+int er_hip_abi_version(void);
+
+/* ---- memory: no unified memory on MI355X, so the mmap'd GGUF bytes are
+ * uploaded once (replaces MTLBuffer(bytesNoCopy:), MemoryMappedFile.swift:142-196) ---- */
+er_status er_hip_alloc(er_hip_ctx *ctx, uint64_t bytes, er_buffer *out);
+er_status er_hip_free(er_hip_ctx *ctx, er_buffer buf);
+er_status er_hip_upload(er_hip_ctx *ctx, er_stream stream, er_buffer dst, uint64_t dst_offset,
+                        const void *src, uint64_t bytes);
+er_status er_hip_download(er_hip_ctx *ctx, er_stream stream, void *dst, er_buffer src,
+                          uint64_t src_offset, uint64_t bytes);
+
+/* ---- streams and events (command buffer commit / completed; GPU timing as in
+ * Gemma4LanguageModel.RuntimeProfiler, Gemma4LanguageModel.swift:135-200) ---- */
+er_status er_hip_stream_create(er_hip_ctx *ctx, er_stream *out);
+er_status er_hip_stream_destroy(er_hip_ctx *ctx, er_stream stream);
+er_status er_hip_synchronize(er_hip_ctx *ctx, er_stream stream);
+er_status er_hip_event_create(er_hip_ctx *ctx, er_event *out);
+er_status er_hip_event_destroy(er_hip_ctx *ctx, er_event ev);
+er_status er_hip_event_record(er_hip_ctx *ctx, er_event ev, er_stream stream);
+er_status er_hip_event_elapsed_ms(er_hip_ctx *ctx, er_event start, er_event end, float *ms);
+
+/* ---- dequantisation to fp32 ----
+ * Replace DequantQ8_0Kernel.dequantise (Sources/EdgeRunnerIO/DequantQ8_0Kernel.swift:18-78),
+ * DequantQ4KMKernel.dequantise (DequantQ4KMKernel.swift:18-78) and
+ * DequantQ6KKernel.dequantise (DequantQ6KKernel.swift:18-78).
+ * blocks.length must be >= count * block bytes (INVALID_BLOCK_DATA_COUNT) and
+ * out.length >= count * weights per block * 4 (ALLOCATION_FAILED).  Results
+ * are bit-identical to the reference's CPU dequantisers. */
+er_status er_hip_dequant_q8_0(er_hip_ctx *ctx, er_stream stream, er_buffer blocks,
+                              uint64_t block_count, er_buffer out);
+er_status er_hip_dequant_q4_k(er_hip_ctx *ctx, er_stream stream, er_buffer blocks,
+                              uint64_t super_block_count, er_buffer out);
+er_status er_hip_dequant_q6_k(er_hip_ctx *ctx, er_stream stream, er_buffer blocks,
+                              uint64_t super_block_count, er_buffer out);
+
+/* ---- decode GEMV: y[M] = W[M,K] . x[K], fp32 in / fp32 out ----
+ * Validation as GEMVKernel.validateKQuantInputShape + encodeKQuantWeights
+ * (GEMVKernel.swift:1415-1432, 1276-1300): K > 0 and K % 256 == 0 else
+ * INVALID_VECTOR_SHAPE; weight.length >= M*(K/256)*blockBytes else
+ * INVALID_MATRIX_SHAPE; input.length >= K*4 and output.length >= M*4 else
+ * ENCODING_FAILED. */
+
+/* GEMVKernel.encodeQ4KWeights (GEMVKernel.swift:704-722; kernel q4_k_gemv_f32). */
+er_status er_hip_encode_q4k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                    er_buffer input, er_buffer output, uint32_t M, uint32_t K);
+/* GEMVKernel.encodeQ6KWeights (GEMVKernel.swift:1164-1182; kernel q6_k_gemv_f32). */
+er_status er_hip_encode_q6k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                    er_buffer input, er_buffer output, uint32_t M, uint32_t K);
+/* Q8_0 GEMV: pipeline "dequant_q8_0_gemv" with ERDequantGEMVParams{rows, cols,
+ * blocksPerRow} (Dequant_Q8_0.metal:86-141, DequantParams.h:11-15).  The
+ * reference encodes it by hand without validation; here K > 0 and K % 32 == 0
+ * (INVALID_VECTOR_SHAPE) and weight.length >= M*(K/32)*34 (INVALID_MATRIX_SHAPE). */
+er_status er_hip_encode_q8_0_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                     er_buffer input, er_buffer output, uint32_t M, uint32_t K);
+
+/* ---- batched (token-axis) GEMV: y[t*M + r] = W[r,:] . x[t*K : (t+1)*K] ----
+ * GEMVKernel.encodeBatchedQ4KWeights (GEMVKernel.swift:682-702, validation
+ * :1319-1361: batchSeq > 0, input >= batchSeq*K*4, output >= batchSeq*M*4 else
+ * ENCODING_FAILED) and dequant_q8_0_gemv_batched (Dequant_Q8_0.metal:143-197).
+ * The Q6_K variant has no reference counterpart but follows the same contract. */
+er_status er_hip_encode_batched_q4k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                            er_buffer input, er_buffer output, uint32_t batch_seq,
+                                            uint32_t M, uint32_t K);
+er_status er_hip_encode_batched_q6k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                            er_buffer input, er_buffer output, uint32_t batch_seq,
+                                            uint32_t M, uint32_t K);
+er_status er_hip_encode_batched_q8_0_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                             er_buffer input, er_buffer output, uint32_t batch_seq,
+                                             uint32_t M, uint32_t K);
+
+/* ---- projection by tensor descriptor (Gemma4LanguageModel.encodeProjection,
+ * Sources/EdgeRunner/Models/Gemma4LanguageModel.swift:4207-4285): dispatches on
+ * tensor->data_type (Q8_0, Q4_K, Q6_K); shape = [K, M]; tokens >= 1 selects the
+ * batched form.  Other data types return INVALID_ARGUMENT. ---- */
+er_status er_hip_encode_projection(er_hip_ctx *ctx, er_stream stream,
+                                   const er_tensor_storage *tensor, er_buffer input,
+                                   er_buffer output, uint32_t tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ER_HIP_H */
