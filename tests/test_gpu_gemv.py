@@ -137,7 +137,8 @@ def test_one_hot_returns_dequantised_column_exactly(gemv, fmt):
         x = np.zeros(K, np.float32)
         x[j] = 1.0
         y = run(gemv, fmt, W, x, M, K)
-        assert np.array_equal(y.view(np.uint32), cols[:, j].view(np.uint32)), j
+        # value equality: a -0.0 weight times 1 summed onto +0.0 gives +0.0
+        assert np.array_equal(y, cols[:, j]), j
 
 
 @pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k"])
