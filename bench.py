@@ -6,8 +6,9 @@ Headline (BASELINE.json `metric`, configs[1]): Q4_K decode GEMV at
 (W + x + y, the reference's formula, GEMVTests.swift:1438-1440) / average
 launch duration.  One step = one GEMV call over one of >= 768 MB of distinct
 weight copies (rotated so every call misses the 256 MB Infinity Cache), with
-x and y resident in HBM.  Timing uses HIP events on the launch stream around
-exactly `--steps` launches after `--warmup` untimed ones.
+x and y resident in HBM.  The `--steps` launches are recorded into a HIP graph
+and replayed; HIP events on the launch stream bracket the replay (after
+`--warmup` untimed launches and one untimed replay).
 
 Also reported in `results`: the other BASELINE GEMV shapes (Q8_0 3072x1024 and
 14336x4096, Q4_K 4096x14336, Q6_K 151936x1024 and 128256x4096).
@@ -65,8 +66,12 @@ def algorithmic_bytes(fmt: str, M: int, K: int) -> int:
 
 
 def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
+    """Times `steps` GEMV launches over rotating weight copies.  The launches
+    are recorded once into a HIP graph and replayed, so the events bracket
+    GPU work only (no Python launch overhead); the eager, Python-launched
+    rate is reported alongside."""
     import edgerunner_amd.synth as synth
-    from edgerunner_amd import GEMVKernel
+    from edgerunner_amd import Capture, GEMVKernel
 
     gemv = GEMVKernel(ctx)
     W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
@@ -80,28 +85,29 @@ def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int)
     for i in range(warmup):
         enc(stream, wbufs[i % copies], xb, yb, M, K)
     stream.synchronize()
+    with Capture(ctx, stream) as cap:
+        for i in range(steps):
+            enc(stream, wbufs[i % copies], xb, yb, M, K)
+    graph = cap.graph
+    graph.launch(stream)  # untimed replay
+    stream.synchronize()
     e0, e1 = ctx.event(), ctx.event()
+    e0.record(stream)
+    graph.launch(stream)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1)
+    avg_us = ms * 1000.0 / steps
+    # eager: Python-launched back-to-back (includes host launch cost)
     e0.record(stream)
     for i in range(steps):
         enc(stream, wbufs[i % copies], xb, yb, M, K)
     e1.record(stream)
     stream.synchronize()
-    ms = e0.elapsed_ms(e1)
-    avg_us = ms * 1000.0 / steps
-    # per-launch event pairs: launch-gap-free kernel duration (diagnostic)
-    evs = [(ctx.event(), ctx.event()) for _ in range(min(steps, 64))]
-    for i, (a, b) in enumerate(evs):
-        a.record(stream)
-        enc(stream, wbufs[i % copies], xb, yb, M, K)
-        b.record(stream)
-    stream.synchronize()
-    per = sorted(a.elapsed_ms(b) * 1000.0 for a, b in evs)
-    med_us = per[len(per) // 2]
-    for a, b in evs:
-        a.destroy()
-        b.destroy()
+    eager_us = e0.elapsed_ms(e1) * 1000.0 / steps
     nbytes = algorithmic_bytes(fmt, M, K)
     y = yb.download(np.float32, stream=stream)
+    graph.destroy()
     for b in wbufs:
         b.free()
     xb.free()
@@ -113,8 +119,7 @@ def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int)
         "fmt": fmt, "M": M, "K": K, "copies": copies, "bytes_per_call": nbytes,
         "us_per_call": avg_us, "GBps": nbytes / (avg_us * 1e-6) / 1e9,
         "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-        "us_per_call_event_pair_median": med_us,
-        "GBps_event_pair": nbytes / (med_us * 1e-6) / 1e9,
+        "us_per_call_eager": eager_us,
         "ms_total": ms, "y_finite": bool(np.all(np.isfinite(y))),
     }
 
@@ -193,8 +198,7 @@ def main() -> int:
         r = bench_gemv(ctx, fmt, M, K, cfg, args.steps, args.warmup)
         results[name] = r
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
-            f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s); event-pair median "
-            f"{r['us_per_call_event_pair_median']:.2f} us")
+            f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s); eager {r['us_per_call_eager']:.2f} us")
 
     h = results[head[0]]
     cpu = None

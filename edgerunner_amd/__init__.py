@@ -5,7 +5,7 @@ hand-written HIP kernels behind the C ABI in include/er_hip.h.  This Python
 package is the host-side mirror of the reference's Swift dispatch protocol
 (GEMVKernel, Dequant*Kernel) used by the tests and the benchmark.
 """
-from .runtime import (AllocationFailed, Buffer, Context, DequantKernelError, DeviceError,  # noqa: F401
+from .runtime import (AllocationFailed, Buffer, Capture, Context, Graph, DequantKernelError, DeviceError,  # noqa: F401
                       EdgeRunnerHIPError, EncodingFailed, Event, FunctionNotFound, GEMVError,
                       InvalidArgument, InvalidBlockDataCount, InvalidMatrixShape,
                       InvalidVectorShape, LibraryNotFound, Stream, default_context)
@@ -13,7 +13,7 @@ from .gemv import (DequantQ4KMKernel, DequantQ6KKernel, DequantQ8_0Kernel,  # no
                    GEMVKernel, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0)
 
 __all__ = [
-    "Context", "Buffer", "Stream", "Event", "default_context",
+    "Context", "Buffer", "Stream", "Event", "Graph", "Capture", "default_context",
     "GEMVKernel", "DequantQ8_0Kernel", "DequantQ4KMKernel", "DequantQ6KKernel",
     "GEMVError", "DequantKernelError", "EdgeRunnerHIPError",
     "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q6_K",

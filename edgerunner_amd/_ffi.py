@@ -57,6 +57,7 @@ class er_device_info(C.Structure):
 _ctx_p = C.c_void_p
 _stream = C.c_void_p
 _event = C.c_void_p
+_graph = C.c_void_p
 _u32 = C.c_uint32
 _u64 = C.c_uint64
 
@@ -79,6 +80,10 @@ SIGNATURES = {
     "er_hip_event_destroy": (C.c_int, [_ctx_p, _event]),
     "er_hip_event_record": (C.c_int, [_ctx_p, _event, _stream]),
     "er_hip_event_elapsed_ms": (C.c_int, [_ctx_p, _event, _event, C.POINTER(C.c_float)]),
+    "er_hip_graph_begin": (C.c_int, [_ctx_p, _stream]),
+    "er_hip_graph_end": (C.c_int, [_ctx_p, _stream, C.POINTER(_graph)]),
+    "er_hip_graph_launch": (C.c_int, [_ctx_p, _graph, _stream]),
+    "er_hip_graph_destroy": (C.c_int, [_ctx_p, _graph]),
     "er_hip_dequant_q8_0": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, er_buffer]),
     "er_hip_dequant_q4_k": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, er_buffer]),
     "er_hip_dequant_q6_k": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, er_buffer]),

@@ -22,12 +22,14 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 
 # Device flags.  Packed-FP32 instruction selection is disabled for every
-# kernel (the hardware's packed fp32 forms are not used by this library).
+# kernel (the hardware's packed fp32 forms are not used by this library);
+# 128-bit LDS accesses are enabled (ds_read_b128 / ds_write_b128).
 DEVICE_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++17",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Xclang", "-target-feature", "-Xclang", "+enable-ds128",
     "-munsafe-fp-atomics",
 ]
 
@@ -66,7 +68,7 @@ def build_host_library(code_object: Path = CODE_OBJECT, out: Path = LIB) -> Path
     host_o = BUILD / "er_hip.o"
     _run(["gcc", "-c", str(blob), "-o", str(blob_o)])
     _run(["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
-          "-I", str(ROCM / "include"), "-I", str(ROOT / "include"),
+          "-I", str(ROCM / "include"), "-I", str(ROOT / "include"), "-I", str(CSRC),
           "-c", str(CSRC / "er_hip.cpp"), "-o", str(host_o)])
     tmp = out.with_suffix(".so.tmp")
     _run(["g++", "-shared", "-o", str(tmp), str(host_o), str(blob_o),

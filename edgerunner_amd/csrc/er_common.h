@@ -27,6 +27,15 @@ ER_DEV float f16_to_f32(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
+// A constant materialised in a VGPR that the compiler treats as opaque, so
+// that masks reach VOP3 forms from a register instead of being split into
+// literal-carrying VOP2 pairs.
+ER_DEV uint32_t vreg_const(uint32_t c) {
+    uint32_t r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+    return r;
+}
+
 // Byte n of a dword, widened exactly (v_cvt_f32_ubyte{0..3}).
 ER_DEV float ub0(uint32_t v) { return (float)(v & 0xffu); }
 ER_DEV float ub1(uint32_t v) { return (float)((v >> 8) & 0xffu); }

@@ -5,33 +5,28 @@
 // and their token-batched forms (Dequant_Q4_K_M.metal:141-214,
 // Dequant_Q8_0.metal:143-197).  Bandwidth-bound: no MFMA.
 //
-// Work decomposition (all formats):
-//   * A row is cut into "slots" of 16 raw bytes of quantised weights
-//     (Q4_K: 8 slots per super-block, 32 weights each; Q6_K: 4 slots per
-//     super-block, 64 weights each; Q8_0: one slot per pair of blocks,
-//     68 bytes / 64 weights).
-//   * A wave64 is split into G = 64/LPR lane groups of LPR lanes; each group
-//     owns R consecutive rows and its lanes stride over the row's slots.
-//     The x values of a slot are read once from LDS and reused for all R rows
-//     of the group, and the raw loads for the R rows are issued back to back
-//     so each lane keeps R independent HBM requests in flight.
-//   * Partial sums are reduced across the LPR lanes with cross-lane
-//     shuffles; lane 0 of each group writes the R outputs.
-//   * The workgroup (4 waves) first stages x (K fp32) in LDS; when K*4 bytes
-//     exceeds the LDS budget (XG = true) x is read from global memory
-//     instead.
-//   * gridDim.y is the token count of the batched form: token t reads
-//     x + t*K and writes y + t*M (the reference's grid-y = token layout).
+// Two kernel families:
 //
-// Scale factoring: per sub-block the kernel accumulates sum(q*x) and uses the
-// precomputed sum(x) of the same 16/32 positions, i.e.
-//   Q4_K: (d*sc)*sum(q*x) - (dmin*m)*sum(x)
-//   Q6_K: (d*sc)*(sum(q6*x) - 32*sum(x))
-//   Q8_0: d*(sum((q+128)*x) - 128*sum(x))
-// which is the reference's sum of dequantised-weight * x products in a
-// different association; fp32 accumulation keeps the result within 1e-3
-// relative L2 of the CPU oracle.
-#include "er_common.h"
+// 1. Integer-dot kernels (Q4_K, and Q8_0 with K % 64 == 0): x is staged once
+//    per workgroup as three int8 limbs per value (er_xlimbs.h) and every
+//    weight x activation product is formed with v_dot4_i32_i8, exactly, in
+//    int32.  A "slot" is 64 weights of one row: a Q4_K sub-block pair
+//    (32 qs bytes + the block header) or two Q8_0 blocks (68 bytes).  A wave
+//    is split into 64/LPR lane groups of LPR lanes; a group owns R rows and
+//    each lane NS slots of each row.  Every weight load of a lane is issued
+//    up front (after the L2-resident x loads, before x staging), and the
+//    slots are consumed in issue order, so the wave computes on the first
+//    slot while the rest are still in flight.
+//
+// 2. fp32 kernels (Q6_K; Q8_0 with an odd number of blocks per row; rows
+//    longer than the integer kernels cover): x is staged in LDS as fp32, a
+//    16-byte "slot" of raw bytes is unpacked in registers and accumulated
+//    with fp32 FMAs.
+//
+// gridDim.y is the token count of the batched form: token t reads x + t*K and
+// writes y + t*M (the reference's grid-y = token layout).
+#include "er_gemv_cfg.h"
+#include "er_xlimbs.h"
 
 #ifndef ER_Q4K_ROWS
 #define ER_Q4K_ROWS 4
@@ -44,6 +39,218 @@
 #endif
 
 #define ER_GEMV_THREADS 256
+
+// ===========================================================================
+// Family 1: integer-dot kernels
+// ===========================================================================
+
+// x chunks held in registers per thread: ceil(4*LPR*NS/256) (the x of one row
+// slice of LPR*NS slots), at most 4; chunks beyond that are staged by
+// xl_store_tail after the weight loads.
+template <int LPR, int NS>
+struct I8Cfg {
+    static constexpr int G = 64 / LPR;
+    static constexpr int XG0 = (4 * LPR * NS + 255) / 256;
+    static constexpr int XG = XG0 < 1 ? 1 : (XG0 > 4 ? 4 : XG0);
+};
+
+// Q4_K slot s of a row = super-block s/4, sub-block pair p = s%4: header
+// (d, dmin, 12 scale bytes) + qs bytes [32p, 32p+32) = weights 64s..64s+63
+// (low nibbles: sub-block 2p, high nibbles: sub-block 2p+1).
+template <int LPR, int NS, int R>
+ER_DEV void gemv_q4k_i8(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                        float *__restrict__ y, uint32_t M, uint32_t K) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    using C = I8Cfg<LPR, NS>;
+    constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR, li = lane % LPR;
+    const uint32_t S = K >> 6;
+    const size_t rowBytes = (size_t)(K >> 8) * 144u;
+    const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+
+    float4 xr[C::XG][4];
+    xl_load<C::XG, NT>(x, K, xr);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 hdr[NS][R], qa[NS][R], qb[NS][R];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t s = min(li + (uint32_t)LPR * j, S - 1u);
+        const uint32_t p = s & 3u;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *bp = W + (size_t)min(row0 + (uint32_t)r, M - 1u) * rowBytes + (s >> 2) * 144u;
+            hdr[j][r] = ld16_a16(bp);
+            qa[j][r] = ld16_a16(bp + 16u + 32u * p);
+            qb[j][r] = ld16_a16(bp + 32u + 32u * p);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    xl_store<C::XG, NT>(lds, K, xr);
+    xl_store_tail<C::XG, NT>(x, lds, K);
+    __syncthreads();
+
+    const XLimbs X = xl_view(lds, K);
+    const uint32_t M0F = vreg_const(0x0f0f0f0fu);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t sRaw = li + (uint32_t)LPR * j;
+        const uint32_t s = min(sRaw, S - 1u);
+        const float live = sRaw < S ? 1.0f : 0.0f;
+        const uint32_t p = s & 3u;
+        u32x4 xv[ER_XL_PLANES][4];
+        xl_read_group(X, s, xv);
+        const float4 c16 = *(const float4 *)__builtin_assume_aligned(X.x16 + 4u * s, 16);
+        const float XL = c16.x + c16.y, XH = c16.z + c16.w;
+        const float sg = live * X.sg64[s];
+        // scale / min bytes of the pair: for p < 2 sc = s[2p..2p+1] & 63 and
+        // m = s[2p+4..2p+5] & 63; for p >= 2 (q = 2p-4) sc = (s[q+8] & 15) |
+        // (s[q] >> 6) << 4 and m = (s[q+8] >> 4) | (s[q+4] >> 6) << 4.
+        const bool lowp = p < 2u;
+        const uint32_t q4 = 2u * p - 4u;
+        const uint32_t sel1 = lowp ? (0x0c0c0000u | ((2u * p + 1u) << 8) | (2u * p))
+                                   : (0x0c0c0000u | ((q4 + 5u) << 8) | (q4 + 4u));
+        const uint32_t sel2 = lowp ? 0x0c0c0c0cu : (0x0c0c0000u | ((q4 + 1u) << 8) | q4);
+        const uint32_t maskLo = lowp ? 0x3f3fu : 0x0f0fu;
+        const uint32_t shM = lowp ? 0u : 4u;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const u32x4 h = hdr[j][r];
+            const uint32_t qw[8] = {qa[j][r].x, qa[j][r].y, qa[j][r].z, qa[j][r].w,
+                                    qb[j][r].x, qb[j][r].y, qb[j][r].z, qb[j][r].w};
+            // low nibbles: positions 4k..4k+3 of sub-block 2p (granule k/4);
+            // high nibbles: the same positions of sub-block 2p+1 (granule 2 + k/4)
+            int cL[ER_XL_PLANES] = {}, cH[ER_XL_PLANES] = {};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int lo = (int)(qw[k] & M0F);
+                const int hi = (int)((qw[k] >> 4) & M0F);
+#pragma unroll
+                for (int l = 0; l < ER_XL_PLANES; ++l) {
+                    cL[l] = __builtin_amdgcn_sdot4(lo, (int)xv[l][k >> 2][k & 3], cL[l], false);
+                    cH[l] = __builtin_amdgcn_sdot4(hi, (int)xv[l][2 + (k >> 2)][k & 3], cH[l], false);
+                }
+            }
+            const float T0 = xl_combine(cL[0], cL[1], cL[2]);
+            const float T1 = xl_combine(cH[0], cH[1], cH[2]);
+            // perm(S0, S1, sel): selector bytes 0-3 pick S1, 4-7 pick S0
+            const uint32_t X1 = __builtin_amdgcn_perm(h.w, h.y, sel1);
+            const uint32_t X2 = __builtin_amdgcn_perm(h.w, h.y, sel2);
+            const uint32_t sc = (X1 & maskLo) | ((X2 >> 2) & 0x3030u);
+            const uint32_t Y1 = __builtin_amdgcn_perm(h.w, h.z, sel1);
+            const uint32_t Y2 = __builtin_amdgcn_perm(h.w, h.z, sel2);
+            const uint32_t mm = ((Y1 >> shM) & maskLo) | ((Y2 >> 2) & 0x3030u);
+            const float d = f16_to_f32(h.x & 0xffffu), dmin = f16_to_f32(h.x >> 16);
+            const float sT = __builtin_fmaf(ub0(sc), T0, ub1(sc) * T1);
+            const float mX = __builtin_fmaf(ub0(mm), XL, ub1(mm) * XH);
+            float a = __builtin_fmaf(-(live * dmin), mX, acc[r]);
+            acc[r] = __builtin_fmaf(d * sg, sT, a);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+    }
+}
+
+// Q8_0 with K % 64 == 0: slot s = blocks 2s, 2s+1 = row bytes [68s, 68s+68)
+// (4-byte aligned).  Dwords v0..v16: block A d = v0[15:0], qs = bytes 2..33
+// (realigned by 2 bytes), block B d = v8[31:16], qs = v9..v16.  The int8 qs
+// bytes feed v_dot4_i32_i8 as they are.
+template <int LPR, int NS, int R>
+ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                         float *__restrict__ y, uint32_t M, uint32_t K) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    using C = I8Cfg<LPR, NS>;
+    constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR, li = lane % LPR;
+    const uint32_t S = K >> 6;
+    const size_t rowBytes = (size_t)S * 68u;
+    const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+
+    float4 xr[C::XG][4];
+    xl_load<C::XG, NT>(x, K, xr);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 v0[NS][R], v1[NS][R], v2[NS][R], v3[NS][R];
+    uint32_t v4[NS][R];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t s = min(li + (uint32_t)LPR * j, S - 1u);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *p = W + (size_t)min(row0 + (uint32_t)r, M - 1u) * rowBytes + (size_t)s * 68u;
+            v0[j][r] = ld16_a4(p);
+            v1[j][r] = ld16_a4(p + 16);
+            v2[j][r] = ld16_a4(p + 32);
+            v3[j][r] = ld16_a4(p + 48);
+            v4[j][r] = ld4_a4(p + 64);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    xl_store<C::XG, NT>(lds, K, xr);
+    xl_store_tail<C::XG, NT>(x, lds, K);
+    __syncthreads();
+
+    const XLimbs X = xl_view(lds, K);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t sRaw = li + (uint32_t)LPR * j;
+        const uint32_t s = min(sRaw, S - 1u);
+        const float sg = sRaw < S ? X.sg64[s] : 0.0f;
+        u32x4 xv[ER_XL_PLANES][4];
+        xl_read_group(X, s, xv);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t v[17] = {v0[j][r].x, v0[j][r].y, v0[j][r].z, v0[j][r].w,
+                                    v1[j][r].x, v1[j][r].y, v1[j][r].z, v1[j][r].w,
+                                    v2[j][r].x, v2[j][r].y, v2[j][r].z, v2[j][r].w,
+                                    v3[j][r].x, v3[j][r].y, v3[j][r].z, v3[j][r].w, v4[j][r]};
+            int cA[ER_XL_PLANES] = {}, cB[ER_XL_PLANES] = {};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int qa = (int)alignbyte(v[k + 1], v[k], 2);
+                const int qb = (int)v[9 + k];
+#pragma unroll
+                for (int l = 0; l < ER_XL_PLANES; ++l) {
+                    cA[l] = __builtin_amdgcn_sdot4(qa, (int)xv[l][k >> 2][k & 3], cA[l], false);
+                    cB[l] = __builtin_amdgcn_sdot4(qb, (int)xv[l][2 + (k >> 2)][k & 3], cB[l], false);
+                }
+            }
+            const float TA = xl_combine(cA[0], cA[1], cA[2]);
+            const float TB = xl_combine(cB[0], cB[1], cB[2]);
+            const float dA = f16_to_f32(v[0] & 0xffffu), dB = f16_to_f32(v[8] >> 16);
+            float a = __builtin_fmaf(sg * dA, TA, acc[r]);
+            acc[r] = __builtin_fmaf(sg * dB, TB, a);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+    }
+}
+
+// ===========================================================================
+// Family 2: fp32 kernels
+// ===========================================================================
 
 // Stages x[0..K) in LDS; returns the pointer the slot loop reads x from.
 template <bool XG>
@@ -376,8 +583,25 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
 
 // ---------------------------------------------------------------------------
 // Entry points (extern "C" so hipModuleGetFunction resolves them by name).
-// Naming: er_gemv_<fmt>_l<LPR>_<x source: s = LDS, g = global>.
+//   er_gemv_<fmt>_i8_l<LPR>_n<NS>_r<R> : integer-dot family (er_gemv_cfg.h)
+//   er_gemv_<fmt>_l<LPR>_<s|g>         : fp32 family, x staged in LDS (s) or
+//                                        read from global memory (g)
 // ---------------------------------------------------------------------------
+#define ER_I8_ENTRY(LPR, NS, R)                                                                \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q4k_i8_l##LPR##_n##NS##_r##R(const uint8_t *__restrict__ W,                  \
+                                             const float *__restrict__ x,                     \
+                                             float *__restrict__ y, uint32_t M, uint32_t K) { \
+        gemv_q4k_i8<LPR, NS, R>(W, x, y, M, K);                                              \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q8_0_i8_l##LPR##_n##NS##_r##R(const uint8_t *__restrict__ W,                 \
+                                              const float *__restrict__ x,                    \
+                                              float *__restrict__ y, uint32_t M, uint32_t K) { \
+        gemv_q8_0_i8<LPR, NS, R>(W, x, y, M, K);                                             \
+    }
+ER_I8_CONFIGS(ER_I8_ENTRY)
+
 #define ER_GEMV_ENTRY(fmt, impl, rows, lpr, xg, tag)                                       \
     extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                        \
         er_gemv_##fmt##_l##lpr##_##tag(const uint8_t *__restrict__ W,                     \
@@ -398,9 +622,10 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
     ER_GEMV_ENTRY(fmt, impl, rows, 8, true, g)   \
     ER_GEMV_ENTRY(fmt, impl, rows, 4, true, g)
 
-ER_GEMV_FAMILY(q4k, gemv_q4k, ER_Q4K_ROWS)
 ER_GEMV_FAMILY(q6k, gemv_q6k, ER_Q6K_ROWS)
-ER_GEMV_FAMILY(q8_0, gemv_q8_0, ER_Q8_0_ROWS)
+// fp32 fallbacks of the integer-dot formats for rows longer than 32768 weights
+ER_GEMV_ENTRY(q4k, gemv_q4k, ER_Q4K_ROWS, 64, true, g)
+ER_GEMV_ENTRY(q8_0, gemv_q8_0, ER_Q8_0_ROWS, 64, true, g)
 
 extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)
 er_gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict__ x,

@@ -9,12 +9,14 @@
 // (Sources/EdgeRunnerMetal/GEMVKernel.swift:1276-1300, 1415-1432) and the
 // Dequant*Kernel.dequantise checks (Sources/EdgeRunnerIO/DequantQ4KMKernel.swift:23-29).
 #include "er_hip.h"
+#include "er_gemv_cfg.h"
 
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 
@@ -34,20 +36,12 @@ er_status fail(er_status st, const char *fmt, ...) {
 }
 
 // Kernel table: every kernel the library launches, resolved at create time.
+// The integer-dot GEMV kernels (one per er_gemv_cfg.h entry and format) are
+// listed separately in kI8Cfg.
 #define ER_KERNEL_LIST(X)                                                              \
     X(DEQUANT_Q8_0, "er_dequant_q8_0")                                                 \
     X(DEQUANT_Q4_K, "er_dequant_q4_k")                                                 \
     X(DEQUANT_Q6_K, "er_dequant_q6_k")                                                 \
-    X(GEMV_Q4K_L64_S, "er_gemv_q4k_l64_s")                                             \
-    X(GEMV_Q4K_L32_S, "er_gemv_q4k_l32_s")                                             \
-    X(GEMV_Q4K_L16_S, "er_gemv_q4k_l16_s")                                             \
-    X(GEMV_Q4K_L8_S, "er_gemv_q4k_l8_s")                                               \
-    X(GEMV_Q4K_L4_S, "er_gemv_q4k_l4_s")                                               \
-    X(GEMV_Q4K_L64_G, "er_gemv_q4k_l64_g")                                             \
-    X(GEMV_Q4K_L32_G, "er_gemv_q4k_l32_g")                                             \
-    X(GEMV_Q4K_L16_G, "er_gemv_q4k_l16_g")                                             \
-    X(GEMV_Q4K_L8_G, "er_gemv_q4k_l8_g")                                               \
-    X(GEMV_Q4K_L4_G, "er_gemv_q4k_l4_g")                                               \
     X(GEMV_Q6K_L64_S, "er_gemv_q6k_l64_s")                                             \
     X(GEMV_Q6K_L32_S, "er_gemv_q6k_l32_s")                                             \
     X(GEMV_Q6K_L16_S, "er_gemv_q6k_l16_s")                                             \
@@ -58,16 +52,8 @@ er_status fail(er_status st, const char *fmt, ...) {
     X(GEMV_Q6K_L16_G, "er_gemv_q6k_l16_g")                                             \
     X(GEMV_Q6K_L8_G, "er_gemv_q6k_l8_g")                                               \
     X(GEMV_Q6K_L4_G, "er_gemv_q6k_l4_g")                                               \
-    X(GEMV_Q8_0_L64_S, "er_gemv_q8_0_l64_s")                                           \
-    X(GEMV_Q8_0_L32_S, "er_gemv_q8_0_l32_s")                                           \
-    X(GEMV_Q8_0_L16_S, "er_gemv_q8_0_l16_s")                                           \
-    X(GEMV_Q8_0_L8_S, "er_gemv_q8_0_l8_s")                                             \
-    X(GEMV_Q8_0_L4_S, "er_gemv_q8_0_l4_s")                                             \
+    X(GEMV_Q4K_L64_G, "er_gemv_q4k_l64_g")                                             \
     X(GEMV_Q8_0_L64_G, "er_gemv_q8_0_l64_g")                                           \
-    X(GEMV_Q8_0_L32_G, "er_gemv_q8_0_l32_g")                                           \
-    X(GEMV_Q8_0_L16_G, "er_gemv_q8_0_l16_g")                                           \
-    X(GEMV_Q8_0_L8_G, "er_gemv_q8_0_l8_g")                                             \
-    X(GEMV_Q8_0_L4_G, "er_gemv_q8_0_l4_g")                                             \
     X(GEMV_Q8_0_ANY, "er_gemv_q8_0_any")
 
 enum KernelId {
@@ -83,12 +69,24 @@ const char *const kKernelNames[K_COUNT] = {
 #undef ER_NAME
 };
 
-// Rows per lane group of each GEMV family; must match ER_*_ROWS in er_gemv.hip.
+// Rows per lane group of the fp32 GEMV family; must match ER_*_ROWS in er_gemv.hip.
 constexpr uint32_t kQ4KRows = 4;
 constexpr uint32_t kQ6KRows = 2;
 constexpr uint32_t kQ8_0Rows = 2;
-constexpr uint32_t kGemvThreads = 256;
-constexpr uint64_t kLdsXLimit = 64u * 1024u;  // bytes of x staged in LDS
+constexpr uint32_t kGemvThreads = 64u * ER_GEMV_WAVES;
+constexpr uint64_t kLdsXLimit = 64u * 1024u;  // bytes of fp32 x staged in LDS
+
+// Integer-dot GEMV configurations {LPR, NS, R} (er_gemv_cfg.h).
+struct I8Cfg {
+    uint8_t lpr, ns, r;
+};
+#define ER_I8_ROW(LPR, NS, R) {LPR, NS, R},
+constexpr I8Cfg kI8Cfg[] = {ER_I8_CONFIGS(ER_I8_ROW)};
+#undef ER_I8_ROW
+constexpr int kI8Count = (int)(sizeof(kI8Cfg) / sizeof(kI8Cfg[0]));
+// Integer-dot kernels stage 3K + K/4 + K/16 bytes of x in LDS; rows up to this
+// length use them (the default dynamic LDS limit is 64 KiB).
+constexpr uint32_t kI8MaxK = 16384;
 
 }  // namespace
 
@@ -96,7 +94,10 @@ struct er_hip_ctx {
     int device = 0;
     hipModule_t module = nullptr;
     hipFunction_t fn[K_COUNT] = {};
+    hipFunction_t fnQ4KI8[kI8Count] = {};
+    hipFunction_t fnQ8I8[kI8Count] = {};
     int cu_count = 0;
+    int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
     er_device_info info{};
 };
 
@@ -125,6 +126,46 @@ er_status launch(const er_hip_ctx *ctx, KernelId k, dim3 grid, dim3 block, uint3
         return fail(ER_ERR_ENCODING_FAILED, "hipModuleLaunchKernel(%s): %s", kKernelNames[k],
                     hipGetErrorString(e));
     return ER_OK;
+}
+
+er_status launch_fn(hipFunction_t f, const char *name, dim3 grid, dim3 block, uint32_t lds,
+                    er_stream stream, void **args) {
+    hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, lds,
+                                         (hipStream_t)stream, args, nullptr);
+    if (e != hipSuccess)
+        return fail(ER_ERR_ENCODING_FAILED, "hipModuleLaunchKernel(%s): %s", name, hipGetErrorString(e));
+    return ER_OK;
+}
+
+// Picks the integer-dot configuration for a row of S 64-weight slots and M
+// rows: the lane split (LPR, NS) that leaves the fewest idle slots (ties: more
+// lanes per row), then the most rows per lane group that still gives every CU
+// two workgroups.  Returns -1 when no configuration covers S.
+int pick_i8(uint32_t S, uint32_t M, int cu) {
+    static const uint32_t lprs[] = {64, 32, 16, 4};
+    uint32_t bestL = 0, bestN = 0, bestWaste = 0xffffffffu;
+    for (uint32_t L : lprs) {
+        const uint32_t N = (S + L - 1) / L;
+        if (N > 8) continue;
+        const uint32_t waste = L * N - S;
+        if (waste < bestWaste) {
+            bestWaste = waste;
+            bestL = L;
+            bestN = N;
+        }
+    }
+    if (!bestL) return -1;
+    const uint32_t G = 64u / bestL;
+    int pick = -1;
+    for (uint32_t R : {4u, 2u, 1u}) {
+        for (int i = 0; i < kI8Count; ++i) {
+            if (kI8Cfg[i].lpr != bestL || kI8Cfg[i].ns != bestN || kI8Cfg[i].r != R) continue;
+            const uint64_t wgs = ((uint64_t)M + ER_GEMV_WAVES * G * R - 1) / (ER_GEMV_WAVES * G * R);
+            if (wgs >= 2u * (uint64_t)cu || R == 1u) return i;
+            if (pick < 0) pick = i;
+        }
+    }
+    return pick;
 }
 
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
@@ -202,33 +243,44 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     st = bind_device(ctx);
     if (st != ER_OK) return st;
 
-    const bool xg = (uint64_t)K * 4u > kLdsXLimit;
-    const uint32_t lds = xg ? 0u : K * 4u;
-    KernelId k;
-    uint32_t rows, slots;
-    if (f == Fmt::Q4_K) {
-        slots = (K / 256u) * 8u;
-        rows = kQ4KRows;
-        k = (KernelId)(K_GEMV_Q4K_L64_S + lpr_index(lanes_per_row(slots)) + (xg ? 5 : 0));
-    } else if (f == Fmt::Q6_K) {
-        slots = (K / 256u) * 4u;
-        rows = kQ6KRows;
-        k = (KernelId)(K_GEMV_Q6K_L64_S + lpr_index(lanes_per_row(slots)) + (xg ? 5 : 0));
-    } else if (K % 64u == 0) {
-        slots = K / 64u;
-        rows = kQ8_0Rows;
-        k = (KernelId)(K_GEMV_Q8_0_L64_S + lpr_index(lanes_per_row(slots)) + (xg ? 5 : 0));
-    } else {
+    void *args[] = {&W.data, &x.data, &y.data, &M, &K};
+    const bool q8Aligned = f == Fmt::Q8_0 && K % 64u == 0;
+    if ((f == Fmt::Q4_K || q8Aligned) && K <= kI8MaxK) {
+        int ci = pick_i8(K / 64u, M, ctx->cu_count);
+        if (ctx->i8_override >= 0 && (uint32_t)kI8Cfg[ctx->i8_override].lpr *
+                                             kI8Cfg[ctx->i8_override].ns >= K / 64u)
+            ci = ctx->i8_override;
+        if (ci >= 0) {
+            const I8Cfg &c = kI8Cfg[ci];
+            const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
+            const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+            dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
+            hipFunction_t fn = f == Fmt::Q4_K ? ctx->fnQ4KI8[ci] : ctx->fnQ8I8[ci];
+            return launch_fn(fn, f == Fmt::Q4_K ? "er_gemv_q4k_i8" : "er_gemv_q8_0_i8", grid,
+                             dim3(kGemvThreads, 1, 1), lds, stream, args);
+        }
+    }
+    if (f == Fmt::Q8_0 && !q8Aligned) {
         // odd number of Q8_0 blocks per row: generic kernel, one row group per wave
-        uint32_t rowsPerBlock = (kGemvThreads / 64u) * 2u;
+        const uint32_t rowsPerBlock = ER_GEMV_WAVES * 2u;
         dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
-        void *args[] = {&W.data, &x.data, &y.data, &M, &K};
         return launch(ctx, K_GEMV_Q8_0_ANY, grid, dim3(kGemvThreads, 1, 1), 0, stream, args);
     }
+    if (f != Fmt::Q6_K) {
+        // rows longer than the integer-dot kernels cover: fp32 kernel, x from global memory
+        const uint32_t rows = f == Fmt::Q4_K ? kQ4KRows : kQ8_0Rows;
+        const uint32_t rowsPerBlock = ER_GEMV_WAVES * rows;
+        dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
+        return launch(ctx, f == Fmt::Q4_K ? K_GEMV_Q4K_L64_G : K_GEMV_Q8_0_L64_G, grid,
+                      dim3(kGemvThreads, 1, 1), 0, stream, args);
+    }
+    const bool xg = (uint64_t)K * 4u > kLdsXLimit;
+    const uint32_t lds = xg ? 0u : K * 4u;
+    const uint32_t slots = (K / 256u) * 4u;
     const uint32_t lpr = lanes_per_row(slots);
-    const uint32_t rowsPerBlock = (kGemvThreads / 64u) * (64u / lpr) * rows;
+    const KernelId k = (KernelId)(K_GEMV_Q6K_L64_S + lpr_index(lpr) + (xg ? 5 : 0));
+    const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / lpr) * kQ6KRows;
     dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
-    void *args[] = {&W.data, &x.data, &y.data, &M, &K};
     return launch(ctx, k, grid, dim3(kGemvThreads, 1, 1), lds, stream, args);
 }
 
@@ -322,6 +374,26 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
             return fail(ER_ERR_FUNCTION_NOT_FOUND, "functionNotFound(%s): %s", kKernelNames[i],
                         hipGetErrorString(e));
         }
+    }
+    for (int i = 0; i < kI8Count; ++i) {
+        char name[64];
+        for (int fmt = 0; fmt < 2; ++fmt) {
+            std::snprintf(name, sizeof(name), "er_gemv_%s_i8_l%u_n%u_r%u", fmt ? "q8_0" : "q4k",
+                          (unsigned)kI8Cfg[i].lpr, (unsigned)kI8Cfg[i].ns, (unsigned)kI8Cfg[i].r);
+            e = hipModuleGetFunction(fmt ? &ctx->fnQ8I8[i] : &ctx->fnQ4KI8[i], ctx->module, name);
+            if (e != hipSuccess) {
+                (void)hipModuleUnload(ctx->module);
+                delete ctx;
+                return fail(ER_ERR_FUNCTION_NOT_FOUND, "functionNotFound(%s): %s", name,
+                            hipGetErrorString(e));
+            }
+        }
+    }
+    if (const char *ov = std::getenv("ER_HIP_GEMV_CONFIG")) {
+        unsigned l = 0, n = 0, r = 0;
+        if (std::sscanf(ov, "%u:%u:%u", &l, &n, &r) == 3)
+            for (int i = 0; i < kI8Count; ++i)
+                if (kI8Cfg[i].lpr == l && kI8Cfg[i].ns == n && kI8Cfg[i].r == r) ctx->i8_override = i;
     }
     er_device_info &info = ctx->info;
     info.device = device;
@@ -488,6 +560,55 @@ er_status er_hip_event_elapsed_ms(er_hip_ctx *ctx, er_event start, er_event end,
     hipError_t e = hipEventSynchronize((hipEvent_t)end);
     if (e == hipSuccess) e = hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end);
     if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipEventElapsedTime: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_graph_begin(er_hip_ctx *ctx, er_stream stream) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!stream) return fail(ER_ERR_INVALID_ARGUMENT, "graph capture needs a created stream, not the null stream");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipError_t e = hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_graph_end(er_hip_ctx *ctx, er_stream stream, er_graph *out) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!stream || !out) return fail(ER_ERR_INVALID_ARGUMENT, "null stream/out");
+    *out = nullptr;
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture((hipStream_t)stream, &g);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    hipGraphExec_t ge = nullptr;
+    e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    *out = (er_graph)ge;
+    return ER_OK;
+}
+
+er_status er_hip_graph_launch(er_hip_ctx *ctx, er_graph graph, er_stream stream) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!graph) return fail(ER_ERR_INVALID_ARGUMENT, "null graph");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipError_t e = hipGraphLaunch((hipGraphExec_t)graph, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(ER_ERR_ENCODING_FAILED, "hipGraphLaunch: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
+er_status er_hip_graph_destroy(er_hip_ctx *ctx, er_graph graph) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!graph) return ER_OK;
+    hipError_t e = hipGraphExecDestroy((hipGraphExec_t)graph);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "hipGraphExecDestroy: %s", hipGetErrorString(e));
     return ER_OK;
 }
 

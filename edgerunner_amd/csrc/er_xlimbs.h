@@ -1,0 +1,165 @@
+// er_xlimbs.h -- activation staging for the integer-dot GEMV kernels.
+//
+// A workgroup converts the fp32 activation vector x[0..K) once into LDS as
+// three signed int8 "limbs" per value, so that the weight x activation
+// products can be formed with v_dot4_i32_i8 (4 MACs per instruction, exact
+// int32 accumulation) instead of per-weight float conversions.
+//
+// Representation, per 64-value group g (positions [64g, 64g+64)):
+//   s_g  = smallest power of two with max|x| / s_g <= 2080768 = 127*2^14
+//          (0 for an all-zero group)
+//   xi   = rint(x / s_g)                   |xi| <= 2080768, exact scaling (s_g = 2^e)
+//   l0   = floor((xi + 8192) / 16384)      in [-127, 127]
+//   r    = xi - 16384 * l0                 in [-8192, 8191]
+//   l1   = floor((r + 64) / 128)           in [-64, 64]
+//   l2   = r - 128 * l1                    in [-64, 63]
+//   x   ~= s_g * (16384 * l0 + 128 * l1 + l2),   |error| <= s_g / 2 <= max|x_g| / 2^21
+// so every activation carries at least 21 significant bits relative to its
+// group maximum (fp32-class), and a one-hot x is represented exactly.
+//
+// LDS layout (K a multiple of 64):
+//   [0, 3K)        planes 0..2: limb bytes l0, l1, l2; 16-byte granules swizzled by xl_gswz
+//   [3K, 3K+K/4)   x16[K/16]  fp32 sums of each 16-value chunk (exact fp32 x)
+//   then           sg64[K/64] the group scales s_g
+#pragma once
+
+#include "er_common.h"
+
+#define ER_XL_QMAX 2080768.0f
+#define ER_XL_PLANES 3
+
+// 16-byte granule swizzle: the 8 lanes that one ds_read_b128 cycle serves read
+// granules 4s+m (s = 8 consecutive slots, m fixed); XOR-ing bits 3-4 into bits
+// 0-1 spreads them over all 8 four-bank groups.
+ER_DEV uint32_t xl_gswz(uint32_t G) { return G ^ ((G >> 3) & 3u); }
+
+ER_DEV uint32_t xl_lds_bytes(uint32_t K) { return ER_XL_PLANES * K + (K / 16u) * 4u + (K / 64u) * 4u; }
+
+struct XLimbs {
+    const uint8_t *planes;
+    const float *x16;
+    const float *sg64;
+    uint32_t K;
+};
+
+ER_DEV XLimbs xl_view(const uint32_t *lds, uint32_t K) {
+    XLimbs v;
+    v.planes = (const uint8_t *)lds;
+    v.x16 = (const float *)(lds + (ER_XL_PLANES * K) / 4u);
+    v.sg64 = v.x16 + (K >> 4);
+    v.K = K;
+    return v;
+}
+
+// Loads of chunk c (16 values) of x for thread `tid`; XG chunks per thread.
+// Out-of-range chunks reload the last chunk (always in bounds, never stored).
+template <int XG, int NT>
+ER_DEV void xl_load(const float *__restrict__ x, uint32_t K, float4 (&xr)[XG][4]) {
+    const uint32_t C16 = K >> 4;
+#pragma unroll
+    for (int c = 0; c < XG; ++c) {
+        const uint32_t t = min(threadIdx.x + (uint32_t)NT * c, C16 - 1u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xr[c][q] = ((const float4 *)(x + 16u * t))[q];
+    }
+}
+
+// Power-of-two group scale for a group maximum mx >= 0: the smallest 2^e with
+// mx / 2^e <= ER_XL_QMAX (0 when mx == 0); inv = 1 / scale exactly.
+ER_DEV void xl_scale(float mx, float *sg, float *inv) {
+    const float v = mx * (1.0f / ER_XL_QMAX);
+    uint32_t b = __float_as_uint(v);
+    b = (b + 0x007fffffu) & 0xff800000u;  // round up to a power of two (v >= 0)
+    if (mx > 0.0f && b == 0u) b = 0x00800000u;  // keep the scale normal
+    *sg = mx > 0.0f ? __uint_as_float(b) : 0.0f;
+    // 1/2^e = 2^-e: exponent field 254 - e_field (exact for normal scales)
+    *inv = mx > 0.0f ? __uint_as_float((254u - (b >> 23)) << 23) : 0.0f;
+}
+
+// Converts one 16-value chunk (index tRaw, values in xr) into LDS.  The 4
+// chunks of a 64-group are held by 4 consecutive lanes, which exchange their
+// maxima; every lane of the wave must call this together.
+ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uint32_t tRaw) {
+    const uint32_t C16 = K >> 4;
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        v[4 * q + 0] = xr[q].x;
+        v[4 * q + 1] = xr[q].y;
+        v[4 * q + 2] = xr[q].z;
+        v[4 * q + 3] = xr[q].w;
+    }
+    float mx = 0.0f, sm = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        mx = fmaxf(mx, fabsf(v[q]));
+        sm += v[q];
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    float sg, inv;
+    xl_scale(mx, &sg, &inv);
+    uint32_t lb[ER_XL_PLANES][4] = {};
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int xi = (int)__builtin_rintf(v[q] * inv);
+        const int l0 = (xi + 8192) >> 14;
+        const int r = xi - (l0 << 14);
+        const int l1 = (r + 64) >> 7;
+        const int l2 = r - (l1 << 7);
+        lb[0][q >> 2] |= ((uint32_t)l0 & 0xffu) << (8 * (q & 3));
+        lb[1][q >> 2] |= ((uint32_t)l1 & 0xffu) << (8 * (q & 3));
+        lb[2][q >> 2] |= ((uint32_t)l2 & 0xffu) << (8 * (q & 3));
+    }
+    // chunks past the end are clamped copies with a different group max: never stored
+    if (tRaw < C16) {
+        uint8_t *planes = (uint8_t *)lds;
+        float *x16 = (float *)(lds + (ER_XL_PLANES * K) / 4u);
+        float *sg64 = x16 + C16;
+        const uint32_t G = xl_gswz(tRaw);
+#pragma unroll
+        for (int l = 0; l < ER_XL_PLANES; ++l)
+            *(u32x4 *)__builtin_assume_aligned(planes + (size_t)l * K + 16u * G, 16) =
+                u32x4{lb[l][0], lb[l][1], lb[l][2], lb[l][3]};
+        x16[tRaw] = sm;
+        if ((tRaw & 3u) == 0) sg64[tRaw >> 2] = sg;
+    }
+}
+
+// Stores the XG register-held chunks of this thread.
+template <int XG, int NT>
+ER_DEV void xl_store(uint32_t *lds, uint32_t K, const float4 (&xr)[XG][4]) {
+#pragma unroll
+    for (int c = 0; c < XG; ++c) xl_store_chunk(lds, K, xr[c], threadIdx.x + (uint32_t)NT * c);
+}
+
+// Chunks with index >= XG*NT (K beyond the register-staged part): loaded and
+// stored after the weight loads are in flight.
+template <int XG, int NT>
+ER_DEV void xl_store_tail(const float *__restrict__ x, uint32_t *lds, uint32_t K) {
+    const uint32_t C16 = K >> 4;
+    for (uint32_t base = (uint32_t)NT * XG; base < C16; base += NT) {
+        float4 xr[4];
+        const uint32_t t = min(base + threadIdx.x, C16 - 1u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xr[q] = ((const float4 *)(x + 16u * t))[q];
+        xl_store_chunk(lds, K, xr, base + threadIdx.x);
+    }
+}
+
+// The 4 granules (64 positions) of 64-group `grp` from every plane.
+ER_DEV void xl_read_group(const XLimbs &X, uint32_t grp, u32x4 (&xv)[ER_XL_PLANES][4]) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const uint32_t off = 16u * xl_gswz(4u * grp + (uint32_t)m);
+#pragma unroll
+        for (int l = 0; l < ER_XL_PLANES; ++l)
+            xv[l][m] = *(const u32x4 *)__builtin_assume_aligned(X.planes + (size_t)l * X.K + off, 16);
+    }
+}
+
+// Limb partial sums (each an exact int32 dot product) recombined into the
+// value of sum(q * xi): c0 * 2^14 + c1 * 2^7 + c2, rounded once to fp32.
+ER_DEV float xl_combine(int c0, int c1, int c2) {
+    return __builtin_fmaf((float)c0, 16384.0f, (float)((c1 << 7) + c2));
+}

@@ -182,6 +182,50 @@ class Event:
             self.handle = C.c_void_p()
 
 
+class Graph:
+    """A recorded sequence of encodes, replayed with launch() (hipGraphExec)."""
+
+    def __init__(self, ctx: "Context", handle):
+        self.ctx = ctx
+        self.handle = handle
+
+    def launch(self, stream: "Optional[Stream]" = None) -> None:
+        check(self.ctx.lib.er_hip_graph_launch(self.ctx.handle, self.handle, _sh(stream)))
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(self.ctx.lib.er_hip_graph_destroy(self.ctx.handle, self.handle))
+            self.handle = C.c_void_p()
+
+
+class Capture:
+    """Context manager recording every encode on `stream` into a Graph:
+
+        with Capture(ctx, stream) as cap:
+            gemv.encodeQ4KWeights(stream, ...)
+        cap.graph.launch(stream)
+    """
+
+    def __init__(self, ctx: "Context", stream: "Stream"):
+        self.ctx = ctx
+        self.stream = stream
+        self.graph: Optional[Graph] = None
+
+    def __enter__(self) -> "Capture":
+        check(self.ctx.lib.er_hip_graph_begin(self.ctx.handle, self.stream.handle))
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> bool:
+        h = C.c_void_p()
+        st = self.ctx.lib.er_hip_graph_end(self.ctx.handle, self.stream.handle, C.byref(h))
+        if exc_type is None:
+            check(st)
+            self.graph = Graph(self.ctx, h)
+        elif st == _ffi.ER_OK and h:
+            self.ctx.lib.er_hip_graph_destroy(self.ctx.handle, h)
+        return False
+
+
 def _sh(stream: Optional[Stream]):
     return stream.handle if stream is not None else None
 

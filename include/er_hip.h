@@ -88,6 +88,7 @@ typedef struct er_tensor_storage {
 typedef struct er_hip_ctx er_hip_ctx;
 typedef void *er_stream; /* hipStream_t; NULL = the device's null stream */
 typedef void *er_event;  /* hipEvent_t */
+typedef void *er_graph;  /* instantiated hipGraphExec_t */
 
 typedef struct er_device_info {
     int device;
@@ -129,6 +130,18 @@ er_status er_hip_event_create(er_hip_ctx *ctx, er_event *out);
 er_status er_hip_event_destroy(er_hip_ctx *ctx, er_event ev);
 er_status er_hip_event_record(er_hip_ctx *ctx, er_event ev, er_stream stream);
 er_status er_hip_event_elapsed_ms(er_hip_ctx *ctx, er_event start, er_event end, float *ms);
+
+/* ---- recorded command sequences: the MTLCommandBuffer / indirect command
+ * buffer analogue for replaying a fixed sequence of encodes (e.g. every
+ * projection of a decode step, GEMVKernel.encode* calls on one command buffer,
+ * Tests/EdgeRunnerMetalTests/GEMVTests.swift:662-734).  Between begin and end,
+ * encode calls on `stream` are recorded instead of executed (the stream must
+ * not be the null stream); the result is replayed with er_hip_graph_launch on
+ * any stream.  Buffers are bound by address at record time. ---- */
+er_status er_hip_graph_begin(er_hip_ctx *ctx, er_stream stream);
+er_status er_hip_graph_end(er_hip_ctx *ctx, er_stream stream, er_graph *out);
+er_status er_hip_graph_launch(er_hip_ctx *ctx, er_graph graph, er_stream stream);
+er_status er_hip_graph_destroy(er_hip_ctx *ctx, er_graph graph);
 
 /* ---- dequantisation to fp32 ----
  * Replace DequantQ8_0Kernel.dequantise (Sources/EdgeRunnerIO/DequantQ8_0Kernel.swift:18-78),
