@@ -153,14 +153,148 @@ def cpu_baseline(fmt: str, M: int, K: int, cfg: int, budget_s: float) -> dict:
     }
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "gemv_hbm_traffic.txt"
+
+
 def load_traffic(name: str):
-    p = ROOT / "profiles" / "traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get(name)
-        except Exception:
-            return None
+    """HBM bytes per launch of workload `name` from the committed rocprofv3
+    counter summary (lines `workload fetch_bytes write_bytes`), or None."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        f = line.split()
+        if len(f) == 3 and f[0] == name and not line.startswith("#"):
+            return int(float(f[1]) + float(f[2]))
     return None
+
+
+COPY_CAL_BYTES = 64 << 20
+
+
+def probe(ctx, todo, steps: int) -> None:
+    """Counter-collection driver (run under `rocprofv3 --pmc ...`): three
+    device-to-device copies of COPY_CAL_BYTES (the calibration kernel of known
+    traffic), then `steps` launches of each workload over rotating weights."""
+    import edgerunner_amd.synth as synth
+    from edgerunner_amd import GEMVKernel
+
+    stream = ctx.stream()
+    src, dst = ctx.alloc(COPY_CAL_BYTES), ctx.alloc(COPY_CAL_BYTES)
+    for _ in range(3):
+        dst.copy_from(src, stream=stream)
+    stream.synchronize()
+    src.free()
+    dst.free()
+    gemv = GEMVKernel(ctx)
+    for name, fmt, M, K, cfg in todo:
+        W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
+        x = synth.normal_f32(synth.seed(cfg, 1), K)
+        copies = max(2, -(-ROTATE_BYTES // W.nbytes))
+        wbufs = [ctx.upload(W, stream) for _ in range(copies)]
+        xb, yb = ctx.upload(x, stream), ctx.alloc(4 * M)
+        enc = getattr(gemv, ENCODE[fmt])
+        for i in range(steps):
+            enc(stream, wbufs[i % copies], xb, yb, M, K)
+        stream.synchronize()
+        log(f"probe {name}: {steps} launches")
+        for b in wbufs:
+            b.free()
+        xb.free()
+        yb.free()
+    stream.destroy()
+
+
+def _read_csv(path: Path):
+    import csv
+    with open(path, newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def summarize(root: Path) -> str:
+    """Markdown summary of a rocprofv3 output tree made by the profiling
+    commands in DESIGN.md: kernel stats (stats/), FETCH_SIZE (fetch/) and
+    WRITE_SIZE (write/) counter runs of `--probe`."""
+    out = []
+    stats = sorted(root.glob("stats/**/*kernel_stats.csv"))
+    if stats:
+        out.append("## Kernel statistics (rocprofv3 --kernel-trace --stats)\n")
+        out.append("| kernel | calls | avg us | min us | max us | % time |")
+        out.append("|---|---|---|---|---|---|")
+        for r in _read_csv(stats[0]):
+            out.append(f"| {r['Name']} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                       f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                       f"{float(r['Percentage']):.1f} |")
+        out.append("")
+    traces = sorted(root.glob("stats/**/*kernel_trace.csv"))
+    if traces:
+        import collections
+        by = collections.defaultdict(list)
+        for r in _read_csv(traces[0]):
+            key = (r["Kernel_Name"], r.get("Grid_Size_X", r.get("Grid_Size", "")),
+                   r.get("Grid_Size_Y", ""))
+            by[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        out.append("## Per-launch-shape durations (kernel trace)\n")
+        out.append("| kernel | grid x | grid y | launches | avg us | median us |")
+        out.append("|---|---|---|---|---|---|")
+        for (k, gx, gy), v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+            v = sorted(v)
+            out.append(f"| {k} | {gx} | {gy} | {len(v)} | {sum(v) / len(v):.2f} | "
+                       f"{v[len(v) // 2]:.2f} |")
+        out.append("")
+    per_workload = {}
+    for counter, sub in (("FETCH_SIZE", "fetch"), ("WRITE_SIZE", "write")):
+        files = sorted(root.glob(f"{sub}/**/*counter_collection.csv"))
+        if not files:
+            continue
+        rows = [r for r in _read_csv(files[0]) if r["Counter_Name"] == counter]
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        # calibration: the COPY_CAL_BYTES device copies are the largest copy dispatches
+        copies = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        big = [v for v in copies if copies and v >= 0.5 * max(copies)]
+        measured = sum(big) / len(big) if big else float("nan")
+        factor = (COPY_CAL_BYTES / 1024) / measured if big else float("nan")
+        # GEMV dispatches in probe order: consecutive runs of one (kernel, grid)
+        runs = []
+        for r in rows:
+            if "copyBuffer" in r["Kernel_Name"]:
+                continue
+            key = (r["Kernel_Name"], r["Grid_Size"])
+            if not runs or runs[-1][0] != key:
+                runs.append((key, []))
+            runs[-1][1].append(float(r["Counter_Value"]))
+        out.append(f"## {counter} per dispatch, rocprofv3 --pmc {counter}\n")
+        out.append(f"Calibration: a {COPY_CAL_BYTES >> 20} MiB device-to-device copy (reads and "
+                   f"writes {COPY_CAL_BYTES >> 10} KiB) counts {measured:.0f} KiB per dispatch on "
+                   f"this counter; scale factor {factor:.4f}.\n")
+        out.append("| workload | kernel | grid | dispatches | KiB/dispatch | calibrated bytes |")
+        out.append("|---|---|---|---|---|---|")
+        for i, ((k, g), vs) in enumerate(runs):
+            name = GEMV_WORKLOADS[i][0] if i < len(GEMV_WORKLOADS) else f"run{i}"
+            avg = sum(vs) / len(vs)
+            cb = avg * 1024 * factor
+            per_workload.setdefault(name, {})[counter] = cb
+            out.append(f"| {name} | {k} | {g} | {len(vs)} | {avg:.1f} | {cb:.0f} |")
+        out.append("")
+    if per_workload:
+        out.append("## HBM traffic per launch vs algorithmic bytes\n")
+        out.append("```")
+        out.append("# workload fetch_bytes write_bytes  (calibrated FETCH_SIZE, WRITE_SIZE)")
+        for name, fmt, M, K, cfg in GEMV_WORKLOADS:
+            if name in per_workload:
+                v = per_workload[name]
+                out.append(f"{name} {v.get('FETCH_SIZE', 0):.0f} {v.get('WRITE_SIZE', 0):.0f}")
+        out.append("```\n")
+        out.append("| workload | algorithmic bytes | measured bytes | ratio |")
+        out.append("|---|---|---|---|")
+        for name, fmt, M, K, cfg in GEMV_WORKLOADS:
+            if name in per_workload:
+                v = per_workload[name]
+                tot = v.get("FETCH_SIZE", 0) + v.get("WRITE_SIZE", 0)
+                alg = algorithmic_bytes(fmt, M, K)
+                out.append(f"| {name} | {alg} | {tot:.0f} | {tot / alg:.3f} |")
+        out.append("")
+    return "\n".join(out)
+
 
 
 def main() -> int:
@@ -172,7 +306,14 @@ def main() -> int:
                     help="comma list of workload names, or 'all' / 'headline'")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter-collection driver for rocprofv3 --pmc (no JSON line)")
+    ap.add_argument("--summarize", metavar="DIR",
+                    help="print a markdown summary of a rocprofv3 output tree and exit")
     args = ap.parse_args()
+    if args.summarize:
+        print(summarize(Path(args.summarize)))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not built)"}))
@@ -192,6 +333,9 @@ def main() -> int:
         todo = [w for w in GEMV_WORKLOADS if w[0] in names]
         if head not in todo:
             todo = [head] + todo
+    if args.probe:
+        probe(ctx, todo, args.steps)
+        return 0
     results = {}
     for name, fmt, M, K, cfg in todo:
         log(f"{name}: running")

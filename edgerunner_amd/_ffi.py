@@ -73,6 +73,7 @@ SIGNATURES = {
     "er_hip_free": (C.c_int, [_ctx_p, er_buffer]),
     "er_hip_upload": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, C.c_void_p, _u64]),
     "er_hip_download": (C.c_int, [_ctx_p, _stream, C.c_void_p, er_buffer, _u64, _u64]),
+    "er_hip_copy": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, er_buffer, _u64, _u64]),
     "er_hip_stream_create": (C.c_int, [_ctx_p, C.POINTER(_stream)]),
     "er_hip_stream_destroy": (C.c_int, [_ctx_p, _stream]),
     "er_hip_synchronize": (C.c_int, [_ctx_p, _stream]),

@@ -490,6 +490,24 @@ er_status er_hip_download(er_hip_ctx *ctx, er_stream stream, void *dst, er_buffe
     return ER_OK;
 }
 
+er_status er_hip_copy(er_hip_ctx *ctx, er_stream stream, er_buffer dst, uint64_t dst_offset,
+                      er_buffer src, uint64_t src_offset, uint64_t bytes) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (dst_offset > dst.length || bytes > dst.length - dst_offset || src_offset > src.length ||
+        bytes > src.length - src_offset)
+        return fail(ER_ERR_INVALID_ARGUMENT, "copy of %llu bytes overruns a buffer",
+                    (unsigned long long)bytes);
+    if (bytes == 0) return ER_OK;
+    if (!dst.data || !src.data) return fail(ER_ERR_INVALID_ARGUMENT, "copy: null pointer");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    hipError_t e = hipMemcpyAsync((char *)dst.data + dst_offset, (const char *)src.data + src_offset,
+                                  bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "copy: %s", hipGetErrorString(e));
+    return ER_OK;
+}
+
 er_status er_hip_stream_create(er_hip_ctx *ctx, er_stream *out) {
     er_status st = check_ctx(ctx);
     if (st != ER_OK) return st;

@@ -131,6 +131,13 @@ class Buffer:
                                            out.nbytes))
         return out
 
+    def copy_from(self, src: "Buffer", nbytes: Optional[int] = None, dst_offset: int = 0,
+                  src_offset: int = 0, stream: "Optional[Stream]" = None) -> None:
+        """Device-to-device copy enqueued on `stream`."""
+        n = src.length - src_offset if nbytes is None else nbytes
+        check(self.ctx.lib.er_hip_copy(self.ctx.handle, _sh(stream), self.raw, dst_offset, src.raw,
+                                       src_offset, n))
+
     def free(self) -> None:
         if self.owned and self.raw.data:
             check(self.ctx.lib.er_hip_free(self.ctx.handle, self.raw))

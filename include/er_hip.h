@@ -120,6 +120,9 @@ er_status er_hip_upload(er_hip_ctx *ctx, er_stream stream, er_buffer dst, uint64
                         const void *src, uint64_t bytes);
 er_status er_hip_download(er_hip_ctx *ctx, er_stream stream, void *dst, er_buffer src,
                           uint64_t src_offset, uint64_t bytes);
+/* Device-to-device copy enqueued on `stream` (MTLBlitCommandEncoder.copy analogue). */
+er_status er_hip_copy(er_hip_ctx *ctx, er_stream stream, er_buffer dst, uint64_t dst_offset,
+                      er_buffer src, uint64_t src_offset, uint64_t bytes);
 
 /* ---- streams and events (command buffer commit / completed; GPU timing as in
  * Gemma4LanguageModel.RuntimeProfiler, Gemma4LanguageModel.swift:135-200) ---- */
