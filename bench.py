@@ -52,6 +52,16 @@ GEMV_WORKLOADS = [
 ]
 
 
+# (name, fmt, T tokens, N, K, BASELINE config index)
+GEMM_WORKLOADS = [
+    ("q4_k_gemm_512x4096x4096", "q4_k", 512, 4096, 4096, 4),
+    ("q4_k_gemm_512x14336x4096", "q4_k", 512, 14336, 4096, 4),
+    ("q8_0_gemm_512x4096x4096", "q8_0", 512, 4096, 4096, 4),
+    ("q8_0_gemm_512x14336x4096", "q8_0", 512, 14336, 4096, 4),
+]
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -122,6 +132,52 @@ def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int)
         "us_per_call_eager": eager_us,
         "ms_total": ms, "y_finite": bool(np.all(np.isfinite(y))),
     }
+
+
+def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
+    """Prefill GEMM: `steps` launches over rotating weight copies, recorded
+    into a HIP graph and replayed between HIP events (as bench_gemv)."""
+    import edgerunner_amd.synth as synth
+    from edgerunner_amd import Capture, QuantGEMMKernel
+
+    gemm = QuantGEMMKernel(ctx)
+    W = synth.weights(fmt, synth.seed(cfg, 0), N, K, **DSCALE[fmt])
+    X = synth.normal_bf16(synth.seed(cfg, 1), T * K)
+    copies = max(2, -(-ROTATE_BYTES // W.nbytes))
+    stream = ctx.stream()
+    wbufs = [ctx.upload(W, stream) for _ in range(copies)]
+    xb = ctx.upload(X, stream)
+    yb = ctx.alloc(4 * T * N)
+    enc = gemm.encodeQ4K if fmt == "q4_k" else gemm.encodeQ8_0
+    for i in range(warmup):
+        enc(stream, wbufs[i % copies], xb, yb, T, N, K)
+    stream.synchronize()
+    with Capture(ctx, stream) as cap:
+        for i in range(steps):
+            enc(stream, wbufs[i % copies], xb, yb, T, N, K)
+    graph = cap.graph
+    graph.launch(stream)
+    stream.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record(stream)
+    graph.launch(stream)
+    e1.record(stream)
+    stream.synchronize()
+    us = e0.elapsed_ms(e1) * 1000.0 / steps
+    y = yb.download(np.float32, count=min(T * N, 1 << 20), stream=stream)
+    graph.destroy()
+    for b in wbufs:
+        b.free()
+    xb.free()
+    yb.free()
+    e0.destroy()
+    e1.destroy()
+    stream.destroy()
+    flops = 2.0 * T * N * K
+    tflops = flops / (us * 1e-6) / 1e12
+    return {"fmt": fmt, "T": T, "N": N, "K": K, "us_per_call": us, "TFLOPs": tflops,
+            "frac_of_mfma_bf16_peak": tflops / MFMA_BF16_PEAK_TFLOPS,
+            "min_bytes": W.nbytes + 2 * T * K + 4 * T * N, "y_finite": bool(np.all(np.isfinite(y)))}
 
 
 def cpu_baseline(fmt: str, M: int, K: int, cfg: int, budget_s: float) -> dict:
@@ -343,6 +399,15 @@ def main() -> int:
         results[name] = r
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
             f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s); eager {r['us_per_call_eager']:.2f} us")
+
+    for name, fmt, T, N, K, cfg in GEMM_WORKLOADS:
+        if args.workloads not in ("all",) and name not in args.workloads.split(","):
+            continue
+        log(f"{name}: running")
+        r = bench_gemm(ctx, fmt, T, N, K, cfg, max(20, args.steps // 4), min(args.warmup, 5))
+        results[name] = r
+        log(f"{name}: {r['us_per_call']:.2f} us/call, {r['TFLOPs']:.1f} TFLOP/s "
+            f"({100 * r['frac_of_mfma_bf16_peak']:.1f}% of bf16 dense peak)")
 
     h = results[head[0]]
     cpu = None

@@ -97,6 +97,8 @@ SIGNATURES = {
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
     "er_hip_encode_batched_q8_0_weights": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
+    "er_hip_gemm_q4_k": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
+    "er_hip_gemm_q8_0": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
     "er_hip_encode_projection": (
         C.c_int, [_ctx_p, _stream, C.POINTER(er_tensor_storage), er_buffer, er_buffer, _u32]),
 }

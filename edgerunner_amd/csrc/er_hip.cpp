@@ -54,7 +54,11 @@ er_status fail(er_status st, const char *fmt, ...) {
     X(GEMV_Q6K_L4_G, "er_gemv_q6k_l4_g")                                               \
     X(GEMV_Q4K_L64_G, "er_gemv_q4k_l64_g")                                             \
     X(GEMV_Q8_0_L64_G, "er_gemv_q8_0_l64_g")                                           \
-    X(GEMV_Q8_0_ANY, "er_gemv_q8_0_any")
+    X(GEMV_Q8_0_ANY, "er_gemv_q8_0_any")                                               \
+    X(GEMM_Q4K_T128, "er_gemm_q4k_t128")                                               \
+    X(GEMM_Q4K_T256, "er_gemm_q4k_t256")                                               \
+    X(GEMM_Q8_0_T128, "er_gemm_q8_0_t128")                                             \
+    X(GEMM_Q8_0_T256, "er_gemm_q8_0_t256")
 
 enum KernelId {
 #define ER_ENUM(id, name) K_##id,
@@ -282,6 +286,42 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / lpr) * kQ6KRows;
     dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
     return launch(ctx, k, grid, dim3(kGemvThreads, 1, 1), lds, stream, args);
+}
+
+// Prefill GEMM: validation mirrors the GEMV rules (K multiple of the block,
+// buffer lengths), then a grid of ceil(N/128) x ceil(T/TT) workgroups.
+er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_buffer x,
+                      er_buffer y, uint32_t T, uint32_t N, uint32_t K) {
+    const uint32_t kmul = f == Fmt::Q4_K ? 256u : 64u;
+    if (K == 0 || K % kmul != 0)
+        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s GEMM: K=%u must be a positive multiple of %u",
+                    fmt_name(f), K, kmul);
+    const uint64_t need = (uint64_t)N * (K / block_weights(f)) * block_bytes(f);
+    if (W.length < need)
+        return fail(ER_ERR_INVALID_MATRIX_SHAPE, "%s GEMM: weight buffer holds %llu bytes, N=%u K=%u needs %llu",
+                    fmt_name(f), (unsigned long long)W.length, N, K, (unsigned long long)need);
+    if (T == 0) return fail(ER_ERR_ENCODING_FAILED, "%s GEMM: tokens must be > 0", fmt_name(f));
+    if (x.length < (uint64_t)T * K * 2u || y.length < (uint64_t)T * N * 4u)
+        return fail(ER_ERR_ENCODING_FAILED, "%s GEMM: x %llu B / y %llu B too small for T=%u N=%u K=%u",
+                    fmt_name(f), (unsigned long long)x.length, (unsigned long long)y.length, T, N, K);
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK || N == 0) return st;
+    if (!W.data || !x.data || !y.data) return fail(ER_ERR_INVALID_ARGUMENT, "GEMM: null buffer");
+    if (!aligned(W.data, 16) || !aligned(x.data, 16) || !aligned(y.data, 4))
+        return fail(ER_ERR_INVALID_ARGUMENT, "GEMM: weight and x must be 16-byte, y 4-byte aligned");
+    if ((T + 127u) / 128u > 65535u)
+        return fail(ER_ERR_ENCODING_FAILED, "GEMM: %u tokens exceed the grid limit", T);
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    // 256-token tiles halve the weight re-reads but need enough workgroups to fill the CUs
+    const uint64_t wg256 = (uint64_t)((N + 127u) / 128u) * ((T + 255u) / 256u);
+    const bool big = T >= 256u && wg256 >= (uint64_t)ctx->cu_count;
+    const uint32_t TT = big ? 256u : 128u;
+    const KernelId k = f == Fmt::Q4_K ? (big ? K_GEMM_Q4K_T256 : K_GEMM_Q4K_T128)
+                                      : (big ? K_GEMM_Q8_0_T256 : K_GEMM_Q8_0_T128);
+    dim3 grid((N + 127u) / 128u, (T + TT - 1u) / TT, 1);
+    void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K};
+    return launch(ctx, k, grid, dim3(256, 1, 1), 0, stream, args);
 }
 
 er_status encode_dequant(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer blocks,
@@ -676,6 +716,16 @@ er_status er_hip_encode_batched_q8_0_weights(er_hip_ctx *ctx, er_stream stream, 
                                              er_buffer input, er_buffer output, uint32_t batch_seq,
                                              uint32_t M, uint32_t K) {
     return encode_gemv(ctx, stream, Fmt::Q8_0, weight, input, output, batch_seq, M, K);
+}
+
+er_status er_hip_gemm_q4_k(er_hip_ctx *ctx, er_stream stream, er_buffer weight, er_buffer x_bf16,
+                           er_buffer y, uint32_t tokens, uint32_t N, uint32_t K) {
+    return encode_gemm(ctx, stream, Fmt::Q4_K, weight, x_bf16, y, tokens, N, K);
+}
+
+er_status er_hip_gemm_q8_0(er_hip_ctx *ctx, er_stream stream, er_buffer weight, er_buffer x_bf16,
+                           er_buffer y, uint32_t tokens, uint32_t N, uint32_t K) {
+    return encode_gemm(ctx, stream, Fmt::Q8_0, weight, x_bf16, y, tokens, N, K);
 }
 
 er_status er_hip_encode_projection(er_hip_ctx *ctx, er_stream stream,

@@ -3,3 +3,4 @@
 // host library embeds and loads with hipModuleLoadData.
 #include "er_dequant.hip"
 #include "er_gemv.hip"
+#include "er_gemm.hip"

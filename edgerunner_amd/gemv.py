@@ -201,3 +201,45 @@ class DequantQ6KKernel(_DequantKernel):
     block_bytes = Q6_K_BLOCK_BYTES
     weights_per_block = 256
     entry = "er_hip_dequant_q6_k"
+
+
+class QuantGEMMKernel:
+    """Prefill GEMM over raw Q4_K / Q8_0 weights on the matrix cores.
+
+    The reference has no quantised GEMM (its prefill is the token-batched
+    GEMV, Dequant_Q8_0.metal:143-197); this class keeps the GEMVKernel style:
+    encode* appends to a stream, execute* allocates, runs, waits and copies out.
+    X is bf16 bits (uint16) [tokens][K]; Y is fp32 [tokens][N]."""
+
+    def __init__(self, ctx: Optional[Context] = None):
+        self.ctx = ctx or default_context()
+        self.lib = self.ctx.lib
+
+    def encodeQ4K(self, stream: Optional[Stream], weightBuffer: Buffer, inputBuffer: Buffer,
+                  outputBuffer: Buffer, tokens: int, N: int, K: int) -> None:
+        check(self.lib.er_hip_gemm_q4_k(self.ctx.handle, _sh(stream), weightBuffer.raw,
+                                        inputBuffer.raw, outputBuffer.raw, tokens, N, K))
+
+    def encodeQ8_0(self, stream: Optional[Stream], weightBuffer: Buffer, inputBuffer: Buffer,
+                   outputBuffer: Buffer, tokens: int, N: int, K: int) -> None:
+        check(self.lib.er_hip_gemm_q8_0(self.ctx.handle, _sh(stream), weightBuffer.raw,
+                                        inputBuffer.raw, outputBuffer.raw, tokens, N, K))
+
+    def execute(self, fmt: str, rawWeights, X_bf16, tokens: int, N: int, K: int) -> np.ndarray:
+        enc = {"q4_k": self.encodeQ4K, "q8_0": self.encodeQ8_0}[fmt]
+        w = _u8(rawWeights)
+        x = np.ascontiguousarray(X_bf16, dtype=np.uint16).reshape(-1)
+        if x.size != tokens * K:
+            raise InvalidVectorShape(f"X holds {x.size} values, tokens*K = {tokens * K}")
+        ctx = self.ctx
+        wb = ctx.upload(w) if w.size else ctx.alloc(0)
+        xb = ctx.upload(x)
+        yb = ctx.alloc(tokens * N * 4)
+        try:
+            enc(None, wb, xb, yb, tokens, N, K)
+            ctx.synchronize()
+            return yb.download(np.float32, tokens * N).reshape(tokens, N)
+        finally:
+            wb.free()
+            xb.free()
+            yb.free()

@@ -195,6 +195,21 @@ er_status er_hip_encode_batched_q8_0_weights(er_hip_ctx *ctx, er_stream stream, 
                                              er_buffer input, er_buffer output, uint32_t batch_seq,
                                              uint32_t M, uint32_t K);
 
+/* ---- prefill GEMM on the matrix cores: Y[t][n] = sum_k X[t][k] * W[n][k] ----
+ * X is bf16 [tokens][K] (16-byte aligned), W the raw Q4_K / Q8_0 rows of an
+ * [K, N] tensor, Y fp32 [tokens][N].  The reference has no quantised GEMM: its
+ * prefill is the token-batched GEMV (dequant_q8_0_gemv_batched,
+ * Dequant_Q8_0.metal:143-197; per-token GEMV loop, LlamaLanguageModel.swift:2552-2617)
+ * and these entry points compute the same product with the weights
+ * dequantised to bf16 tiles and multiplied with fp32 accumulation.
+ * Validation: tokens >= 1; Q4_K K % 256 == 0, Q8_0 K % 64 == 0, else
+ * INVALID_VECTOR_SHAPE; weight too short -> INVALID_MATRIX_SHAPE; x shorter
+ * than tokens*K*2 or y shorter than tokens*N*4 -> ENCODING_FAILED. */
+er_status er_hip_gemm_q4_k(er_hip_ctx *ctx, er_stream stream, er_buffer weight, er_buffer x_bf16,
+                           er_buffer y, uint32_t tokens, uint32_t N, uint32_t K);
+er_status er_hip_gemm_q8_0(er_hip_ctx *ctx, er_stream stream, er_buffer weight, er_buffer x_bf16,
+                           er_buffer y, uint32_t tokens, uint32_t N, uint32_t K);
+
 /* ---- projection by tensor descriptor (Gemma4LanguageModel.encodeProjection,
  * Sources/EdgeRunner/Models/Gemma4LanguageModel.swift:4207-4285): dispatches on
  * tensor->data_type (Q8_0, Q4_K, Q6_K); shape = [K, M]; tokens >= 1 selects the

@@ -1,0 +1,107 @@
+"""Prefill GEMM parity: Y = X (bf16) . W^T over raw Q4_K / Q8_0 weights on the
+matrix cores.  Bars: relative L2 <= 1e-2 against the CPU oracle (per-token GEMV
+on bf16-widened X; the north-star bound for bf16-MFMA GEMM), and <= 1e-5
+against a float64 product of X and the bf16-rounded dequantised weights --
+the kernel's own arithmetic, which pins the MFMA operand and accumulator
+layouts exactly."""
+import numpy as np
+import pytest
+
+import edgerunner_amd.synth as synth
+from edgerunner_amd import EncodingFailed, InvalidMatrixShape, InvalidVectorShape, QuantGEMMKernel
+from oracle import ref
+from oracle import restate_np as rn
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+DSCALE = {"q8_0": {"dscale": 0.02}, "q4_k": {"dscale": 0.01, "dminscale": 0.01}}
+
+
+def bf16_round(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return (u.astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_to_f32(x):
+    return (np.asarray(x, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.fixture(scope="module")
+def gemm(ctx):
+    return QuantGEMMKernel(ctx)
+
+
+def case(fmt, T, N, K, seed):
+    W = synth.weights(fmt, synth.seed(40 + seed, 0), N, K, **DSCALE[fmt])
+    X = synth.normal_bf16(synth.seed(40 + seed, 1), T * K)
+    return W, X
+
+
+def check(gemm, fmt, T, N, K, seed=0, rows=None):
+    W, X = case(fmt, T, N, K, seed)
+    Y = gemm.execute(fmt, W, X, T, N, K)
+    Wd = rn.weights_f32(fmt, W, N, K)
+    Xf = bf16_to_f32(X).reshape(T, K)
+    sel = np.arange(T) if rows is None else np.asarray(rows)
+    exact = Xf[sel].astype(np.float64) @ bf16_round(Wd).astype(np.float64).T
+    assert rel_l2(Y[sel], exact) < 1e-5, "kernel arithmetic (bf16 W, fp32 sums)"
+    oracle = np.stack([ref.gemv(fmt, W, Xf[t], N, K) for t in sel])
+    err = rel_l2(Y[sel], oracle)
+    print(f"{fmt} T={T} N={N} K={K}: rel_l2 vs oracle {err:.2e}")
+    assert err < 1e-2
+    return Y
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("T,N,K", [(128, 128, 256), (1, 128, 512), (37, 100, 1024), (200, 300, 768),
+                                   (256, 256, 2048), (300, 130, 1280)])
+def test_shapes(gemm, fmt, T, N, K):
+    if fmt == "q4_k" and K % 256:
+        pytest.skip("Q4_K needs K % 256 == 0")
+    check(gemm, fmt, T, N, K)
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+def test_q8_0_small_k(gemm, fmt):
+    if fmt == "q8_0":
+        check(gemm, fmt, 64, 96, 64)
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("N", [4096, 14336])
+def test_baseline_shapes_sampled(gemm, fmt, N):
+    """T = 512 tokens, K = 4096; every column of a sample of
+    token rows (first, last, tile edges, seeded random) against the oracle."""
+    T, K = 512, 4096
+    rng = np.random.default_rng(N)
+    rows = sorted(set([0, 1, 127, 128, 255, 256, 511]) | set(rng.integers(0, T, 9).tolist()))
+    check(gemm, fmt, T, N, K, seed=1, rows=rows)
+
+
+def test_one_hot_tokens_extract_weight_rows(gemm):
+    """X = identity rows: Y[t] is column t of the dequantised (bf16-rounded) W."""
+    T, N, K = 256, 64, 256
+    W = synth.q4_k(synth.seed(45, 0), N, K)
+    eye = np.zeros((T, K), np.float32)
+    eye[np.arange(T), np.arange(T)] = 1.0
+    X = (eye.view(np.uint32) >> 16).astype(np.uint16)
+    Y = gemm.execute("q4_k", W, X, T, N, K)
+    Wd = bf16_round(rn.weights_f32("q4_k", W, N, K))
+    assert np.array_equal(Y, Wd.T)
+
+
+def test_validation(ctx, gemm):
+    N, K, T = 8, 512, 4
+    W = synth.q4_k(1, N, K)
+    X = synth.normal_bf16(2, T * K)
+    with pytest.raises(InvalidVectorShape):
+        gemm.execute("q4_k", W, synth.normal_bf16(2, T * 384), T, N, 384)
+    with pytest.raises(InvalidMatrixShape):
+        gemm.execute("q4_k", W[:-1], X, T, N, K)
+    wb, xb, yb = ctx.upload(W), ctx.upload(X), ctx.alloc(T * N * 4 - 4)
+    with pytest.raises(EncodingFailed):
+        gemm.encodeQ4K(None, wb, xb, yb, T, N, K)
+    with pytest.raises(InvalidVectorShape):
+        gemm.encodeQ8_0(None, wb, xb, ctx.alloc(T * N * 4), T, N, 96)
