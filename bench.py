@@ -377,7 +377,8 @@ def main() -> int:
 
     from edgerunner_amd import Context
     ctx = Context(0)
-    log(f"device {ctx.info.name.decode()} arch={ctx.arch} CUs={ctx.compute_units}")
+    log(f"device {ctx.info.name.decode()} arch={ctx.arch} CUs={ctx.compute_units} "
+        f"LDS/workgroup={ctx.info.lds_per_workgroup} clock={ctx.info.clock_khz} kHz")
 
     head = GEMV_WORKLOADS[0]
     if args.workloads == "all":

@@ -49,6 +49,7 @@ class er_device_info(C.Structure):
         ("memory_clock_khz", C.c_int),
         ("memory_bus_width", C.c_int),
         ("total_memory", C.c_uint64),
+        ("lds_per_workgroup", C.c_uint64),
         ("name", C.c_char * 64),
         ("arch", C.c_char * 64),
     ]

@@ -78,9 +78,12 @@ ER_DEV void dequant_w(const WRaw &r, uint32_t chunk, uint32_t h, uint32_t (&out)
         const float sL = d * ub0(sc2), mL = dmin * ub0(m2);
         const float sH = d * ub1(sc2), mH = dmin * ub1(m2);
         const uint32_t qw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+        // the nibble mask lives in a register so each masked byte converts with
+        // one v_cvt_f32_ubyteN instead of a bit-field extract and a convert
+        const uint32_t M0F = vreg_const(0x0f0f0f0fu);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const uint32_t lo = qw[k] & 0x0f0f0f0fu, hi = (qw[k] >> 4) & 0x0f0f0f0fu;
+            const uint32_t lo = qw[k] & M0F, hi = (qw[k] >> 4) & M0F;
             out[2 * k + 0] = pack_bf16x2(__builtin_fmaf(sL, ub0(lo), -mL), __builtin_fmaf(sL, ub1(lo), -mL));
             out[2 * k + 1] = pack_bf16x2(__builtin_fmaf(sL, ub2(lo), -mL), __builtin_fmaf(sL, ub3(lo), -mL));
             out[8 + 2 * k + 0] = pack_bf16x2(__builtin_fmaf(sH, ub0(hi), -mH), __builtin_fmaf(sH, ub1(hi), -mH));
@@ -213,3 +216,172 @@ ER_GEMM_ENTRY(q4k, true, 128)
 ER_GEMM_ENTRY(q4k, true, 256)
 ER_GEMM_ENTRY(q8_0, false, 128)
 ER_GEMM_ENTRY(q8_0, false, 256)
+
+// ---------------------------------------------------------------------------
+// Pipelined variant: two LDS stages and one register stage, so the global
+// loads of chunk c+2 are in flight while the MFMAs of chunk c run; one
+// barrier per chunk.  Tiles are walked XCD-major: workgroup L runs on XCD
+// L % 8 (round-robin dispatch) and takes tile (L % 8) * per + L / 8 of the
+// (N-tile major, token-tile minor) order, so each XCD's L2 keeps a contiguous
+// slice of W while it sweeps the token tiles.
+// ---------------------------------------------------------------------------
+template <bool Q4K, int TT>
+ER_DEV void gemm_q_pipe(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X,
+                        float *__restrict__ Y, uint32_t T, uint32_t N, uint32_t K, uint32_t SK) {
+    constexpr int WT = TT / 2;
+    constexpr int AI = WT / 32;
+    constexpr int XLOADS = TT * ER_GEMM_KC * 2 / 16 / 256;
+    constexpr int ASZ = TT * ER_GEMM_PITCH, BSZ = ER_GEMM_TN * ER_GEMM_PITCH;
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];  // 2 x (A stage + B stage)
+
+    const uint32_t nT = (T + TT - 1) / TT, nN = (N + ER_GEMM_TN - 1) / ER_GEMM_TN;
+    const uint32_t total = nT * nN * SK, per = (total + 7u) / 8u;
+    const uint32_t L = blockIdx.x;
+    const uint32_t item = (L % 8u) * per + L / 8u;  // (N tile, K split, token tile), token tile fastest
+    if (item >= total) return;
+    const uint32_t tt = item % nT, rest = item / nT;
+    const uint32_t ks0 = rest % SK, nt = rest / SK;
+    const uint32_t n0 = nt * ER_GEMM_TN, t0 = tt * TT;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const size_t rowBytes = Q4K ? (size_t)(K >> 8) * 144u : (size_t)(K >> 6) * 68u;
+    const uint32_t NCall = K / ER_GEMM_KC;
+    const uint32_t cBeg = (uint32_t)(((uint64_t)NCall * ks0) / SK);
+    const uint32_t NC = (uint32_t)(((uint64_t)NCall * (ks0 + 1u)) / SK) - cBeg;
+    const uint32_t wRow = min(n0 + (tid >> 1), N - 1u), wh = tid & 1u;
+    auto load_x = [&](uint32_t chunk, u32x4 (&xr)[XLOADS]) {
+#pragma unroll
+        for (int q = 0; q < XLOADS; ++q) {
+            const uint32_t p = tid + 256u * q;
+            const uint32_t row = min(t0 + (p >> 3), T - 1u);
+            xr[q] = *(const u32x4 *)(X + (size_t)row * K + chunk * ER_GEMM_KC + 8u * (p & 7u));
+        }
+    };
+    auto store_stage = [&](uint32_t stage, uint32_t chunk, const WRaw &wr, const u32x4 (&xr)[XLOADS]) {
+        uint16_t *As = smem + stage * (ASZ + BSZ);
+        uint16_t *Bs = As + ASZ;
+        uint32_t wd[16];
+        dequant_w<Q4K>(wr, chunk, wh, wd);
+        uint16_t *brow = Bs + (tid >> 1) * ER_GEMM_PITCH;
+        if (Q4K) {
+            *(u32x4 *)(brow + 16u * wh) = u32x4{wd[0], wd[1], wd[2], wd[3]};
+            *(u32x4 *)(brow + 16u * wh + 8u) = u32x4{wd[4], wd[5], wd[6], wd[7]};
+            *(u32x4 *)(brow + 32u + 16u * wh) = u32x4{wd[8], wd[9], wd[10], wd[11]};
+            *(u32x4 *)(brow + 32u + 16u * wh + 8u) = u32x4{wd[12], wd[13], wd[14], wd[15]};
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *(u32x4 *)(brow + 32u * wh + 8u * q) = u32x4{wd[4 * q], wd[4 * q + 1], wd[4 * q + 2], wd[4 * q + 3]};
+        }
+#pragma unroll
+        for (int q = 0; q < XLOADS; ++q) {
+            const uint32_t p = tid + 256u * q;
+            *(u32x4 *)(As + (p >> 3) * ER_GEMM_PITCH + 8u * (p & 7u)) = xr[q];
+        }
+    };
+
+    f32x16 acc[AI][2];
+#pragma unroll
+    for (int i = 0; i < AI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Register buffers rotate over 3 chunks: the global loads of chunk c+3
+    // are issued in iteration c, two iterations before they are stored to LDS.
+    WRaw wr[3];
+    u32x4 xr[3][XLOADS];
+    const uint32_t wt = wave >> 1, wn = wave & 1u;
+    auto mfma_stage = [&](uint32_t stage) {
+        const uint16_t *As = smem + stage * (ASZ + BSZ);
+        const uint16_t *Bs = As + ASZ;
+#pragma unroll
+        for (int ks = 0; ks < ER_GEMM_KC / 16; ++ks) {
+            const uint32_t kof = 16u * ks + 8u * (lane >> 5);
+            bf16x8 a[AI], b[2];
+#pragma unroll
+            for (int i = 0; i < AI; ++i)
+                a[i] = *(const bf16x8 *)(As + (wt * WT + 32u * i + (lane & 31u)) * ER_GEMM_PITCH + kof);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *(const bf16x8 *)(Bs + (wn * 64u + 32u * j + (lane & 31u)) * ER_GEMM_PITCH + kof);
+#pragma unroll
+            for (int i = 0; i < AI; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    };
+    // chunk c's data sits in register buffer c % 3
+    load_w<Q4K>(W, rowBytes, wRow, cBeg, wh, wr[0]);
+    load_x(cBeg, xr[0]);
+    if (NC > 1) {
+        load_w<Q4K>(W, rowBytes, wRow, cBeg + 1, wh, wr[1]);
+        load_x(cBeg + 1, xr[1]);
+    }
+    if (NC > 2) {
+        load_w<Q4K>(W, rowBytes, wRow, cBeg + 2, wh, wr[2]);
+        load_x(cBeg + 2, xr[2]);
+    }
+    store_stage(0, cBeg, wr[0], xr[0]);
+    // iteration c: barrier; MFMAs of stage c%2 (issued first, so the dequant
+    // VALU work below overlaps them on the matrix pipe); store chunk c+1
+    // (buffer (c+1)%3) into stage (c+1)%2; load chunk c+3 into buffer c%3
+    // (free: chunk c was stored last iteration)
+#define ER_GEMM_STEP(B)                                                                  \
+    {                                                                                    \
+        const uint32_t c = c3 + (B);                                                     \
+        if (c < NC) {                                                                    \
+            __syncthreads();                                                             \
+            mfma_stage(c & 1u);                                                          \
+            if (c + 1 < NC) store_stage((c + 1) & 1u, cBeg + c + 1, wr[((B) + 1) % 3], xr[((B) + 1) % 3]); \
+            if (c + 3 < NC) {                                                            \
+                load_w<Q4K>(W, rowBytes, wRow, cBeg + c + 3, wh, wr[(B)]);               \
+                load_x(cBeg + c + 3, xr[(B)]);                                           \
+            }                                                                            \
+        }                                                                                \
+    }
+    for (uint32_t c3 = 0; c3 < NC; c3 += 3) {
+        ER_GEMM_STEP(0)
+        ER_GEMM_STEP(1)
+        ER_GEMM_STEP(2)
+    }
+#undef ER_GEMM_STEP
+#pragma unroll
+    for (int i = 0; i < AI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t n = n0 + wn * 64u + 32u * j + (lane & 31u);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t t = t0 + wt * WT + 32u * i + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3);
+                if (t < T && n < N) {
+                    if (SK == 1) Y[(size_t)t * N + n] = acc[i][j][r];
+                    else atomicAdd(Y + (size_t)t * N + n, acc[i][j][r]);  // Y zero-filled by er_fill_zero
+                }
+            }
+        }
+}
+
+// Zero fill for split-K accumulation (a kernel, so that it can be recorded in
+// a HIP graph; 16-byte stores, n4 float4 elements).
+extern "C" __global__ void __launch_bounds__(256) er_fill_zero(float4 *__restrict__ p, uint64_t n4) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n4; i += (uint64_t)gridDim.x * 256u)
+        p[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+#define ER_GEMMP_ENTRY(fmt, q4k, tt)                                                             \
+    extern "C" __global__ void __launch_bounds__(256)                                          \
+        er_gemmp_##fmt##_t##tt(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X,  \
+                               float *__restrict__ Y, uint32_t T, uint32_t N, uint32_t K,       \
+                               uint32_t SK) {                                                   \
+        gemm_q_pipe<q4k, tt>(W, X, Y, T, N, K, SK);                                             \
+    }
+
+ER_GEMMP_ENTRY(q4k, true, 64)
+ER_GEMMP_ENTRY(q8_0, false, 64)
+ER_GEMMP_ENTRY(q4k, true, 128)
+ER_GEMMP_ENTRY(q4k, true, 256)
+ER_GEMMP_ENTRY(q8_0, false, 128)
+ER_GEMMP_ENTRY(q8_0, false, 256)

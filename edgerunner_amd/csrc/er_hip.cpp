@@ -58,7 +58,14 @@ er_status fail(er_status st, const char *fmt, ...) {
     X(GEMM_Q4K_T128, "er_gemm_q4k_t128")                                               \
     X(GEMM_Q4K_T256, "er_gemm_q4k_t256")                                               \
     X(GEMM_Q8_0_T128, "er_gemm_q8_0_t128")                                             \
-    X(GEMM_Q8_0_T256, "er_gemm_q8_0_t256")
+    X(GEMM_Q8_0_T256, "er_gemm_q8_0_t256")                                             \
+    X(GEMMP_Q4K_T64, "er_gemmp_q4k_t64")                                               \
+    X(GEMMP_Q8_0_T64, "er_gemmp_q8_0_t64")                                             \
+    X(FILL_ZERO, "er_fill_zero")                                                       \
+    X(GEMMP_Q4K_T128, "er_gemmp_q4k_t128")                                             \
+    X(GEMMP_Q4K_T256, "er_gemmp_q4k_t256")                                             \
+    X(GEMMP_Q8_0_T128, "er_gemmp_q8_0_t128")                                           \
+    X(GEMMP_Q8_0_T256, "er_gemmp_q8_0_t256")
 
 enum KernelId {
 #define ER_ENUM(id, name) K_##id,
@@ -102,6 +109,8 @@ struct er_hip_ctx {
     hipFunction_t fnQ8I8[kI8Count] = {};
     int cu_count = 0;
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
+    int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1 selects the non-pipelined GEMM (benchmark comparison)
+    uint32_t gemm_tt = 0, gemm_sk = 0;  // ER_HIP_GEMM_TILE=tt:sk (benchmark sweeps only)
     er_device_info info{};
 };
 
@@ -313,15 +322,47 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
         return fail(ER_ERR_ENCODING_FAILED, "GEMM: %u tokens exceed the grid limit", T);
     st = bind_device(ctx);
     if (st != ER_OK) return st;
-    // 256-token tiles halve the weight re-reads but need enough workgroups to fill the CUs
-    const uint64_t wg256 = (uint64_t)((N + 127u) / 128u) * ((T + 255u) / 256u);
-    const bool big = T >= 256u && wg256 >= (uint64_t)ctx->cu_count;
-    const uint32_t TT = big ? 256u : 128u;
-    const KernelId k = f == Fmt::Q4_K ? (big ? K_GEMM_Q4K_T256 : K_GEMM_Q4K_T128)
-                                      : (big ? K_GEMM_Q8_0_T256 : K_GEMM_Q8_0_T128);
-    dim3 grid((N + 127u) / 128u, (T + TT - 1u) / TT, 1);
-    void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K};
-    return launch(ctx, k, grid, dim3(256, 1, 1), 0, stream, args);
+    // Tile height TT (tokens) and K split SK: 128-token tiles (64 for short
+    // inputs), then split K until the grid gives every CU a workgroup
+    // (measured on MI355X: 512x14336x4096 is fastest unsplit, 512x4096x4096
+    // with two K splits).
+    void *args1[] = {&W.data, &x.data, &y.data, &T, &N, &K};
+    const uint32_t nN = (N + 127u) / 128u;
+    uint32_t TT = T >= 128u ? 128u : 64u, SK = 1u;
+    const uint32_t NC = K / 64u;
+    while (SK < 8u && 2u * SK <= NC && (uint64_t)nN * ((T + TT - 1u) / TT) * SK < (uint64_t)ctx->cu_count)
+        SK *= 2u;
+    if (ctx->gemm_tt) TT = ctx->gemm_tt;
+    if (ctx->gemm_sk) SK = std::min<uint32_t>(ctx->gemm_sk, NC);
+    const uint32_t lds = 2u * (TT + 128u) * 72u * 2u;
+    if (ctx->gemm_variant == 1 || lds > ctx->info.lds_per_workgroup) {
+        // single-stage kernel (benchmark comparison, or two LDS stages do not fit)
+        const bool big = TT == 256u;
+        const uint32_t TT1 = big ? 256u : 128u;
+        const KernelId k = f == Fmt::Q4_K ? (big ? K_GEMM_Q4K_T256 : K_GEMM_Q4K_T128)
+                                          : (big ? K_GEMM_Q8_0_T256 : K_GEMM_Q8_0_T128);
+        dim3 grid((N + 127u) / 128u, (T + TT1 - 1u) / TT1, 1);
+        return launch(ctx, k, grid, dim3(256, 1, 1), 0, stream, args1);
+    }
+    if (SK > 1u) {
+        // split K accumulates with fp32 atomics into a zero-filled Y
+        uint64_t n4 = (uint64_t)T * N / 4u, tail = (uint64_t)T * N % 4u;
+        if (tail || !aligned(y.data, 16)) SK = 1u;
+        else {
+            void *zargs[] = {&y.data, &n4};
+            const uint64_t blocks = std::min<uint64_t>((n4 + 255u) / 256u, 4096u);
+            st = launch(ctx, K_FILL_ZERO, dim3((uint32_t)blocks, 1, 1), dim3(256, 1, 1), 0, stream, zargs);
+            if (st != ER_OK) return st;
+        }
+    }
+    KernelId k;
+    if (TT == 256u) k = f == Fmt::Q4_K ? K_GEMMP_Q4K_T256 : K_GEMMP_Q8_0_T256;
+    else if (TT == 128u) k = f == Fmt::Q4_K ? K_GEMMP_Q4K_T128 : K_GEMMP_Q8_0_T128;
+    else k = f == Fmt::Q4_K ? K_GEMMP_Q4K_T64 : K_GEMMP_Q8_0_T64;
+    const uint32_t items = nN * ((T + TT - 1u) / TT) * SK;
+    void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K, &SK};
+    dim3 grid(8u * ((items + 7u) / 8u), 1, 1);
+    return launch(ctx, k, grid, dim3(256, 1, 1), lds, stream, args);
 }
 
 er_status encode_dequant(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer blocks,
@@ -429,6 +470,14 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
             }
         }
     }
+    if (const char *gv = std::getenv("ER_HIP_GEMM_VARIANT")) ctx->gemm_variant = std::atoi(gv);
+    if (const char *gt = std::getenv("ER_HIP_GEMM_TILE")) {
+        unsigned a = 0, b = 0;
+        if (std::sscanf(gt, "%u:%u", &a, &b) == 2 && (a == 64 || a == 128 || a == 256) && b >= 1) {
+            ctx->gemm_tt = a;
+            ctx->gemm_sk = b;
+        }
+    }
     if (const char *ov = std::getenv("ER_HIP_GEMV_CONFIG")) {
         unsigned l = 0, n = 0, r = 0;
         if (std::sscanf(ov, "%u:%u:%u", &l, &n, &r) == 3)
@@ -442,6 +491,7 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
     info.memory_clock_khz = prop.memoryClockRate;
     info.memory_bus_width = prop.memoryBusWidth;
     info.total_memory = prop.totalGlobalMem;
+    info.lds_per_workgroup = prop.sharedMemPerBlock;
     std::snprintf(info.name, sizeof(info.name), "%.63s", prop.name);
     std::snprintf(info.arch, sizeof(info.arch), "%.63s", prop.gcnArchName);
     *out_ctx = ctx;

@@ -97,6 +97,7 @@ typedef struct er_device_info {
     int memory_clock_khz;
     int memory_bus_width;
     uint64_t total_memory;
+    uint64_t lds_per_workgroup; /* bytes of LDS one workgroup may allocate */
     char name[64];
     char arch[64];
 } er_device_info;
