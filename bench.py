@@ -180,6 +180,49 @@ def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warm
             "min_bytes": W.nbytes + 2 * T * K + 4 * T * N, "y_finite": bool(np.all(np.isfinite(y)))}
 
 
+def bench_chain(ctx, steps: int, warmup: int) -> dict:
+    """one decode step's projections (28 Qwen3-0.6B layers,
+    Q4_K_M mix, 151936-row Q6_K head), recorded into a HIP graph; `steps`
+    replays timed between HIP events, per-projection and fused forms."""
+    from edgerunner_amd.chain import ChainSpec, DecodeChain, make_inputs, make_weights
+
+    spec = ChainSpec()
+    stream = ctx.stream()
+    ch = DecodeChain(ctx, spec, make_weights(spec), make_inputs(spec), stream)
+    stream.synchronize()
+    out = {"weight_bytes_per_step": spec.weight_bytes()}
+    e0, e1 = ctx.event(), ctx.event()
+    for fused in (False, True):
+        for _ in range(warmup):
+            ch.encode(stream, fused)
+        g = ch.capture(stream, fused)
+        g.launch(stream)
+        stream.synchronize()
+        e0.record(stream)
+        for _ in range(steps):
+            g.launch(stream)
+        e1.record(stream)
+        stream.synchronize()
+        us = e0.elapsed_ms(e1) * 1000.0 / steps
+        e0.record(stream)
+        for _ in range(max(1, steps // 10)):
+            ch.encode(stream, fused)
+        e1.record(stream)
+        stream.synchronize()
+        eager = e0.elapsed_ms(e1) * 1000.0 / max(1, steps // 10)
+        g.destroy()
+        tag = "fused" if fused else "per_projection"
+        out[tag] = {"launches": spec.launches(fused), "us_per_step": us,
+                    "GBps": spec.weight_bytes() / (us * 1e-6) / 1e9,
+                    "frac_of_hbm_peak": spec.weight_bytes() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                    "us_per_step_eager": eager}
+    e0.destroy()
+    e1.destroy()
+    ch.free()
+    stream.destroy()
+    return out
+
+
 def cpu_baseline(fmt: str, M: int, K: int, cfg: int, budget_s: float) -> dict:
     """Times the CPU oracle (oracle/er_oracle.c, the reference's Swift CPU
     loop restated in C) on the same synthetic workload, all rows of the matrix,
@@ -353,6 +396,14 @@ def summarize(root: Path) -> str:
 
 
 
+def _rounded(v):
+    if isinstance(v, dict):
+        return {k: _rounded(x) for k, x in v.items()}
+    if isinstance(v, float):
+        return round(v, 4)
+    return v
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -410,6 +461,16 @@ def main() -> int:
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['TFLOPs']:.1f} TFLOP/s "
             f"({100 * r['frac_of_mfma_bf16_peak']:.1f}% of bf16 dense peak)")
 
+    if args.workloads in ("all", "chain") or "decode_chain" in args.workloads:
+        log("decode_chain: running")
+        r = bench_chain(ctx, max(20, args.steps // 4), 3)
+        results["decode_chain_qwen3_0.6b_q4km"] = r
+        for tag in ("per_projection", "fused"):
+            v = r[tag]
+            log(f"decode_chain {tag}: {v['launches']} launches, {v['us_per_step']:.1f} us/step, "
+                f"{v['GBps']:.0f} GB/s ({100 * v['frac_of_hbm_peak']:.1f}% of 8 TB/s); "
+                f"eager {v['us_per_step_eager']:.1f} us")
+
     h = results[head[0]]
     cpu = None
     if not args.no_cpu_baseline:
@@ -444,8 +505,7 @@ def main() -> int:
         },
         "cpu_baseline": ({k: (round(v, 3) if isinstance(v, float) else v)
                           for k, v in cpu.items() if k != "us_per_call"} if cpu else None),
-        "results": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
-                         for kk, vv in v.items()} for k, v in results.items()},
+        "results": _rounded(results),
     }
     print(json.dumps(out), flush=True)
     return 0

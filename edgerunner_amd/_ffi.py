@@ -92,6 +92,13 @@ SIGNATURES = {
     "er_hip_encode_q4k_weights": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
     "er_hip_encode_q6k_weights": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
     "er_hip_encode_q8_0_weights": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q4k_weights_dual": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q4k_weights_triple": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer,
+                  er_buffer, _u32, _u32, _u32, _u32]),
+    "er_hip_encode_q4k_weights_dual_geglu": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
     "er_hip_encode_batched_q4k_weights": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
     "er_hip_encode_batched_q6k_weights": (

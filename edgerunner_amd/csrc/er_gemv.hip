@@ -57,19 +57,85 @@ struct I8Cfg {
 // Q4_K slot s of a row = super-block s/4, sub-block pair p = s%4: header
 // (d, dmin, 12 scale bytes) + qs bytes [32p, 32p+32) = weights 64s..64s+63
 // (low nibbles: sub-block 2p, high nibbles: sub-block 2p+1).
-template <int LPR, int NS, int R>
-ER_DEV void gemv_q4k_i8(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                        float *__restrict__ y, uint32_t M, uint32_t K) {
+
+// Per-lane constants of pair p for the scale / min byte extraction:
+//   p < 2 : sc = s[2p..2p+1] & 63,   m = s[2p+4..2p+5] & 63
+//   p >= 2: sc = (s[q+8] & 15) | (s[q] >> 6) << 4,  m = (s[q+8] >> 4) | (s[q+4] >> 6) << 4,
+//           q = 2p - 4
+struct Q4Sel {
+    uint32_t sel1, sel2, maskLo, shM;
+};
+ER_DEV Q4Sel q4k_sel(uint32_t p) {
+    const bool lowp = p < 2u;
+    const uint32_t q4 = 2u * p - 4u;
+    Q4Sel c;
+    c.sel1 = lowp ? (0x0c0c0000u | ((2u * p + 1u) << 8) | (2u * p)) : (0x0c0c0000u | ((q4 + 5u) << 8) | (q4 + 4u));
+    c.sel2 = lowp ? 0x0c0c0c0cu : (0x0c0c0000u | ((q4 + 1u) << 8) | q4);
+    c.maskLo = lowp ? 0x3f3fu : 0x0f0fu;
+    c.shM = lowp ? 0u : 4u;
+    return c;
+}
+
+// Contribution of one slot (header h, qs qa|qb) against the staged x limbs xv
+// of the same 64 positions: (d * s_g) * sum(sc * q * xi) - dmin * sum(m * X_sub).
+ER_DEV float q4k_slot_dot(const u32x4 &h, const u32x4 &qa, const u32x4 &qb,
+                          const u32x4 (&xv)[ER_XL_PLANES][4], float XL, float XH, float sg, float live,
+                          const Q4Sel &c, uint32_t M0F) {
+    const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    // low nibbles: positions 4k..4k+3 of sub-block 2p (granule k/4);
+    // high nibbles: the same positions of sub-block 2p+1 (granule 2 + k/4)
+    int cL[ER_XL_PLANES] = {}, cH[ER_XL_PLANES] = {};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int lo = (int)(qw[k] & M0F);
+        const int hi = (int)((qw[k] >> 4) & M0F);
+#pragma unroll
+        for (int l = 0; l < ER_XL_PLANES; ++l) {
+            cL[l] = __builtin_amdgcn_sdot4(lo, (int)xv[l][k >> 2][k & 3], cL[l], false);
+            cH[l] = __builtin_amdgcn_sdot4(hi, (int)xv[l][2 + (k >> 2)][k & 3], cH[l], false);
+        }
+    }
+    const float T0 = xl_combine(cL[0], cL[1], cL[2]);
+    const float T1 = xl_combine(cH[0], cH[1], cH[2]);
+    // perm(S0, S1, sel): selector bytes 0-3 pick S1, 4-7 pick S0
+    const uint32_t X1 = __builtin_amdgcn_perm(h.w, h.y, c.sel1);
+    const uint32_t X2 = __builtin_amdgcn_perm(h.w, h.y, c.sel2);
+    const uint32_t sc = (X1 & c.maskLo) | ((X2 >> 2) & 0x3030u);
+    const uint32_t Y1 = __builtin_amdgcn_perm(h.w, h.z, c.sel1);
+    const uint32_t Y2 = __builtin_amdgcn_perm(h.w, h.z, c.sel2);
+    const uint32_t mm = ((Y1 >> c.shM) & c.maskLo) | ((Y2 >> 2) & 0x3030u);
+    const float d = f16_to_f32(h.x & 0xffffu), dmin = f16_to_f32(h.x >> 16);
+    const float sT = __builtin_fmaf(ub0(sc), T0, ub1(sc) * T1);
+    const float mX = __builtin_fmaf(ub0(mm), XL, ub1(mm) * XH);
+    return __builtin_fmaf(d * sg, sT, -(live * dmin) * mX);
+}
+
+// Output epilogues of the row-list kernel.
+#define ER_EPI_STORE 0  // every row r writes yrow[r]
+#define ER_EPI_GEGLU 1  // rows [0, R/2) are gate rows, [R/2, R) the matching up rows:
+                        // writes gelu_tanh(gate) * up to the gate row's output
+
+// GELU, tanh approximation, saturated outside [-10, 10] (as the reference's
+// q4_k_gelu_tanh, Dequant_Q4_K_M.metal:913-923).
+ER_DEV float gelu_tanh(float g) {
+    if (g > 10.0f) return g;
+    if (g < -10.0f) return 0.0f;
+    const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    return g * 0.5f * (1.0f + tanhf(inner));
+}
+
+// Integer-dot Q4_K GEMV over the R rows (given by pointer) of this thread's
+// lane group; x is staged by the whole workgroup.  Every lane of the
+// workgroup must call it (it contains a barrier).
+template <int LPR, int NS, int R, int EPI>
+ER_DEV void gemv_q4k_i8_core(const uint8_t *const (&rowp)[R], float *const (&yrow)[R], const bool (&rowLive)[R],
+                             const float *__restrict__ x, uint32_t K) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     using C = I8Cfg<LPR, NS>;
     constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
-    x += (size_t)blockIdx.y * K;
-    y += (size_t)blockIdx.y * M;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t g = lane / LPR, li = lane % LPR;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t li = lane % LPR;
     const uint32_t S = K >> 6;
-    const size_t rowBytes = (size_t)(K >> 8) * 144u;
-    const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
 
     float4 xr[C::XG][4];
     xl_load<C::XG, NT>(x, K, xr);
@@ -81,7 +147,7 @@ ER_DEV void gemv_q4k_i8(const uint8_t *__restrict__ W, const float *__restrict__
         const uint32_t p = s & 3u;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint8_t *bp = W + (size_t)min(row0 + (uint32_t)r, M - 1u) * rowBytes + (s >> 2) * 144u;
+            const uint8_t *bp = rowp[r] + (s >> 2) * 144u;
             hdr[j][r] = ld16_a16(bp);
             qa[j][r] = ld16_a16(bp + 16u + 32u * p);
             qb[j][r] = ld16_a16(bp + 32u + 32u * p);
@@ -102,64 +168,120 @@ ER_DEV void gemv_q4k_i8(const uint8_t *__restrict__ W, const float *__restrict__
         const uint32_t sRaw = li + (uint32_t)LPR * j;
         const uint32_t s = min(sRaw, S - 1u);
         const float live = sRaw < S ? 1.0f : 0.0f;
-        const uint32_t p = s & 3u;
         u32x4 xv[ER_XL_PLANES][4];
         xl_read_group(X, s, xv);
         const float4 c16 = *(const float4 *)__builtin_assume_aligned(X.x16 + 4u * s, 16);
         const float XL = c16.x + c16.y, XH = c16.z + c16.w;
         const float sg = live * X.sg64[s];
-        // scale / min bytes of the pair: for p < 2 sc = s[2p..2p+1] & 63 and
-        // m = s[2p+4..2p+5] & 63; for p >= 2 (q = 2p-4) sc = (s[q+8] & 15) |
-        // (s[q] >> 6) << 4 and m = (s[q+8] >> 4) | (s[q+4] >> 6) << 4.
-        const bool lowp = p < 2u;
-        const uint32_t q4 = 2u * p - 4u;
-        const uint32_t sel1 = lowp ? (0x0c0c0000u | ((2u * p + 1u) << 8) | (2u * p))
-                                   : (0x0c0c0000u | ((q4 + 5u) << 8) | (q4 + 4u));
-        const uint32_t sel2 = lowp ? 0x0c0c0c0cu : (0x0c0c0000u | ((q4 + 1u) << 8) | q4);
-        const uint32_t maskLo = lowp ? 0x3f3fu : 0x0f0fu;
-        const uint32_t shM = lowp ? 0u : 4u;
+        const Q4Sel sel = q4k_sel(s & 3u);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const u32x4 h = hdr[j][r];
-            const uint32_t qw[8] = {qa[j][r].x, qa[j][r].y, qa[j][r].z, qa[j][r].w,
-                                    qb[j][r].x, qb[j][r].y, qb[j][r].z, qb[j][r].w};
-            // low nibbles: positions 4k..4k+3 of sub-block 2p (granule k/4);
-            // high nibbles: the same positions of sub-block 2p+1 (granule 2 + k/4)
-            int cL[ER_XL_PLANES] = {}, cH[ER_XL_PLANES] = {};
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int lo = (int)(qw[k] & M0F);
-                const int hi = (int)((qw[k] >> 4) & M0F);
-#pragma unroll
-                for (int l = 0; l < ER_XL_PLANES; ++l) {
-                    cL[l] = __builtin_amdgcn_sdot4(lo, (int)xv[l][k >> 2][k & 3], cL[l], false);
-                    cH[l] = __builtin_amdgcn_sdot4(hi, (int)xv[l][2 + (k >> 2)][k & 3], cH[l], false);
-                }
-            }
-            const float T0 = xl_combine(cL[0], cL[1], cL[2]);
-            const float T1 = xl_combine(cH[0], cH[1], cH[2]);
-            // perm(S0, S1, sel): selector bytes 0-3 pick S1, 4-7 pick S0
-            const uint32_t X1 = __builtin_amdgcn_perm(h.w, h.y, sel1);
-            const uint32_t X2 = __builtin_amdgcn_perm(h.w, h.y, sel2);
-            const uint32_t sc = (X1 & maskLo) | ((X2 >> 2) & 0x3030u);
-            const uint32_t Y1 = __builtin_amdgcn_perm(h.w, h.z, sel1);
-            const uint32_t Y2 = __builtin_amdgcn_perm(h.w, h.z, sel2);
-            const uint32_t mm = ((Y1 >> shM) & maskLo) | ((Y2 >> 2) & 0x3030u);
-            const float d = f16_to_f32(h.x & 0xffffu), dmin = f16_to_f32(h.x >> 16);
-            const float sT = __builtin_fmaf(ub0(sc), T0, ub1(sc) * T1);
-            const float mX = __builtin_fmaf(ub0(mm), XL, ub1(mm) * XH);
-            float a = __builtin_fmaf(-(live * dmin), mX, acc[r]);
-            acc[r] = __builtin_fmaf(d * sg, sT, a);
+            acc[r] += q4k_slot_dot(hdr[j][r], qa[j][r], qb[j][r], xv, XL, XH, sg, live, sel, M0F);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
     if (li == 0) {
+        if (EPI == ER_EPI_GEGLU) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+            for (int r = 0; r < R / 2; ++r)
+                if (rowLive[r]) *yrow[r] = gelu_tanh(acc[r]) * acc[R / 2 + r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (rowLive[r]) *yrow[r] = acc[r];
+        }
     }
+}
+
+template <int LPR, int NS, int R>
+ER_DEV void gemv_q4k_i8(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                        float *__restrict__ y, uint32_t M, uint32_t K) {
+    using C = I8Cfg<LPR, NS>;
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR;
+    const size_t rowBytes = (size_t)(K >> 8) * 144u;
+    const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+    const uint8_t *rowp[R];
+    float *yrow[R];
+    bool live[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = min(row0 + (uint32_t)r, M - 1u);
+        rowp[r] = W + (size_t)row * rowBytes;
+        yrow[r] = y + row;
+        live[r] = row0 + (uint32_t)r < M;
+    }
+    gemv_q4k_i8_core<LPR, NS, R, ER_EPI_STORE>(rowp, yrow, live, x, K);
+}
+
+// Several Q4_K matrices sharing one x and K (the reference's dual / triple
+// projections, q4_k_gemv_dual_f32 / q4_k_gemv_three_f32,
+// Dequant_Q4_K_M.metal:704-803, 1024-1202): rows of A, B, C are concatenated
+// into one row space; a lane group's R rows may cross a matrix boundary.
+struct Q4Multi {
+    const uint8_t *W[3];
+    float *y[3];
+    uint32_t M[3];
+};
+
+template <int LPR, int NS, int R>
+ER_DEV void gemv_q4k_i8_multi(const Q4Multi &mm, const float *__restrict__ x, uint32_t K) {
+    using C = I8Cfg<LPR, NS>;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR;
+    const size_t rowBytes = (size_t)(K >> 8) * 144u;
+    const uint32_t Mt = mm.M[0] + mm.M[1] + mm.M[2];
+    const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+    const uint8_t *rowp[R];
+    float *yrow[R];
+    bool live[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        uint32_t v = min(row0 + (uint32_t)r, Mt - 1u);
+        int m = 0;
+        if (v >= mm.M[0]) {
+            v -= mm.M[0];
+            m = 1;
+            if (v >= mm.M[1]) {
+                v -= mm.M[1];
+                m = 2;
+            }
+        }
+        rowp[r] = mm.W[m] + (size_t)v * rowBytes;
+        yrow[r] = mm.y[m] + v;
+        live[r] = row0 + (uint32_t)r < Mt;
+    }
+    gemv_q4k_i8_core<LPR, NS, R, ER_EPI_STORE>(rowp, yrow, live, x, K);
+}
+
+// Fused gate/up GeGLU (q4_k_gemv_dual_geglu_f32, Dequant_Q4_K_M.metal:925-1022):
+// y[r] = gelu_tanh(gate[r] . x) * (up[r] . x).  A lane group owns R/2 output
+// rows and computes the gate and up dot products of each in the same lanes.
+template <int LPR, int NS, int R>
+ER_DEV void gemv_q4k_i8_geglu(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
+                              const float *__restrict__ x, float *__restrict__ y, uint32_t M, uint32_t K) {
+    static_assert(R % 2 == 0, "GeGLU pairs gate and up rows");
+    using C = I8Cfg<LPR, NS>;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR;
+    const size_t rowBytes = (size_t)(K >> 8) * 144u;
+    const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)(R / 2);
+    const uint8_t *rowp[R];
+    float *yrow[R];
+    bool live[R];
+#pragma unroll
+    for (int r = 0; r < R / 2; ++r) {
+        const uint32_t row = min(row0 + (uint32_t)r, M - 1u);
+        rowp[r] = Wg + (size_t)row * rowBytes;
+        rowp[R / 2 + r] = Wu + (size_t)row * rowBytes;
+        yrow[r] = yrow[R / 2 + r] = y + row;
+        live[r] = live[R / 2 + r] = row0 + (uint32_t)r < M;
+    }
+    gemv_q4k_i8_core<LPR, NS, R, ER_EPI_GEGLU>(rowp, yrow, live, x, K);
 }
 
 // Q8_0 with K % 64 == 0: slot s = blocks 2s, 2s+1 = row bytes [68s, 68s+68)
@@ -601,6 +723,23 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
         gemv_q8_0_i8<LPR, NS, R>(W, x, y, M, K);                                             \
     }
 ER_I8_CONFIGS(ER_I8_ENTRY)
+
+// Multi-matrix and GeGLU Q4_K kernels: R counts row computations per lane
+// group (GeGLU: R/2 gate rows + the matching up rows).
+#define ER_I8_MULTI_ENTRY(LPR, NS, R)                                                          \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q4k_multi_l##LPR##_n##NS##_r##R(Q4Multi mm, const float *__restrict__ x,       \
+                                                uint32_t K) {                                 \
+        gemv_q4k_i8_multi<LPR, NS, R>(mm, x, K);                                              \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q4k_geglu_l##LPR##_n##NS##_r##R(const uint8_t *__restrict__ Wg,                \
+                                                const uint8_t *__restrict__ Wu,                \
+                                                const float *__restrict__ x,                   \
+                                                float *__restrict__ y, uint32_t M, uint32_t K) { \
+        gemv_q4k_i8_geglu<LPR, NS, R>(Wg, Wu, x, y, M, K);                                    \
+    }
+ER_I8_MULTI_CONFIGS(ER_I8_MULTI_ENTRY)
 
 #define ER_GEMV_ENTRY(fmt, impl, rows, lpr, xg, tag)                                       \
     extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                        \

@@ -18,3 +18,12 @@
 
 #define ER_I8_CONFIGS(X) \
     ER_I8_CONFIGS_L(X, 64) ER_I8_CONFIGS_L(X, 32) ER_I8_CONFIGS_L(X, 16) ER_I8_CONFIGS_L(X, 4)
+
+// Multi-matrix / GeGLU Q4_K kernels: R in {2, 4} row computations per lane
+// group (GeGLU pairs a gate and an up row, so R is even).
+#define ER_I8_MULTI_CONFIGS_L(X, LPR) \
+    X(LPR, 1, 4) X(LPR, 1, 2) X(LPR, 2, 4) X(LPR, 2, 2) X(LPR, 3, 2) X(LPR, 4, 2)
+
+#define ER_I8_MULTI_CONFIGS(X) \
+    ER_I8_MULTI_CONFIGS_L(X, 64) ER_I8_MULTI_CONFIGS_L(X, 32) ER_I8_MULTI_CONFIGS_L(X, 16) \
+    ER_I8_MULTI_CONFIGS_L(X, 4)

@@ -99,6 +99,19 @@ constexpr int kI8Count = (int)(sizeof(kI8Cfg) / sizeof(kI8Cfg[0]));
 // length use them (the default dynamic LDS limit is 64 KiB).
 constexpr uint32_t kI8MaxK = 16384;
 
+// Multi-matrix / GeGLU Q4_K configurations {LPR, NS, R} (er_gemv_cfg.h).
+#define ER_I8_ROW(LPR, NS, R) {LPR, NS, R},
+constexpr I8Cfg kI8MultiCfg[] = {ER_I8_MULTI_CONFIGS(ER_I8_ROW)};
+#undef ER_I8_ROW
+constexpr int kI8MultiCount = (int)(sizeof(kI8MultiCfg) / sizeof(kI8MultiCfg[0]));
+
+// Kernel argument block of er_gemv_q4k_multi_* (matches Q4Multi in er_gemv.hip).
+struct Q4MultiArgs {
+    const void *W[3];
+    void *y[3];
+    uint32_t M[3];
+};
+
 }  // namespace
 
 struct er_hip_ctx {
@@ -107,6 +120,8 @@ struct er_hip_ctx {
     hipFunction_t fn[K_COUNT] = {};
     hipFunction_t fnQ4KI8[kI8Count] = {};
     hipFunction_t fnQ8I8[kI8Count] = {};
+    hipFunction_t fnQ4KMulti[kI8MultiCount] = {};
+    hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
     int cu_count = 0;
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
     int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1 selects the non-pipelined GEMM (benchmark comparison)
@@ -179,6 +194,35 @@ int pick_i8(uint32_t S, uint32_t M, int cu) {
         }
     }
     return pick;
+}
+
+// Multi-matrix / GeGLU configuration for S slots and Mt total row
+// computations: as pick_i8, over kI8MultiCfg (R in {4, 2}).
+int pick_i8_multi(uint32_t S, uint32_t Mt, int cu) {
+    static const uint32_t lprs[] = {64, 32, 16, 4};
+    uint32_t bestL = 0, bestN = 0, bestWaste = 0xffffffffu;
+    for (uint32_t L : lprs) {
+        const uint32_t N = (S + L - 1) / L;
+        if (N > 4) continue;
+        const uint32_t waste = L * N - S;
+        if (waste < bestWaste) {
+            bestWaste = waste;
+            bestL = L;
+            bestN = N;
+        }
+    }
+    if (!bestL) return -1;
+    const uint32_t G = 64u / bestL;
+    int fallback = -1;
+    for (uint32_t R : {4u, 2u}) {
+        for (int i = 0; i < kI8MultiCount; ++i) {
+            if (kI8MultiCfg[i].lpr != bestL || kI8MultiCfg[i].ns != bestN || kI8MultiCfg[i].r != R) continue;
+            const uint64_t wgs = ((uint64_t)Mt + ER_GEMV_WAVES * G * R - 1) / (ER_GEMV_WAVES * G * R);
+            if (wgs >= 2u * (uint64_t)cu) return i;
+            fallback = i;  // the last match is R = 2: most workgroups
+        }
+    }
+    return fallback;
 }
 
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
@@ -365,6 +409,69 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     return launch(ctx, k, grid, dim3(256, 1, 1), lds, stream, args);
 }
 
+// Fused Q4_K projections: validation of each weight as encodeQ4KWeights, then
+// one multi-matrix launch (fp32 fallback: one GEMV per matrix).
+er_status encode_q4k_multi(er_hip_ctx *ctx, er_stream stream, const er_buffer *Ws, er_buffer x,
+                           const er_buffer *ys, const uint32_t *Ms, int count, uint32_t K) {
+    for (int i = 0; i < count; ++i) {
+        er_status st = validate_gemv(Fmt::Q4_K, Ws[i], x, ys[i], 1, Ms[i], K);
+        if (st != ER_OK) return st;
+    }
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    uint64_t Mt = 0;
+    for (int i = 0; i < count; ++i) Mt += Ms[i];
+    if (Mt == 0) return ER_OK;
+    if (Mt > 0xffffffffull) return fail(ER_ERR_INVALID_MATRIX_SHAPE, "Q4_K multi: too many rows");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    const int ci = K <= kI8MaxK ? pick_i8_multi(K / 64u, (uint32_t)Mt, ctx->cu_count) : -1;
+    if (ci < 0) {
+        for (int i = 0; i < count; ++i) {
+            st = encode_gemv(ctx, stream, Fmt::Q4_K, Ws[i], x, ys[i], 1, Ms[i], K);
+            if (st != ER_OK) return st;
+        }
+        return ER_OK;
+    }
+    const I8Cfg &c = kI8MultiCfg[ci];
+    Q4MultiArgs a{};
+    for (int i = 0; i < 3; ++i) {
+        const int j = i < count ? i : 0;
+        a.W[i] = Ws[j].data;
+        a.y[i] = ys[j].data;
+        a.M[i] = i < count ? Ms[i] : 0u;
+    }
+    const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
+    const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+    void *args[] = {&a, &x.data, &K};
+    dim3 grid((uint32_t)((Mt + rowsPerBlock - 1) / rowsPerBlock), 1, 1);
+    return launch_fn(ctx->fnQ4KMulti[ci], "er_gemv_q4k_multi", grid, dim3(kGemvThreads, 1, 1), lds,
+                     stream, args);
+}
+
+er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_buffer Wu, er_buffer x,
+                           er_buffer y, uint32_t M, uint32_t K) {
+    er_status st = validate_gemv(Fmt::Q4_K, Wg, x, y, 1, M, K);
+    if (st != ER_OK) return st;
+    st = validate_gemv(Fmt::Q4_K, Wu, x, y, 1, M, K);
+    if (st != ER_OK) return st;
+    st = check_ctx(ctx);
+    if (st != ER_OK || M == 0) return st;
+    const int ci = K <= kI8MaxK ? pick_i8_multi(K / 64u, 2u * M, ctx->cu_count) : -1;
+    if (ci < 0)
+        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "Q4_K dual GeGLU: K=%u exceeds the fused kernel's %u", K,
+                    kI8MaxK);
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    const I8Cfg &c = kI8MultiCfg[ci];
+    const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * (c.r / 2u);
+    const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+    void *args[] = {&Wg.data, &Wu.data, &x.data, &y.data, &M, &K};
+    dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, 1, 1);
+    return launch_fn(ctx->fnQ4KGeglu[ci], "er_gemv_q4k_geglu", grid, dim3(kGemvThreads, 1, 1), lds,
+                     stream, args);
+}
+
 er_status encode_dequant(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer blocks,
                          uint64_t count, er_buffer out) {
     const uint64_t need = count * block_bytes(f);
@@ -462,6 +569,21 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
             std::snprintf(name, sizeof(name), "er_gemv_%s_i8_l%u_n%u_r%u", fmt ? "q8_0" : "q4k",
                           (unsigned)kI8Cfg[i].lpr, (unsigned)kI8Cfg[i].ns, (unsigned)kI8Cfg[i].r);
             e = hipModuleGetFunction(fmt ? &ctx->fnQ8I8[i] : &ctx->fnQ4KI8[i], ctx->module, name);
+            if (e != hipSuccess) {
+                (void)hipModuleUnload(ctx->module);
+                delete ctx;
+                return fail(ER_ERR_FUNCTION_NOT_FOUND, "functionNotFound(%s): %s", name,
+                            hipGetErrorString(e));
+            }
+        }
+    }
+    for (int i = 0; i < kI8MultiCount; ++i) {
+        char name[64];
+        for (int kind = 0; kind < 2; ++kind) {
+            std::snprintf(name, sizeof(name), "er_gemv_q4k_%s_l%u_n%u_r%u", kind ? "geglu" : "multi",
+                          (unsigned)kI8MultiCfg[i].lpr, (unsigned)kI8MultiCfg[i].ns,
+                          (unsigned)kI8MultiCfg[i].r);
+            e = hipModuleGetFunction(kind ? &ctx->fnQ4KGeglu[i] : &ctx->fnQ4KMulti[i], ctx->module, name);
             if (e != hipSuccess) {
                 (void)hipModuleUnload(ctx->module);
                 delete ctx;
@@ -748,6 +870,31 @@ er_status er_hip_encode_q6k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer
 er_status er_hip_encode_q8_0_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
                                      er_buffer input, er_buffer output, uint32_t M, uint32_t K) {
     return encode_gemv(ctx, stream, Fmt::Q8_0, weight, input, output, 1, M, K);
+}
+
+er_status er_hip_encode_q4k_weights_dual(er_hip_ctx *ctx, er_stream stream, er_buffer weight_a,
+                                         er_buffer weight_b, er_buffer input, er_buffer output_a,
+                                         er_buffer output_b, uint32_t M, uint32_t K) {
+    const er_buffer Ws[2] = {weight_a, weight_b}, ys[2] = {output_a, output_b};
+    const uint32_t Ms[2] = {M, M};
+    return encode_q4k_multi(ctx, stream, Ws, input, ys, Ms, 2, K);
+}
+
+er_status er_hip_encode_q4k_weights_triple(er_hip_ctx *ctx, er_stream stream, er_buffer weight_a,
+                                           er_buffer weight_b, er_buffer weight_c, er_buffer input,
+                                           er_buffer output_a, er_buffer output_b,
+                                           er_buffer output_c, uint32_t rows_a, uint32_t rows_b,
+                                           uint32_t rows_c, uint32_t K) {
+    const er_buffer Ws[3] = {weight_a, weight_b, weight_c}, ys[3] = {output_a, output_b, output_c};
+    const uint32_t Ms[3] = {rows_a, rows_b, rows_c};
+    return encode_q4k_multi(ctx, stream, Ws, input, ys, Ms, 3, K);
+}
+
+er_status er_hip_encode_q4k_weights_dual_geglu(er_hip_ctx *ctx, er_stream stream,
+                                               er_buffer gate_weight, er_buffer up_weight,
+                                               er_buffer input, er_buffer output, uint32_t M,
+                                               uint32_t K) {
+    return encode_q4k_geglu(ctx, stream, gate_weight, up_weight, input, output, M, K);
 }
 
 er_status er_hip_encode_batched_q4k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,

@@ -79,6 +79,64 @@ class GEMVKernel:
             self.ctx.handle, _sh(stream), weightBuffer.raw, inputBuffer.raw, outputBuffer.raw,
             batchSeq, M, K))
 
+    def encodeQ4KWeightsDual(self, stream: Optional[Stream], weightBufferA: Buffer,
+                             weightBufferB: Buffer, inputBuffer: Buffer, outputBufferA: Buffer,
+                             outputBufferB: Buffer, M: int, K: int) -> None:
+        """GEMVKernel.encodeQ4KWeightsDual (GEMVKernel.swift:879-928)."""
+        check(self.lib.er_hip_encode_q4k_weights_dual(
+            self.ctx.handle, _sh(stream), weightBufferA.raw, weightBufferB.raw, inputBuffer.raw,
+            outputBufferA.raw, outputBufferB.raw, M, K))
+
+    def encodeQ4KWeightsTriple(self, stream: Optional[Stream], weightBufferA: Buffer,
+                               weightBufferB: Buffer, weightBufferC: Buffer, inputBuffer: Buffer,
+                               outputBufferA: Buffer, outputBufferB: Buffer, outputBufferC: Buffer,
+                               rowsA: int, rowsB: int, rowsC: int, K: int) -> None:
+        """GEMVKernel.encodeQ4KWeightsTriple (GEMVKernel.swift:978-1043)."""
+        check(self.lib.er_hip_encode_q4k_weights_triple(
+            self.ctx.handle, _sh(stream), weightBufferA.raw, weightBufferB.raw, weightBufferC.raw,
+            inputBuffer.raw, outputBufferA.raw, outputBufferB.raw, outputBufferC.raw, rowsA, rowsB,
+            rowsC, K))
+
+    def encodeQ4KWeightsDualGeGLU(self, stream: Optional[Stream], gateWeightBuffer: Buffer,
+                                  upWeightBuffer: Buffer, inputBuffer: Buffer, outputBuffer: Buffer,
+                                  M: int, K: int) -> None:
+        """GEMVKernel.encodeQ4KWeightsDualGeGLU (GEMVKernel.swift:930-976)."""
+        check(self.lib.er_hip_encode_q4k_weights_dual_geglu(
+            self.ctx.handle, _sh(stream), gateWeightBuffer.raw, upWeightBuffer.raw,
+            inputBuffer.raw, outputBuffer.raw, M, K))
+
+    def executeQ4KWeightsMulti(self, rawWeights: list, x, rows: list, K: int, geglu: bool = False):
+        """Uploads 2 or 3 Q4_K matrices sharing x and runs the dual / triple
+        (or, with geglu=True and two equal-height matrices, the fused GeGLU)
+        projection; returns the list of outputs (one array for GeGLU)."""
+        ctx = self.ctx
+        xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        wbs = [ctx.upload(_u8(w)) for w in rawWeights]
+        xb = ctx.upload(xv)
+        try:
+            if geglu:
+                yb = ctx.alloc(rows[0] * 4)
+                self.encodeQ4KWeightsDualGeGLU(None, wbs[0], wbs[1], xb, yb, rows[0], K)
+                ctx.synchronize()
+                out = yb.download(np.float32, rows[0])
+                yb.free()
+                return out
+            ybs = [ctx.alloc(m * 4) for m in rows]
+            if len(rawWeights) == 2:
+                self.encodeQ4KWeightsDual(None, wbs[0], wbs[1], xb, ybs[0], ybs[1], rows[0], K)
+            else:
+                self.encodeQ4KWeightsTriple(None, wbs[0], wbs[1], wbs[2], xb, ybs[0], ybs[1], ybs[2],
+                                            rows[0], rows[1], rows[2], K)
+            ctx.synchronize()
+            outs = [b.download(np.float32, m) for b, m in zip(ybs, rows)]
+            for b in ybs:
+                b.free()
+            return outs
+        finally:
+            for b in wbs:
+                b.free()
+            xb.free()
+
     def encodeProjection(self, stream: Optional[Stream], weightBuffer: Buffer, dataType: int,
                          inputBuffer: Buffer, outputBuffer: Buffer, M: int, K: int,
                          tokens: int = 1, byteOffset: int = 0) -> None:

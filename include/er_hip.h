@@ -181,6 +181,29 @@ er_status er_hip_encode_q6k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer
 er_status er_hip_encode_q8_0_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
                                      er_buffer input, er_buffer output, uint32_t M, uint32_t K);
 
+/* ---- fused Q4_K projections sharing one input vector (one launch, x read
+ * and staged once).  Validation per weight as encodeQ4KWeights; inputs and
+ * outputs too short -> ENCODING_FAILED.
+ * GEMVKernel.encodeQ4KWeightsDual (GEMVKernel.swift:879-928, kernel
+ * q4_k_gemv_dual_f32): yA = WA.x, yB = WB.x, both M x K. */
+er_status er_hip_encode_q4k_weights_dual(er_hip_ctx *ctx, er_stream stream, er_buffer weight_a,
+                                         er_buffer weight_b, er_buffer input, er_buffer output_a,
+                                         er_buffer output_b, uint32_t M, uint32_t K);
+/* GEMVKernel.encodeQ4KWeightsTriple (GEMVKernel.swift:978-1043, kernel
+ * q4_k_gemv_three_f32): three matrices of rows_a / rows_b / rows_c rows. */
+er_status er_hip_encode_q4k_weights_triple(er_hip_ctx *ctx, er_stream stream, er_buffer weight_a,
+                                           er_buffer weight_b, er_buffer weight_c, er_buffer input,
+                                           er_buffer output_a, er_buffer output_b,
+                                           er_buffer output_c, uint32_t rows_a, uint32_t rows_b,
+                                           uint32_t rows_c, uint32_t K);
+/* GEMVKernel.encodeQ4KWeightsDualGeGLU (GEMVKernel.swift:930-976, kernel
+ * q4_k_gemv_dual_geglu_f32): y = gelu_tanh(Wgate.x) * (Wup.x), gelu_tanh
+ * saturated outside [-10, 10].  K <= 16384 (else INVALID_VECTOR_SHAPE). */
+er_status er_hip_encode_q4k_weights_dual_geglu(er_hip_ctx *ctx, er_stream stream,
+                                               er_buffer gate_weight, er_buffer up_weight,
+                                               er_buffer input, er_buffer output, uint32_t M,
+                                               uint32_t K);
+
 /* ---- batched (token-axis) GEMV: y[t*M + r] = W[r,:] . x[t*K : (t+1)*K] ----
  * GEMVKernel.encodeBatchedQ4KWeights (GEMVKernel.swift:682-702, validation
  * :1319-1361: batchSeq > 0, input >= batchSeq*K*4, output >= batchSeq*M*4 else

@@ -524,6 +524,18 @@ void er_ref_make_q6k_weights(int rows, int cols, uint8_t *bytes) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* GELU, tanh approximation, saturated outside [-10, 10]: cpuGeluTanh,
+ * Tests/EdgeRunnerMetalTests/GEMVTests.swift:38-47 (fp32 evaluation order of
+ * the Swift expression: c * (v + 0.044715 * v * v * v), v * 0.5 * (1 + tanh)). */
+float er_ref_gelu_tanh(float v) {
+    if (v > 10.0f) return v;
+    if (v < -10.0f) return 0.0f;
+    const float c = 0.7978845608028654f;
+    float inner = c * (v + 0.044715f * v * v * v);
+    return v * 0.5f * (1.0f + tanhf(inner));
+}
+
+/* ------------------------------------------------------------------------ */
 /* Greedy top-1 over logits: lowest index wins ties, as the reference's
  * Swift max(by:) in GEMVTests.swift:629 and Dequant_Q6_K.metal:327,338.      */
 /* ------------------------------------------------------------------------ */

@@ -59,6 +59,8 @@ def load():
         f = getattr(lib, name)
         f.argtypes = [C.c_int, C.c_int, u8p]
         f.restype = None
+    lib.er_ref_gelu_tanh.argtypes = [C.c_float]
+    lib.er_ref_gelu_tanh.restype = C.c_float
     lib.er_ref_argmax.argtypes = [f32p, C.c_uint32]
     lib.er_ref_argmax.restype = C.c_uint32
     lib.er_ref_max_threads.argtypes = []
@@ -139,6 +141,11 @@ def make_q6k_weights(rows: int, cols: int) -> np.ndarray:
     out = np.zeros(rows * cols // 256 * 210, dtype=np.uint8)
     load().er_ref_make_q6k_weights(rows, cols, out.ctypes.data_as(u8p))
     return out
+
+
+def gelu_tanh(v) -> np.ndarray:
+    f = load().er_ref_gelu_tanh
+    return np.array([f(float(t)) for t in np.asarray(v, np.float32).ravel()], np.float32)
 
 
 def argmax(v) -> int:

@@ -128,3 +128,20 @@ def test_quantize_q8_0_rows_closed_forms():
     row[3] = -2.5
     q = ref.quantize_q8_0_rows(row, 1, 32, 0, 1)[2:6].view(np.int8)
     assert list(q) == [127, 0, 2, -2]
+
+
+def test_gelu_tanh_oracle():
+    """cpuGeluTanh (GEMVTests.swift:38-47): odd-part identity g(x) - g(-x) = x,
+    saturation outside [-10, 10], and the tanh form's known distance (< 2e-3)
+    from the exact x * Phi(x)."""
+    import math
+    xs = np.linspace(-9.5, 9.5, 381).astype(np.float32)
+    g = ref.gelu_tanh(xs)
+    gm = ref.gelu_tanh(-xs)
+    assert np.allclose(g - gm, xs, atol=2e-6)
+    exact = np.array([0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))) for v in xs.astype(np.float64)])
+    assert np.max(np.abs(g - exact)) < 2e-3
+    big = np.array([10.5, 12.0, 1e4], np.float32)
+    assert np.array_equal(ref.gelu_tanh(big), big)
+    assert np.all(ref.gelu_tanh(-big) == 0.0)
+    assert ref.gelu_tanh([0.0])[0] == 0.0
