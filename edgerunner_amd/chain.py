@@ -25,7 +25,7 @@ Two execution forms are recorded into a HIP graph:
     dispatch pattern);
   * fused: q/k/v as one triple projection and gate/up as one dual projection
     (encodeQ4KWeightsTriple / encodeQ4KWeightsDual, one x read each),
-    5 launches per layer + head = 141.
+    4 launches per layer + head = 113.
 """
 from __future__ import annotations
 
@@ -80,7 +80,7 @@ class ChainSpec:
         return tot
 
     def launches(self, fused: bool) -> int:
-        return self.layers * (5 if fused else 7) + 1
+        return self.layers * (4 if fused else 7) + 1
 
 
 def make_weights(spec: ChainSpec, config: int = 5) -> Dict[Tuple[int, str], np.ndarray]:

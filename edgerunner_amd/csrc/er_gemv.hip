@@ -7,19 +7,20 @@
 //
 // Two kernel families:
 //
-// 1. Integer-dot kernels (Q4_K, and Q8_0 with K % 64 == 0): x is staged once
+// 1. Integer-dot kernels (Q4_K, Q6_K, and Q8_0 with K % 64 == 0): x is staged once
 //    per workgroup as three int8 limbs per value (er_xlimbs.h) and every
 //    weight x activation product is formed with v_dot4_i32_i8, exactly, in
 //    int32.  A "slot" is 64 weights of one row: a Q4_K sub-block pair
-//    (32 qs bytes + the block header) or two Q8_0 blocks (68 bytes).  A wave
+//    (32 qs bytes + the block header), two Q8_0 blocks (68 bytes) or a
+//    quarter of a Q6_K block (48 bytes of ql/qh, 4 scales, d).  A wave
 //    is split into 64/LPR lane groups of LPR lanes; a group owns R rows and
 //    each lane NS slots of each row.  Every weight load of a lane is issued
 //    up front (after the L2-resident x loads, before x staging), and the
 //    slots are consumed in issue order, so the wave computes on the first
 //    slot while the rest are still in flight.
 //
-// 2. fp32 kernels (Q6_K; Q8_0 with an odd number of blocks per row; rows
-//    longer than the integer kernels cover): x is staged in LDS as fp32, a
+// 2. fp32 kernels (Q8_0 with an odd number of blocks per row; rows longer
+//    than the integer kernels cover): x is staged in LDS as fp32, a
 //    16-byte "slot" of raw bytes is unpacked in registers and accumulated
 //    with fp32 FMAs.
 //
@@ -370,6 +371,118 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
     }
 }
 
+// Q6_K slot s of a row = super-block b = s/4, half h = (s/2)%2, lane chunk
+// c = s%2: ql bytes [64h+16c, +16) (q1 low / q3 high nibbles) and
+// [64h+32+16c, +16) (q2 / q4), qh bytes [128+32h+16c, +16) (2 high bits of
+// q1..q4), scales sc[8h+2m+c] (m = 0..3) and d.  Its weights are positions
+// 256b + 128h + 32m + 16c + [0, 16): x granules G0 + 2m with G0 = 16b+8h+c,
+// 64-groups 4b+2h (m < 2) and 4b+2h+1.  Blocks are 2-byte aligned: the
+// fields are fetched with the aligned-window loads (ld16_a2 / ld8_a2).
+// Value = d * sc * (q6 - 32): the -32 is applied through the x chunk sums.
+template <int LPR, int NS, int R>
+ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                        float *__restrict__ y, uint32_t M, uint32_t K) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    using C = I8Cfg<LPR, NS>;
+    constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR, li = lane % LPR;
+    const uint32_t S = K >> 6;
+    const size_t rowBytes = (size_t)(K >> 8) * 210u;
+    const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+
+    float4 xr[C::XG][4];
+    xl_load<C::XG, NT>(x, K, xr);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 fa[NS][R], fb[NS][R], fh[NS][R];
+    u32x2 fs[NS][R];
+    uint32_t fd[NS][R];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t s = min(li + (uint32_t)LPR * j, S - 1u);
+        const uint32_t h = (s >> 1) & 1u, c = s & 1u;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = W + (size_t)min(row0 + (uint32_t)r, M - 1u) * rowBytes + (s >> 2) * 210u;
+            fa[j][r] = ld16_a2(blk + 64u * h + 16u * c);
+            fb[j][r] = ld16_a2(blk + 64u * h + 32u + 16u * c);
+            fh[j][r] = ld16_a2(blk + 128u + 32u * h + 16u * c);
+            fs[j][r] = ld8_a2(blk + 192u + 8u * h);
+            fd[j][r] = ld2(blk + 208u);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    xl_store<C::XG, NT>(lds, K, xr);
+    xl_store_tail<C::XG, NT>(x, lds, K);
+    __syncthreads();
+
+    const XLimbs X = xl_view(lds, K);
+    const uint32_t M0F = vreg_const(0x0f0f0f0fu), M30 = vreg_const(0x30303030u);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t sRaw = li + (uint32_t)LPR * j;
+        const uint32_t s = min(sRaw, S - 1u);
+        const float live = sRaw < S ? 1.0f : 0.0f;
+        const uint32_t b = s >> 2, h = (s >> 1) & 1u, c = s & 1u;
+        const uint32_t G0 = 16u * b + 8u * h + c;
+        // x limbs of the 4 granules G0 + 2m, and their sums / group scales
+        u32x4 xv[ER_XL_PLANES][4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t off = 16u * xl_gswz(G0 + 2u * m);
+#pragma unroll
+            for (int l = 0; l < ER_XL_PLANES; ++l)
+                xv[l][m] = *(const u32x4 *)__builtin_assume_aligned(X.planes + (size_t)l * X.K + off, 16);
+        }
+        const float sgA = live * X.sg64[4u * b + 2u * h], sgB = live * X.sg64[4u * b + 2u * h + 1u];
+        float X32[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) X32[m] = 32.0f * X.x16[G0 + 2u * m];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t A[4] = {fa[j][r].x, fa[j][r].y, fa[j][r].z, fa[j][r].w};
+            const uint32_t B[4] = {fb[j][r].x, fb[j][r].y, fb[j][r].z, fb[j][r].w};
+            const uint32_t H[4] = {fh[j][r].x, fh[j][r].y, fh[j][r].z, fh[j][r].w};
+            int cq[4][ER_XL_PLANES] = {};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q[4] = {(A[k] & M0F) | ((H[k] << 4) & M30),
+                                       (B[k] & M0F) | ((H[k] << 2) & M30),
+                                       ((A[k] >> 4) & M0F) | (H[k] & M30),
+                                       ((B[k] >> 4) & M0F) | ((H[k] >> 2) & M30)};
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+#pragma unroll
+                    for (int l = 0; l < ER_XL_PLANES; ++l)
+                        cq[m][l] = __builtin_amdgcn_sdot4((int)q[m], (int)xv[l][m][k], cq[m][l], false);
+            }
+            // scales: m = 0, 1 in dword x (bytes c, 2 + c), m = 2, 3 in dword y
+            const float s0 = (float)(int8_t)(fs[j][r].x >> (8u * c));
+            const float s1 = (float)(int8_t)(fs[j][r].x >> (8u * c + 16u));
+            const float s2 = (float)(int8_t)(fs[j][r].y >> (8u * c));
+            const float s3 = (float)(int8_t)(fs[j][r].y >> (8u * c + 16u));
+            float v = s0 * __builtin_fmaf(sgA, xl_combine(cq[0][0], cq[0][1], cq[0][2]), -live * X32[0]);
+            v = __builtin_fmaf(s1, __builtin_fmaf(sgA, xl_combine(cq[1][0], cq[1][1], cq[1][2]), -live * X32[1]), v);
+            v = __builtin_fmaf(s2, __builtin_fmaf(sgB, xl_combine(cq[2][0], cq[2][1], cq[2][2]), -live * X32[2]), v);
+            v = __builtin_fmaf(s3, __builtin_fmaf(sgB, xl_combine(cq[3][0], cq[3][1], cq[3][2]), -live * X32[3]), v);
+            acc[r] = __builtin_fmaf(f16_to_f32(fd[j][r]), v, acc[r]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+    }
+}
+
 // ===========================================================================
 // Family 2: fp32 kernels
 // ===========================================================================
@@ -705,7 +818,7 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
 
 // ---------------------------------------------------------------------------
 // Entry points (extern "C" so hipModuleGetFunction resolves them by name).
-//   er_gemv_<fmt>_i8_l<LPR>_n<NS>_r<R> : integer-dot family (er_gemv_cfg.h)
+//   er_gemv_<fmt>_i8_l<LPR>_n<NS>_r<R> : integer-dot family (er_gemv_cfg.h; q4k, q8_0, q6k)
 //   er_gemv_<fmt>_l<LPR>_<s|g>         : fp32 family, x staged in LDS (s) or
 //                                        read from global memory (g)
 // ---------------------------------------------------------------------------
@@ -721,6 +834,12 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
                                               const float *__restrict__ x,                    \
                                               float *__restrict__ y, uint32_t M, uint32_t K) { \
         gemv_q8_0_i8<LPR, NS, R>(W, x, y, M, K);                                             \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q6k_i8_l##LPR##_n##NS##_r##R(const uint8_t *__restrict__ W,                  \
+                                             const float *__restrict__ x,                     \
+                                             float *__restrict__ y, uint32_t M, uint32_t K) { \
+        gemv_q6k_i8<LPR, NS, R>(W, x, y, M, K);                                              \
     }
 ER_I8_CONFIGS(ER_I8_ENTRY)
 

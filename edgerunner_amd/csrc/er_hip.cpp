@@ -120,12 +120,14 @@ struct er_hip_ctx {
     hipFunction_t fn[K_COUNT] = {};
     hipFunction_t fnQ4KI8[kI8Count] = {};
     hipFunction_t fnQ8I8[kI8Count] = {};
+    hipFunction_t fnQ6KI8[kI8Count] = {};
     hipFunction_t fnQ4KMulti[kI8MultiCount] = {};
     hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
     int cu_count = 0;
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
     int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1 selects the non-pipelined GEMM (benchmark comparison)
     uint32_t gemm_tt = 0, gemm_sk = 0;  // ER_HIP_GEMM_TILE=tt:sk (benchmark sweeps only)
+    int gemv_fp32 = 0;  // ER_HIP_GEMV_FP32=1 selects the fp32 GEMV family (benchmark comparison)
     er_device_info info{};
 };
 
@@ -165,23 +167,46 @@ er_status launch_fn(hipFunction_t f, const char *name, dim3 grid, dim3 block, ui
     return ER_OK;
 }
 
-// Picks the integer-dot configuration for a row of S 64-weight slots and M
-// rows: the lane split (LPR, NS) that leaves the fewest idle slots (ties: more
-// lanes per row), then the most rows per lane group that still gives every CU
-// two workgroups.  Returns -1 when no configuration covers S.
-int pick_i8(uint32_t S, uint32_t M, int cu) {
+// Lane-group width L (lanes per row) and slots per lane N = ceil(S / L) for
+// S slots and M rows, N <= maxN.  Among the widths whose one-row-per-group
+// grid (R = 1) gives at least every other CU a workgroup, the one with the
+// fewest idle slot lanes; when none does (short matrices, latency-bound), the
+// one with the most workgroups.  Sets L = 0 when no width fits.
+void pick_lanes(uint32_t S, uint32_t M, uint32_t maxN, int cu, uint32_t &L, uint32_t &N) {
     static const uint32_t lprs[] = {64, 32, 16, 4};
-    uint32_t bestL = 0, bestN = 0, bestWaste = 0xffffffffu;
-    for (uint32_t L : lprs) {
-        const uint32_t N = (S + L - 1) / L;
-        if (N > 8) continue;
-        const uint32_t waste = L * N - S;
-        if (waste < bestWaste) {
+    uint32_t bestWaste = 0xffffffffu;
+    uint64_t bestWgs = 0;
+    bool bestFull = false;
+    L = N = 0;
+    for (uint32_t l : lprs) {
+        const uint32_t n = (S + l - 1) / l;
+        if (n > maxN) continue;
+        const uint32_t waste = l * n - S;
+        const uint64_t rowsPerWg = (uint64_t)ER_GEMV_WAVES * (64u / l);
+        const uint64_t wgs = ((uint64_t)M + rowsPerWg - 1) / rowsPerWg;
+        const bool full = 2u * wgs >= (uint64_t)cu;
+        bool better;
+        if (full)
+            better = !bestFull || waste < bestWaste;
+        else
+            better = !bestFull && (wgs > bestWgs || (wgs == bestWgs && waste < bestWaste));
+        if (L == 0 || better) {
+            L = l;
+            N = n;
             bestWaste = waste;
-            bestL = L;
-            bestN = N;
+            bestWgs = wgs;
+            bestFull = full;
         }
     }
+}
+
+// Picks the integer-dot configuration for a row of S 64-weight slots and M
+// rows: the lane split (LPR, NS) of pick_lanes, then the most rows per lane
+// group that still gives every CU two workgroups.  Returns -1 when no
+// configuration covers S.
+int pick_i8(uint32_t S, uint32_t M, int cu) {
+    uint32_t bestL = 0, bestN = 0;
+    pick_lanes(S, M, 8, cu, bestL, bestN);
     if (!bestL) return -1;
     const uint32_t G = 64u / bestL;
     int pick = -1;
@@ -199,18 +224,8 @@ int pick_i8(uint32_t S, uint32_t M, int cu) {
 // Multi-matrix / GeGLU configuration for S slots and Mt total row
 // computations: as pick_i8, over kI8MultiCfg (R in {4, 2}).
 int pick_i8_multi(uint32_t S, uint32_t Mt, int cu) {
-    static const uint32_t lprs[] = {64, 32, 16, 4};
-    uint32_t bestL = 0, bestN = 0, bestWaste = 0xffffffffu;
-    for (uint32_t L : lprs) {
-        const uint32_t N = (S + L - 1) / L;
-        if (N > 4) continue;
-        const uint32_t waste = L * N - S;
-        if (waste < bestWaste) {
-            bestWaste = waste;
-            bestL = L;
-            bestN = N;
-        }
-    }
+    uint32_t bestL = 0, bestN = 0;
+    pick_lanes(S, Mt, 4, cu, bestL, bestN);
     if (!bestL) return -1;
     const uint32_t G = 64u / bestL;
     int fallback = -1;
@@ -302,7 +317,7 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
 
     void *args[] = {&W.data, &x.data, &y.data, &M, &K};
     const bool q8Aligned = f == Fmt::Q8_0 && K % 64u == 0;
-    if ((f == Fmt::Q4_K || q8Aligned) && K <= kI8MaxK) {
+    if ((f != Fmt::Q8_0 || q8Aligned) && K <= kI8MaxK && ctx->gemv_fp32 == 0) {
         int ci = pick_i8(K / 64u, M, ctx->cu_count);
         if (ctx->i8_override >= 0 && (uint32_t)kI8Cfg[ctx->i8_override].lpr *
                                              kI8Cfg[ctx->i8_override].ns >= K / 64u)
@@ -312,9 +327,10 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
             const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
             const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
             dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
-            hipFunction_t fn = f == Fmt::Q4_K ? ctx->fnQ4KI8[ci] : ctx->fnQ8I8[ci];
-            return launch_fn(fn, f == Fmt::Q4_K ? "er_gemv_q4k_i8" : "er_gemv_q8_0_i8", grid,
-                             dim3(kGemvThreads, 1, 1), lds, stream, args);
+            hipFunction_t fn = f == Fmt::Q4_K ? ctx->fnQ4KI8[ci]
+                                              : (f == Fmt::Q8_0 ? ctx->fnQ8I8[ci] : ctx->fnQ6KI8[ci]);
+            return launch_fn(fn, f == Fmt::Q4_K ? "er_gemv_q4k_i8" : (f == Fmt::Q8_0 ? "er_gemv_q8_0_i8" : "er_gemv_q6k_i8"),
+                             grid, dim3(kGemvThreads, 1, 1), lds, stream, args);
         }
     }
     if (f == Fmt::Q8_0 && !q8Aligned) {
@@ -565,10 +581,12 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
     }
     for (int i = 0; i < kI8Count; ++i) {
         char name[64];
-        for (int fmt = 0; fmt < 2; ++fmt) {
-            std::snprintf(name, sizeof(name), "er_gemv_%s_i8_l%u_n%u_r%u", fmt ? "q8_0" : "q4k",
+        static const char *const fmts[3] = {"q4k", "q8_0", "q6k"};
+        for (int fmt = 0; fmt < 3; ++fmt) {
+            std::snprintf(name, sizeof(name), "er_gemv_%s_i8_l%u_n%u_r%u", fmts[fmt],
                           (unsigned)kI8Cfg[i].lpr, (unsigned)kI8Cfg[i].ns, (unsigned)kI8Cfg[i].r);
-            e = hipModuleGetFunction(fmt ? &ctx->fnQ8I8[i] : &ctx->fnQ4KI8[i], ctx->module, name);
+            hipFunction_t *slot = fmt == 0 ? &ctx->fnQ4KI8[i] : (fmt == 1 ? &ctx->fnQ8I8[i] : &ctx->fnQ6KI8[i]);
+            e = hipModuleGetFunction(slot, ctx->module, name);
             if (e != hipSuccess) {
                 (void)hipModuleUnload(ctx->module);
                 delete ctx;
@@ -593,6 +611,7 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
         }
     }
     if (const char *gv = std::getenv("ER_HIP_GEMM_VARIANT")) ctx->gemm_variant = std::atoi(gv);
+    if (const char *fv = std::getenv("ER_HIP_GEMV_FP32")) ctx->gemv_fp32 = std::atoi(fv);
     if (const char *gt = std::getenv("ER_HIP_GEMM_TILE")) {
         unsigned a = 0, b = 0;
         if (std::sscanf(gt, "%u:%u", &a, &b) == 2 && (a == 64 || a == 128 || a == 256) && b >= 1) {
