@@ -52,6 +52,12 @@ GEMV_WORKLOADS = [
 ]
 
 
+# Greedy top-1 heads: (name, M, K, BASELINE config index)
+TOP1_WORKLOADS = [
+    ("q6_k_top1_151936x1024", 151936, 1024, 3),
+    ("q6_k_top1_128256x4096", 128256, 4096, 3),
+]
+
 # (name, fmt, T tokens, N, K, BASELINE config index)
 GEMM_WORKLOADS = [
     ("q4_k_gemm_512x4096x4096", "q4_k", 512, 4096, 4096, 4),
@@ -132,6 +138,54 @@ def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int)
         "us_per_call_eager": eager_us,
         "ms_total": ms, "y_finite": bool(np.all(np.isfinite(y))),
     }
+
+
+def bench_top1(ctx, M: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
+    """Q6_K head with fused greedy top-1 (GEMV + partial epilogue, then the
+    one-workgroup reduce): `steps` calls over rotating weight copies in a HIP
+    graph, as bench_gemv.  Bytes per call: W + x + the 4-byte index."""
+    import edgerunner_amd.synth as synth
+    from edgerunner_amd import Capture, GEMVKernel
+
+    gemv = GEMVKernel(ctx)
+    W = synth.weights("q6_k", synth.seed(cfg, 0), M, K, **DSCALE["q6_k"])
+    x = synth.normal_f32(synth.seed(cfg, 1), K)
+    copies = max(2, -(-ROTATE_BYTES // W.nbytes))
+    stream = ctx.stream()
+    wbufs = [ctx.upload(W, stream) for _ in range(copies)]
+    xb = ctx.upload(x, stream)
+    n = gemv.q6KTop1PartialCount(M)
+    pv, pi, ob = ctx.alloc(4 * n), ctx.alloc(4 * n), ctx.alloc(4)
+
+    def enc(i):
+        gemv.encodeQ6KWeightsPackedTop1(stream, wbufs[i % copies], xb, pv, pi, ob, M, K)
+
+    for i in range(warmup):
+        enc(i)
+    stream.synchronize()
+    with Capture(ctx, stream) as cap:
+        for i in range(steps):
+            enc(i)
+    cap.graph.launch(stream)
+    stream.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record(stream)
+    cap.graph.launch(stream)
+    e1.record(stream)
+    stream.synchronize()
+    avg_us = e0.elapsed_ms(e1) * 1000.0 / steps
+    nbytes = weight_bytes("q6_k", M, K) + 4 * K + 4
+    idx = int(ob.download(np.uint32, 1, stream=stream)[0])
+    cap.graph.destroy()
+    for b in wbufs + [xb, pv, pi, ob]:
+        b.free()
+    e0.destroy()
+    e1.destroy()
+    stream.destroy()
+    return {"M": M, "K": K, "copies": copies, "bytes_per_call": nbytes, "us_per_call": avg_us,
+            "GBps": nbytes / (avg_us * 1e-6) / 1e9,
+            "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "launches_per_call": 2, "index": idx}
 
 
 def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
@@ -451,6 +505,15 @@ def main() -> int:
         results[name] = r
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
             f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s); eager {r['us_per_call_eager']:.2f} us")
+
+    for name, M, K, cfg in TOP1_WORKLOADS:
+        if args.workloads not in ("all",) and name not in args.workloads.split(","):
+            continue
+        log(f"{name}: running")
+        r = bench_top1(ctx, M, K, cfg, max(20, args.steps // 2), min(args.warmup, 5))
+        results[name] = r
+        log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
+            f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s), row {r['index']}")
 
     for name, fmt, T, N, K, cfg in GEMM_WORKLOADS:
         if args.workloads not in ("all",) and name not in args.workloads.split(","):

@@ -99,6 +99,8 @@ SIGNATURES = {
                   er_buffer, _u32, _u32, _u32, _u32]),
     "er_hip_encode_q4k_weights_dual_geglu": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q6k_weights_packed_top1": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
     "er_hip_encode_batched_q4k_weights": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
     "er_hip_encode_batched_q6k_weights": (

@@ -371,6 +371,95 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
     }
 }
 
+// ---------------------------------------------------------------------------
+// Greedy top-1 over a Q6_K head (the reference's q6_k_gemv_packed_4row_top1_f32
+// + q6_k_top1_reduce, Dequant_Q6_K.metal:196-365).  Selection rule, kept
+// exactly: each 4-row quad's candidate is row 4t, replaced by a later row of
+// the quad only when strictly larger (so a NaN in row 4t makes the quad's
+// candidate NaN); candidates then merge from (-inf, 0), a candidate winning
+// when larger, or equal with a lower row index.  That merge is the minimum
+// under the order (-value, index) with NaN candidates never taken, so the
+// result does not depend on how the merge tree is shaped: each workgroup
+// merges its quads into one (value, row) partial, and er_top1_reduce merges
+// the partials.
+
+// (v, i) <- (ov, oi) when ov is larger, or equal with a lower index.
+ER_DEV void top1_merge(float &v, uint32_t &i, float ov, uint32_t oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+ER_DEV void top1_wave_merge(float &v, uint32_t &i) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const uint32_t oi = (uint32_t)__shfl_xor((int)i, off, 64);
+        top1_merge(v, i, ov, oi);
+    }
+}
+
+// Workgroup epilogue: RPW row values of this workgroup (rows blockIdx.x * RPW
+// + [0, RPW), RPW a multiple of 4, M a multiple of 4) -> partial
+// (pv, pi)[blockIdx.x].  `mine` lanes hold acc[0..R) for local rows
+// base + [0, R).
+template <uint32_t RPW>
+ER_DEV void top1_epilogue(const float *acc, int R, uint32_t base, bool mine, uint32_t M,
+                          float *__restrict__ pv, uint32_t *__restrict__ pi) {
+    __shared__ float tv[RPW];
+    if (mine)
+        for (int r = 0; r < R; ++r) tv[base + (uint32_t)r] = acc[r];
+    __syncthreads();
+    if (threadIdx.x < 64u) {
+        const uint32_t first = blockIdx.x * RPW;
+        float bv = -__builtin_inff();
+        uint32_t bi = 0;
+        for (uint32_t q = threadIdx.x; q < RPW / 4u; q += 64u) {
+            const uint32_t r0 = first + 4u * q;
+            if (r0 < M) {
+                float v = tv[4u * q];
+                uint32_t i = r0;
+#pragma unroll
+                for (uint32_t k = 1; k < 4; ++k)
+                    if (tv[4u * q + k] > v) {
+                        v = tv[4u * q + k];
+                        i = r0 + k;
+                    }
+                top1_merge(bv, bi, v, i);
+            }
+        }
+        top1_wave_merge(bv, bi);
+        if (threadIdx.x == 0) {
+            pv[blockIdx.x] = bv;
+            pi[blockIdx.x] = bi;
+        }
+    }
+}
+
+// One workgroup of 256 lanes: merges `count` partials into out[0].
+extern "C" __global__ void __launch_bounds__(256)
+    er_top1_reduce(const float *__restrict__ pv, const uint32_t *__restrict__ pi,
+                   uint32_t *__restrict__ out, uint32_t count) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    float bv = -__builtin_inff();
+    uint32_t bi = 0;
+    for (uint32_t t = threadIdx.x; t < count; t += 256u) top1_merge(bv, bi, pv[t], pi[t]);
+    top1_wave_merge(bv, bi);
+    if ((threadIdx.x & 63u) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        bv = sv[0];
+        bi = si[0];
+        for (int w = 1; w < 4; ++w) top1_merge(bv, bi, sv[w], si[w]);
+        out[0] = bi;
+    }
+}
+
 // Q6_K slot s of a row = super-block b = s/4, half h = (s/2)%2, lane chunk
 // c = s%2: ql bytes [64h+16c, +16) (q1 low / q3 high nibbles) and
 // [64h+32+16c, +16) (q2 / q4), qh bytes [128+32h+16c, +16) (2 high bits of
@@ -379,9 +468,10 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
 // 64-groups 4b+2h (m < 2) and 4b+2h+1.  Blocks are 2-byte aligned: the
 // fields are fetched with the aligned-window loads (ld16_a2 / ld8_a2).
 // Value = d * sc * (q6 - 32): the -32 is applied through the x chunk sums.
-template <int LPR, int NS, int R>
+template <int LPR, int NS, int R, bool TOP1 = false>
 ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                        float *__restrict__ y, uint32_t M, uint32_t K) {
+                        float *__restrict__ y, uint32_t M, uint32_t K,
+                        float *__restrict__ pv = nullptr, uint32_t *__restrict__ pi = nullptr) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     using C = I8Cfg<LPR, NS>;
     constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
@@ -476,7 +566,9 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    if (li == 0) {
+    if constexpr (TOP1) {
+        top1_epilogue<ER_GEMV_WAVES * C::G * R>(acc, R, (wave * C::G + g) * R, li == 0, M, pv, pi);
+    } else if (li == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
             if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
@@ -819,6 +911,7 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
 // ---------------------------------------------------------------------------
 // Entry points (extern "C" so hipModuleGetFunction resolves them by name).
 //   er_gemv_<fmt>_i8_l<LPR>_n<NS>_r<R> : integer-dot family (er_gemv_cfg.h; q4k, q8_0, q6k)
+//   er_gemv_q6k_top1_l<LPR>_n<NS>_r<R> : Q6_K with the top-1 partial epilogue
 //   er_gemv_<fmt>_l<LPR>_<s|g>         : fp32 family, x staged in LDS (s) or
 //                                        read from global memory (g)
 // ---------------------------------------------------------------------------
@@ -840,6 +933,13 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
                                              const float *__restrict__ x,                     \
                                              float *__restrict__ y, uint32_t M, uint32_t K) { \
         gemv_q6k_i8<LPR, NS, R>(W, x, y, M, K);                                              \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q6k_top1_l##LPR##_n##NS##_r##R(const uint8_t *__restrict__ W,                \
+                                               const float *__restrict__ x,                   \
+                                               float *__restrict__ pv, uint32_t *__restrict__ pi, \
+                                               uint32_t M, uint32_t K) {                      \
+        gemv_q6k_i8<LPR, NS, R, true>(W, x, nullptr, M, K, pv, pi);                          \
     }
 ER_I8_CONFIGS(ER_I8_ENTRY)
 

@@ -62,6 +62,7 @@ er_status fail(er_status st, const char *fmt, ...) {
     X(GEMMP_Q4K_T64, "er_gemmp_q4k_t64")                                               \
     X(GEMMP_Q8_0_T64, "er_gemmp_q8_0_t64")                                             \
     X(FILL_ZERO, "er_fill_zero")                                                       \
+    X(TOP1_REDUCE, "er_top1_reduce")                                                   \
     X(GEMMP_Q4K_T128, "er_gemmp_q4k_t128")                                             \
     X(GEMMP_Q4K_T256, "er_gemmp_q4k_t256")                                             \
     X(GEMMP_Q8_0_T128, "er_gemmp_q8_0_t128")                                           \
@@ -121,6 +122,7 @@ struct er_hip_ctx {
     hipFunction_t fnQ4KI8[kI8Count] = {};
     hipFunction_t fnQ8I8[kI8Count] = {};
     hipFunction_t fnQ6KI8[kI8Count] = {};
+    hipFunction_t fnQ6KTop1[kI8Count] = {};
     hipFunction_t fnQ4KMulti[kI8MultiCount] = {};
     hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
     int cu_count = 0;
@@ -274,8 +276,8 @@ const char *fmt_name(Fmt f) {
 
 // validateKQuantInputShape (GEMVKernel.swift:1415-1432) plus the buffer-length
 // guard of encodeKQuantWeights / encodeBatchedKQuantWeights (:1296-1300, :1339-1344).
-er_status validate_gemv(Fmt f, er_buffer W, er_buffer x, er_buffer y, uint32_t batch, uint32_t M,
-                        uint32_t K) {
+er_status validate_gemv_shape(Fmt f, er_buffer W, uint64_t xLen, uint64_t yLen, uint32_t batch,
+                              uint32_t M, uint32_t K) {
     const uint32_t bw = block_weights(f);
     if (K == 0 || K % bw != 0)
         return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s GEMV: K=%u must be a positive multiple of %u",
@@ -286,12 +288,19 @@ er_status validate_gemv(Fmt f, er_buffer W, er_buffer x, er_buffer y, uint32_t b
                     "%s GEMV: weight buffer holds %llu bytes, M=%u K=%u needs %llu", fmt_name(f),
                     (unsigned long long)W.length, M, K, (unsigned long long)expected);
     if (batch == 0) return fail(ER_ERR_ENCODING_FAILED, "%s GEMV: batchSeq must be > 0", fmt_name(f));
-    if (x.length < (uint64_t)batch * K * 4u || y.length < (uint64_t)batch * M * 4u)
+    if (xLen < (uint64_t)batch * K * 4u || yLen < (uint64_t)batch * M * 4u)
         return fail(ER_ERR_ENCODING_FAILED,
                     "%s GEMV: input %llu B / output %llu B too small for batch=%u M=%u K=%u",
-                    fmt_name(f), (unsigned long long)x.length, (unsigned long long)y.length, batch, M,
+                    fmt_name(f), (unsigned long long)xLen, (unsigned long long)yLen, batch, M,
                     K);
-    if (M == 0) return ER_OK;
+    return ER_OK;
+}
+
+// validate_gemv_shape, then the pointer rules of the kernels.
+er_status validate_gemv(Fmt f, er_buffer W, er_buffer x, er_buffer y, uint32_t batch, uint32_t M,
+                        uint32_t K) {
+    er_status st = validate_gemv_shape(f, W, x.length, y.length, batch, M, K);
+    if (st != ER_OK || M == 0) return st;
     if (!W.data || !x.data || !y.data)
         return fail(ER_ERR_INVALID_ARGUMENT, "%s GEMV: null buffer", fmt_name(f));
     if (!aligned(W.data, 16))
@@ -355,6 +364,56 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / lpr) * kQ6KRows;
     dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
     return launch(ctx, k, grid, dim3(kGemvThreads, 1, 1), lds, stream, args);
+}
+
+// Greedy top-1 over a Q6_K head (GEMVKernel.encodeQ6KWeightsPackedTop1,
+// GEMVKernel.swift:1205-1265): M % 4 == 0 (INVALID_MATRIX_SHAPE), then the
+// K-quant shape rules, then partial buffers of >= M/4 entries and a 4-byte
+// index buffer (ENCODING_FAILED).  Two launches: the integer-dot Q6_K GEMV
+// with the top-1 epilogue (one partial per workgroup, at most M/4 of them)
+// and er_top1_reduce.
+er_status encode_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buffer x,
+                          er_buffer pv, er_buffer pi, er_buffer out, uint32_t M, uint32_t K) {
+    if (M % 4u != 0)
+        return fail(ER_ERR_INVALID_MATRIX_SHAPE, "Q6_K top-1: M=%u must be a multiple of 4", M);
+    er_status st = validate_gemv_shape(Fmt::Q6_K, W, x.length, (uint64_t)M * 4u, 1, M, K);
+    if (st != ER_OK) return st;
+    const uint64_t partials = M / 4u;
+    if (pv.length < partials * 4u || pi.length < partials * 4u || out.length < 4u)
+        return fail(ER_ERR_ENCODING_FAILED,
+                    "Q6_K top-1: partial buffers %llu / %llu B and index buffer %llu B too small for M=%u",
+                    (unsigned long long)pv.length, (unsigned long long)pi.length,
+                    (unsigned long long)out.length, M);
+    st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!W.data || !x.data || !pv.data || !pi.data || !out.data)
+        return fail(ER_ERR_INVALID_ARGUMENT, "Q6_K top-1: null buffer");
+    if (!aligned(W.data, 16) || !aligned(x.data, 16) || !aligned(pv.data, 4) || !aligned(pi.data, 4) ||
+        !aligned(out.data, 4))
+        return fail(ER_ERR_INVALID_ARGUMENT,
+                    "Q6_K top-1: weight and input must be 16-byte, partial and index buffers 4-byte aligned");
+    const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+    if (K > kI8MaxK || lds + 1024u > ctx->info.lds_per_workgroup)
+        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "Q6_K top-1: K=%u exceeds the supported %u", K, kI8MaxK);
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    uint32_t count = 0;
+    if (M > 0) {
+        int ci = pick_i8(K / 64u, M, ctx->cu_count);
+        if (ctx->i8_override >= 0 && (uint32_t)kI8Cfg[ctx->i8_override].lpr *
+                                             kI8Cfg[ctx->i8_override].ns >= K / 64u)
+            ci = ctx->i8_override;
+        if (ci < 0) return fail(ER_ERR_INVALID_VECTOR_SHAPE, "Q6_K top-1: no configuration for K=%u", K);
+        const I8Cfg &c = kI8Cfg[ci];
+        const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
+        count = (M + rowsPerBlock - 1) / rowsPerBlock;
+        void *args[] = {&W.data, &x.data, &pv.data, &pi.data, &M, &K};
+        st = launch_fn(ctx->fnQ6KTop1[ci], "er_gemv_q6k_top1", dim3(count, 1, 1), dim3(kGemvThreads, 1, 1),
+                       lds, stream, args);
+        if (st != ER_OK) return st;
+    }
+    void *rargs[] = {&pv.data, &pi.data, &out.data, &count};
+    return launch(ctx, K_TOP1_REDUCE, dim3(1, 1, 1), dim3(256, 1, 1), 0, stream, rargs);
 }
 
 // Prefill GEMM: validation mirrors the GEMV rules (K multiple of the block,
@@ -581,11 +640,13 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
     }
     for (int i = 0; i < kI8Count; ++i) {
         char name[64];
-        static const char *const fmts[3] = {"q4k", "q8_0", "q6k"};
-        for (int fmt = 0; fmt < 3; ++fmt) {
-            std::snprintf(name, sizeof(name), "er_gemv_%s_i8_l%u_n%u_r%u", fmts[fmt],
+        static const char *const kinds[4] = {"q4k_i8", "q8_0_i8", "q6k_i8", "q6k_top1"};
+        hipFunction_t *const slots[4] = {&ctx->fnQ4KI8[i], &ctx->fnQ8I8[i], &ctx->fnQ6KI8[i],
+                                         &ctx->fnQ6KTop1[i]};
+        for (int fmt = 0; fmt < 4; ++fmt) {
+            std::snprintf(name, sizeof(name), "er_gemv_%s_l%u_n%u_r%u", kinds[fmt],
                           (unsigned)kI8Cfg[i].lpr, (unsigned)kI8Cfg[i].ns, (unsigned)kI8Cfg[i].r);
-            hipFunction_t *slot = fmt == 0 ? &ctx->fnQ4KI8[i] : (fmt == 1 ? &ctx->fnQ8I8[i] : &ctx->fnQ6KI8[i]);
+            hipFunction_t *slot = slots[fmt];
             e = hipModuleGetFunction(slot, ctx->module, name);
             if (e != hipSuccess) {
                 (void)hipModuleUnload(ctx->module);
@@ -914,6 +975,13 @@ er_status er_hip_encode_q4k_weights_dual_geglu(er_hip_ctx *ctx, er_stream stream
                                                er_buffer input, er_buffer output, uint32_t M,
                                                uint32_t K) {
     return encode_q4k_geglu(ctx, stream, gate_weight, up_weight, input, output, M, K);
+}
+
+er_status er_hip_encode_q6k_weights_packed_top1(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                                er_buffer input, er_buffer partial_values,
+                                                er_buffer partial_indices, er_buffer output_index,
+                                                uint32_t M, uint32_t K) {
+    return encode_q6k_top1(ctx, stream, weight, input, partial_values, partial_indices, output_index, M, K);
 }
 
 er_status er_hip_encode_batched_q4k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,

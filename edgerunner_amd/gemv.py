@@ -105,6 +105,40 @@ class GEMVKernel:
             self.ctx.handle, _sh(stream), gateWeightBuffer.raw, upWeightBuffer.raw,
             inputBuffer.raw, outputBuffer.raw, M, K))
 
+    @staticmethod
+    def q6KTop1PartialCount(rows: int) -> int:
+        """Entries each partial buffer of the top-1 head needs
+        (GEMVKernel.q6KTop1PartialCount, GEMVKernel.swift:50-52)."""
+        return (rows + 3) // 4
+
+    def encodeQ6KWeightsPackedTop1(self, stream: Optional[Stream], weightBuffer: Buffer,
+                                   inputBuffer: Buffer, partialValuesBuffer: Buffer,
+                                   partialIndicesBuffer: Buffer, outputIndexBuffer: Buffer,
+                                   M: int, K: int) -> None:
+        """GEMVKernel.encodeQ6KWeightsPackedTop1 (GEMVKernel.swift:1205-1265):
+        outputIndexBuffer[0] (uint32) = the row of the largest W.x value,
+        lowest row on ties."""
+        check(self.lib.er_hip_encode_q6k_weights_packed_top1(
+            self.ctx.handle, _sh(stream), weightBuffer.raw, inputBuffer.raw,
+            partialValuesBuffer.raw, partialIndicesBuffer.raw, outputIndexBuffer.raw, M, K))
+
+    def executeQ6KWeightsTop1(self, rawWeights, x, M: int, K: int) -> int:
+        """Uploads W and x, runs the top-1 head and returns the row index."""
+        xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        if xv.size != K:
+            raise InvalidVectorShape(f"x.count {xv.size} != K {K}")
+        ctx = self.ctx
+        n = self.q6KTop1PartialCount(M)
+        wb, xb = ctx.upload(_u8(rawWeights)), ctx.upload(xv)
+        pv, pi, ob = ctx.alloc(max(4, 4 * n)), ctx.alloc(max(4, 4 * n)), ctx.alloc(4)
+        try:
+            self.encodeQ6KWeightsPackedTop1(None, wb, xb, pv, pi, ob, M, K)
+            ctx.synchronize()
+            return int(ob.download(np.uint32, 1)[0])
+        finally:
+            for b in (wb, xb, pv, pi, ob):
+                b.free()
+
     def executeQ4KWeightsMulti(self, rawWeights: list, x, rows: list, K: int, geglu: bool = False):
         """Uploads 2 or 3 Q4_K matrices sharing x and runs the dual / triple
         (or, with geglu=True and two equal-height matrices, the fused GeGLU)

@@ -204,6 +204,21 @@ er_status er_hip_encode_q4k_weights_dual_geglu(er_hip_ctx *ctx, er_stream stream
                                                er_buffer input, er_buffer output, uint32_t M,
                                                uint32_t K);
 
+/* ---- greedy top-1 over a Q6_K head ----
+ * GEMVKernel.encodeQ6KWeightsPackedTop1 (GEMVKernel.swift:1205-1265; kernels
+ * q6_k_gemv_packed_4row_top1_f32 + q6_k_top1_reduce, Dequant_Q6_K.metal:196-365).
+ * output_index[0] = the row of the largest W.x value, lowest row on ties (the
+ * reference's rule, NaN handling included).  M % 4 == 0 else
+ * INVALID_MATRIX_SHAPE; K rules as er_hip_encode_q6k_weights; partial_values
+ * and partial_indices of >= M/4 fp32 / uint32 entries (q6KTop1PartialCount,
+ * GEMVKernel.swift:50-52) and output_index >= 4 bytes, else ENCODING_FAILED.
+ * The partial buffers are scratch; their contents afterwards are unspecified.
+ * K <= 16384 (else INVALID_VECTOR_SHAPE). */
+er_status er_hip_encode_q6k_weights_packed_top1(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                                er_buffer input, er_buffer partial_values,
+                                                er_buffer partial_indices, er_buffer output_index,
+                                                uint32_t M, uint32_t K);
+
 /* ---- batched (token-axis) GEMV: y[t*M + r] = W[r,:] . x[t*K : (t+1)*K] ----
  * GEMVKernel.encodeBatchedQ4KWeights (GEMVKernel.swift:682-702, validation
  * :1319-1361: batchSeq > 0, input >= batchSeq*K*4, output >= batchSeq*M*4 else

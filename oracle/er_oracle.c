@@ -21,6 +21,8 @@
  *   - quantize_q8_0_rows: closed-form checks (max |v| maps to +-127, rint
  *     ties-to-even, zero rows) and round-trip error bound.
  *   - argmax: brute force with lowest-index ties.
+ *   - top1: equals argmax on finite values (brute force); hand-derived
+ *     answers for NaN candidates and all -inf inputs.
  *   - xoshiro256** / splitmix64: published reference outputs.
  */
 #include <math.h>
@@ -544,6 +546,30 @@ uint32_t er_ref_argmax(const float *v, uint32_t n) {
     for (uint32_t i = 1; i < n; ++i)
         if (v[i] > v[best]) best = i;
     return best;
+}
+
+/* Greedy top-1 as q6_k_gemv_packed_4row_top1_f32 + q6_k_top1_reduce
+ * (Dequant_Q6_K.metal:196-365): per 4-row quad, start from row 4t and take a
+ * later row only when strictly larger (Dequant_Q6_K.metal:298-311); then a
+ * serial merge of the quad candidates from (-inf, 0), a candidate winning
+ * when larger or equal with a lower index (:327, :338).  n % 4 == 0. */
+uint32_t er_ref_top1(const float *v, uint32_t n) {
+    float best = -INFINITY;
+    uint32_t bestIdx = 0;
+    for (uint32_t t = 0; t + 3 < n; t += 4) {
+        float cv = v[t];
+        uint32_t ci = t;
+        for (uint32_t k = 1; k < 4; ++k)
+            if (v[t + k] > cv) {
+                cv = v[t + k];
+                ci = t + k;
+            }
+        if (cv > best || (cv == best && ci < bestIdx)) {
+            best = cv;
+            bestIdx = ci;
+        }
+    }
+    return bestIdx;
 }
 
 int er_ref_max_threads(void) {

@@ -63,6 +63,8 @@ def load():
     lib.er_ref_gelu_tanh.restype = C.c_float
     lib.er_ref_argmax.argtypes = [f32p, C.c_uint32]
     lib.er_ref_argmax.restype = C.c_uint32
+    lib.er_ref_top1.argtypes = [f32p, C.c_uint32]
+    lib.er_ref_top1.restype = C.c_uint32
     lib.er_ref_max_threads.argtypes = []
     lib.er_ref_max_threads.restype = C.c_int
     _lib = lib
@@ -151,6 +153,13 @@ def gelu_tanh(v) -> np.ndarray:
 def argmax(v) -> int:
     a, ap = _f32(v)
     return int(load().er_ref_argmax(ap, a.size))
+
+
+def top1(v) -> int:
+    """Row chosen by the reference's two-stage top-1 (len(v) % 4 == 0)."""
+    a, ap = _f32(v)
+    assert a.size % 4 == 0
+    return int(load().er_ref_top1(ap, a.size))
 
 
 def f16_to_f32(h: int) -> float:

@@ -145,3 +145,33 @@ def test_gelu_tanh_oracle():
     assert np.array_equal(ref.gelu_tanh(big), big)
     assert np.all(ref.gelu_tanh(-big) == 0.0)
     assert ref.gelu_tanh([0.0])[0] == 0.0
+
+
+def test_top1_oracle_equals_argmax_on_finite_values():
+    """The reference's two-stage top-1 (quad candidates, then a merge that
+    prefers lower indices on ties) picks numpy's argmax (first maximum) for
+    finite inputs, ties included."""
+    rng = np.random.default_rng(7)
+    for n in (4, 8, 12, 64, 1000, 4096):
+        v = rng.standard_normal(n).astype(np.float32)
+        assert ref.top1(v) == int(np.argmax(v))
+        w = np.round(v * 2).astype(np.float32)  # many ties
+        assert ref.top1(w) == int(np.argmax(w))
+    v = np.zeros(16, np.float32)
+    assert ref.top1(v) == 0
+    v[[6, 9, 13]] = 3.0
+    assert ref.top1(v) == 6
+
+
+def test_top1_oracle_nan_and_infinity_rules():
+    """Hand-derived from the kernels' comparisons: a NaN in a quad's first row
+    makes the quad's candidate NaN, which never wins the merge; a NaN later in
+    a quad is skipped; with every candidate -inf the merge keeps its start
+    value (-inf, row 0)."""
+    nan, inf = float("nan"), float("inf")
+    assert ref.top1([nan, 9, 9, 9, 1, 2, 3, 0]) == 6     # quad 0 dropped
+    assert ref.top1([1, nan, 5, 2, 0, 0, 0, 0]) == 2     # NaN skipped inside the quad
+    assert ref.top1([nan] * 8) == 0
+    assert ref.top1([-inf] * 8) == 0
+    assert ref.top1([-inf, -inf, -inf, -inf, -inf, -5.0, -inf, -inf]) == 5
+    assert ref.top1([0, 0, 0, 0, inf, 0, 0, inf]) == 4
