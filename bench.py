@@ -58,6 +58,12 @@ TOP1_WORKLOADS = [
     ("q6_k_top1_128256x4096", 128256, 4096, 3),
 ]
 
+# Q8_0 row quantizer: (name, rows, row length, BASELINE config index)
+QUANT_WORKLOADS = [
+    ("q8_0_quantize_512x4096", 512, 4096, 4),
+    ("q8_0_quantize_8192x4096", 8192, 4096, 4),
+]
+
 # (name, fmt, T tokens, N, K, BASELINE config index)
 GEMM_WORKLOADS = [
     ("q4_k_gemm_512x4096x4096", "q4_k", 512, 4096, 4096, 4),
@@ -186,6 +192,45 @@ def bench_top1(ctx, M: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
             "GBps": nbytes / (avg_us * 1e-6) / 1e9,
             "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "launches_per_call": 2, "index": idx}
+
+
+def bench_quant(ctx, rows: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
+    """Q8_0 row quantizer over `rows` fp32 rows of K values, rotating source
+    copies, in a HIP graph.  Bytes per call: 4 per value read + 34 per block
+    written."""
+    import edgerunner_amd.synth as synth
+    from edgerunner_amd import Capture, QuantizeQ8RowsKernel
+
+    qk = QuantizeQ8RowsKernel(ctx)
+    src = synth.normal_f32(synth.seed(cfg, 9), rows * K)
+    copies = max(2, -(-ROTATE_BYTES // src.nbytes))
+    stream = ctx.stream()
+    sbufs = [ctx.upload(src, stream) for _ in range(copies)]
+    db = ctx.alloc(rows * (K // 32) * 34)
+    for i in range(warmup):
+        qk.encode(stream, sbufs[i % copies], db, rows, K, 0, K // 32)
+    stream.synchronize()
+    with Capture(ctx, stream) as cap:
+        for i in range(steps):
+            qk.encode(stream, sbufs[i % copies], db, rows, K, 0, K // 32)
+    cap.graph.launch(stream)
+    stream.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record(stream)
+    cap.graph.launch(stream)
+    e1.record(stream)
+    stream.synchronize()
+    avg_us = e0.elapsed_ms(e1) * 1000.0 / steps
+    nbytes = rows * K * 4 + rows * (K // 32) * 34
+    cap.graph.destroy()
+    for b in sbufs + [db]:
+        b.free()
+    e0.destroy()
+    e1.destroy()
+    stream.destroy()
+    return {"rows": rows, "K": K, "copies": copies, "bytes_per_call": nbytes, "us_per_call": avg_us,
+            "GBps": nbytes / (avg_us * 1e-6) / 1e9,
+            "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
 def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
@@ -514,6 +559,15 @@ def main() -> int:
         results[name] = r
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
             f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s), row {r['index']}")
+
+    for name, rows, K, cfg in QUANT_WORKLOADS:
+        if args.workloads not in ("all",) and name not in args.workloads.split(","):
+            continue
+        log(f"{name}: running")
+        r = bench_quant(ctx, rows, K, cfg, max(20, args.steps // 2), min(args.warmup, 5))
+        results[name] = r
+        log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
+            f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s)")
 
     for name, fmt, T, N, K, cfg in GEMM_WORKLOADS:
         if args.workloads not in ("all",) and name not in args.workloads.split(","):

@@ -10,11 +10,11 @@ from .runtime import (AllocationFailed, Buffer, Capture, Context, Graph, Dequant
                       InvalidArgument, InvalidBlockDataCount, InvalidMatrixShape,
                       InvalidVectorShape, LibraryNotFound, Stream, default_context)
 from .gemv import (DequantQ4KMKernel, DequantQ6KKernel, DequantQ8_0Kernel,  # noqa: F401
-                   GEMVKernel, QuantGEMMKernel, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0)
+                   GEMVKernel, QuantGEMMKernel, QuantizeQ8RowsKernel, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0)
 
 __all__ = [
     "Context", "Buffer", "Stream", "Event", "Graph", "Capture", "default_context",
-    "GEMVKernel", "QuantGEMMKernel", "DequantQ8_0Kernel", "DequantQ4KMKernel", "DequantQ6KKernel",
+    "GEMVKernel", "QuantGEMMKernel", "QuantizeQ8RowsKernel", "DequantQ8_0Kernel", "DequantQ4KMKernel", "DequantQ6KKernel",
     "GEMVError", "DequantKernelError", "EdgeRunnerHIPError",
     "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q6_K",
 ]

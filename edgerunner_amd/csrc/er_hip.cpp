@@ -63,6 +63,8 @@ er_status fail(er_status st, const char *fmt, ...) {
     X(GEMMP_Q8_0_T64, "er_gemmp_q8_0_t64")                                             \
     X(FILL_ZERO, "er_fill_zero")                                                       \
     X(TOP1_REDUCE, "er_top1_reduce")                                                   \
+    X(QUANT_Q8_0_V, "er_quantize_q8_0_rows_v")                                         \
+    X(QUANT_Q8_0_S, "er_quantize_q8_0_rows_s")                                         \
     X(GEMMP_Q4K_T128, "er_gemmp_q4k_t128")                                             \
     X(GEMMP_Q4K_T256, "er_gemmp_q4k_t256")                                             \
     X(GEMMP_Q8_0_T128, "er_gemmp_q8_0_t128")                                           \
@@ -414,6 +416,41 @@ er_status encode_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buf
     }
     void *rargs[] = {&pv.data, &pi.data, &out.data, &count};
     return launch(ctx, K_TOP1_REDUCE, dim3(1, 1, 1), dim3(256, 1, 1), 0, stream, rargs);
+}
+
+// Q8_0 row quantizer (quantize_q8_0_rows, Dequant_Q8_0.metal:19-49, encoded
+// by LlamaLanguageModel.encodeQ8Rows, LlamaLanguageModel.swift:1820-1850).
+// The reference dispatches it without checks; here the source and destination
+// extents the parameters imply must fit the buffers (ENCODING_FAILED), so no
+// launch can touch memory outside them.
+er_status encode_quantize_q8_0(er_hip_ctx *ctx, er_stream stream, er_buffer src, er_buffer dst,
+                               uint32_t rowCount, uint32_t srcStride, uint32_t dstRowBase,
+                               uint32_t blocksPerRow) {
+    if (rowCount == 0 || blocksPerRow == 0) return check_ctx(ctx);
+    const uint64_t srcNeed = ((uint64_t)(rowCount - 1u) * srcStride + (uint64_t)blocksPerRow * 32u) * 4u;
+    const uint64_t dstNeed = ((uint64_t)dstRowBase + rowCount) * blocksPerRow * 34u;
+    if (src.length < srcNeed || dst.length < dstNeed)
+        return fail(ER_ERR_ENCODING_FAILED,
+                    "quantize_q8_0_rows: source %llu B (needs %llu) / destination %llu B (needs %llu)",
+                    (unsigned long long)src.length, (unsigned long long)srcNeed,
+                    (unsigned long long)dst.length, (unsigned long long)dstNeed);
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!src.data || !dst.data) return fail(ER_ERR_INVALID_ARGUMENT, "quantize_q8_0_rows: null buffer");
+    if (!aligned(src.data, 4) || !aligned(dst.data, 2))
+        return fail(ER_ERR_INVALID_ARGUMENT,
+                    "quantize_q8_0_rows: source must be 4-byte and destination 2-byte aligned");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    const bool vec = aligned(src.data, 16) && srcStride % 4u == 0;
+    const uint64_t blocks = (uint64_t)rowCount * blocksPerRow;
+    if (blocks >= (1ull << 32))
+        return fail(ER_ERR_ENCODING_FAILED, "quantize_q8_0_rows: %llu blocks exceed 2^32 - 1",
+                    (unsigned long long)blocks);
+    const uint64_t wgs = std::min<uint64_t>((blocks + 31u) / 32u, 8192u);  // 32 blocks per pass
+    void *args[] = {&src.data, &dst.data, &rowCount, &srcStride, &dstRowBase, &blocksPerRow};
+    return launch(ctx, vec ? K_QUANT_Q8_0_V : K_QUANT_Q8_0_S, dim3((uint32_t)wgs, 1, 1), dim3(256, 1, 1), 0,
+                  stream, args);
 }
 
 // Prefill GEMM: validation mirrors the GEMV rules (K multiple of the block,
@@ -982,6 +1019,14 @@ er_status er_hip_encode_q6k_weights_packed_top1(er_hip_ctx *ctx, er_stream strea
                                                 er_buffer partial_indices, er_buffer output_index,
                                                 uint32_t M, uint32_t K) {
     return encode_q6k_top1(ctx, stream, weight, input, partial_values, partial_indices, output_index, M, K);
+}
+
+er_status er_hip_quantize_q8_0_rows(er_hip_ctx *ctx, er_stream stream, er_buffer source,
+                                    er_buffer destination, uint32_t row_count,
+                                    uint32_t source_row_stride, uint32_t destination_row_base,
+                                    uint32_t blocks_per_row) {
+    return encode_quantize_q8_0(ctx, stream, source, destination, row_count, source_row_stride,
+                                destination_row_base, blocks_per_row);
 }
 
 er_status er_hip_encode_batched_q4k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,

@@ -4,3 +4,4 @@
 #include "er_dequant.hip"
 #include "er_gemv.hip"
 #include "er_gemm.hip"
+#include "er_quant.hip"

@@ -335,3 +335,40 @@ class QuantGEMMKernel:
             wb.free()
             xb.free()
             yb.free()
+
+
+class QuantizeQ8RowsKernel:
+    """Q8_0 row quantizer: the reference's `quantize_q8_0_rows` pipeline as
+    LlamaLanguageModel.encodeQ8Rows encodes it (LlamaLanguageModel.swift:1820-1850,
+    kernel Dequant_Q8_0.metal:19-49).  encode appends to a stream;
+    execute allocates, runs, waits and returns the destination bytes."""
+
+    def __init__(self, ctx: Optional[Context] = None):
+        self.ctx = ctx or default_context()
+        self.lib = self.ctx.lib
+
+    def encode(self, stream: Optional[Stream], sourceBuffer: Buffer, destinationBuffer: Buffer,
+               rowCount: int, sourceRowStride: int, destinationRowBase: int,
+               blocksPerRow: int) -> None:
+        check(self.lib.er_hip_quantize_q8_0_rows(self.ctx.handle, _sh(stream), sourceBuffer.raw,
+                                                 destinationBuffer.raw, rowCount, sourceRowStride,
+                                                 destinationRowBase, blocksPerRow))
+
+    def execute(self, source, rowCount: int, sourceRowStride: int, destinationRowBase: int,
+                blocksPerRow: int, destination=None) -> np.ndarray:
+        """source: fp32 values; destination: optional existing Q8_0 bytes whose
+        rows outside [destinationRowBase, +rowCount) are kept."""
+        src = np.ascontiguousarray(source, dtype=np.float32).reshape(-1)
+        nbytes = (destinationRowBase + rowCount) * blocksPerRow * Q8_0_BLOCK_BYTES
+        dst = (np.zeros(nbytes, np.uint8) if destination is None
+               else np.ascontiguousarray(destination, dtype=np.uint8).reshape(-1))
+        ctx = self.ctx
+        sb = ctx.upload(src) if src.size else ctx.alloc(4)
+        db = ctx.upload(dst) if dst.size else ctx.alloc(2)
+        try:
+            self.encode(None, sb, db, rowCount, sourceRowStride, destinationRowBase, blocksPerRow)
+            ctx.synchronize()
+            return db.download(np.uint8, dst.size) if dst.size else dst
+        finally:
+            sb.free()
+            db.free()

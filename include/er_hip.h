@@ -219,6 +219,21 @@ er_status er_hip_encode_q6k_weights_packed_top1(er_hip_ctx *ctx, er_stream strea
                                                 er_buffer partial_indices, er_buffer output_index,
                                                 uint32_t M, uint32_t K);
 
+/* ---- Q8_0 row quantizer ----
+ * Kernel quantize_q8_0_rows with ERQuantizeQ8RowsParams{rowCount,
+ * sourceRowStride, destinationRowBase, blocksPerRow} (Dequant_Q8_0.metal:9-49),
+ * as encoded by LlamaLanguageModel.encodeQ8Rows (LlamaLanguageModel.swift:1820-1850):
+ * fp32 source rows (stride in floats) -> Q8_0 blocks of destination rows
+ * destination_row_base + r.  Per block: scale = maxAbs/127, d = fp16(scale),
+ * q = clamp(rint(v/scale), -127, 127).  source must hold
+ * ((row_count-1)*stride + blocks_per_row*32) floats and destination
+ * (destination_row_base + row_count)*blocks_per_row*34 bytes, else
+ * ENCODING_FAILED; source 4-byte and destination 2-byte aligned. */
+er_status er_hip_quantize_q8_0_rows(er_hip_ctx *ctx, er_stream stream, er_buffer source,
+                                    er_buffer destination, uint32_t row_count,
+                                    uint32_t source_row_stride, uint32_t destination_row_base,
+                                    uint32_t blocks_per_row);
+
 /* ---- batched (token-axis) GEMV: y[t*M + r] = W[r,:] . x[t*K : (t+1)*K] ----
  * GEMVKernel.encodeBatchedQ4KWeights (GEMVKernel.swift:682-702, validation
  * :1319-1361: batchSeq > 0, input >= batchSeq*K*4, output >= batchSeq*M*4 else
