@@ -233,6 +233,38 @@ def bench_quant(ctx, rows: int, K: int, cfg: int, steps: int, warmup: int) -> di
             "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_gguf_upload(ctx, gib: float, reps: int = 3) -> dict:
+    """GGUF file -> HBM: writes a synthetic GGUF of `gib` GiB (random Q4_K
+    bytes) to a temporary file, opens it (map + parse + checks) and times
+    er_hip_gguf_upload of its data section.  Host-to-device over PCIe:
+    page-cache reads, pinned staging, DMA."""
+    import tempfile
+    from edgerunner_amd.gguf import GGUFLoader, GGUFMetadataValueType as VT, GGUFTensorType as TT
+    from edgerunner_amd.gguf import write_gguf
+
+    rows = int(gib * (1 << 30)) // (16 * 144)  # 4096-column Q4_K rows
+    payload = np.random.default_rng(7).integers(0, 256, size=rows * 16 * 144, dtype=np.uint8)
+    with tempfile.TemporaryDirectory() as d:
+        path = write_gguf(Path(d) / "synthetic.gguf", [("general.architecture", VT.string, "llama")],
+                          [("blk.0.ffn_up.weight", [4096, rows], TT.q4_K, payload.tobytes())])
+        del payload
+        t0 = time.perf_counter()
+        loader = GGUFLoader(path)
+        open_s = time.perf_counter() - t0
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            w = loader.load(ctx)
+            times.append(time.perf_counter() - t0)
+            loader.deviceData.free()
+            del w
+        off, n = loader.dataSection()
+        loader.close()
+    best = min(times)
+    return {"bytes": n, "open_ms": open_s * 1e3, "upload_ms": best * 1e3,
+            "GBps": n / best / 1e9, "reps": reps}
+
+
 def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
     """Prefill GEMM: `steps` launches over rotating weight copies, recorded
     into a HIP graph and replayed between HIP events (as bench_gemv)."""
@@ -577,6 +609,13 @@ def main() -> int:
         results[name] = r
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['TFLOPs']:.1f} TFLOP/s "
             f"({100 * r['frac_of_mfma_bf16_peak']:.1f}% of bf16 dense peak)")
+
+    if args.workloads == "all" or "gguf_upload" in args.workloads:
+        log("gguf_upload_1gib: running")
+        r = bench_gguf_upload(ctx, 1.0)
+        results["gguf_upload_1gib"] = r
+        log(f"gguf_upload_1gib: open {r['open_ms']:.1f} ms, upload {r['upload_ms']:.1f} ms, "
+            f"{r['GBps']:.1f} GB/s host-to-HBM")
 
     if args.workloads in ("all", "chain") or "decode_chain" in args.workloads:
         log("decode_chain: running")

@@ -24,6 +24,13 @@ STATUS_NAMES = {
     7: "allocationFailed",
     8: "invalidArgument",
     9: "deviceError",
+    10: "fileNotFound",
+    11: "invalidFormat",
+    12: "unsupportedVersion",
+    13: "unsupportedDataType",
+    14: "mmapFailed",
+    15: "missingMetadata",
+    16: "tensorNotFound",
 }
 
 
@@ -38,6 +45,33 @@ class er_tensor_storage(C.Structure):
         ("data_type", C.c_uint32),
         ("ndim", C.c_uint32),
         ("shape", C.c_uint64 * 4),
+    ]
+
+
+class er_gguf_value(C.Structure):
+    _fields_ = [
+        ("type", C.c_uint32),
+        ("elem_type", C.c_uint32),
+        ("count", C.c_uint64),
+        ("u", C.c_uint64),
+        ("i", C.c_int64),
+        ("f", C.c_double),
+        ("str", C.c_void_p),   # count bytes of UTF-8 (may hold NULs)
+        ("node", C.c_void_p),
+    ]
+
+
+class er_gguf_tensor_info(C.Structure):
+    _fields_ = [
+        ("name", C.c_char_p),
+        ("ndim", C.c_uint32),
+        ("ggml_type", C.c_uint32),
+        ("dims", C.c_uint64 * 8),
+        ("offset", C.c_uint64),
+        ("element_count", C.c_uint64),
+        ("byte_count", C.c_uint64),
+        ("data_type", C.c_uint32),
+        ("reserved", C.c_uint32),
     ]
 
 
@@ -111,6 +145,25 @@ SIGNATURES = {
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
     "er_hip_gemm_q4_k": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
     "er_hip_gemm_q8_0": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
+    "er_gguf_parse_memory": (C.c_int, [C.c_void_p, C.c_uint64, _u32, C.POINTER(C.c_void_p)]),
+    "er_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "er_gguf_close": (None, [C.c_void_p]),
+    "er_gguf_header": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                                 C.POINTER(C.c_uint64)]),
+    "er_gguf_metadata_count": (C.c_uint64, [C.c_void_p]),
+    "er_gguf_metadata_key": (C.c_int, [C.c_void_p, C.c_uint64, C.POINTER(C.c_char_p)]),
+    "er_gguf_metadata_value": (C.c_int, [C.c_void_p, C.c_uint64, C.POINTER(er_gguf_value)]),
+    "er_gguf_find_metadata": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "er_gguf_array_get": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(er_gguf_value)]),
+    "er_gguf_tensor_count": (C.c_uint64, [C.c_void_p]),
+    "er_gguf_tensor_info_at": (C.c_int, [C.c_void_p, C.c_uint64, C.POINTER(er_gguf_tensor_info)]),
+    "er_gguf_find_tensor": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "er_gguf_data_section": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "er_gguf_tensor_host_data": (C.c_int, [C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p),
+                                           C.POINTER(C.c_uint64)]),
+    "er_hip_gguf_upload": (C.c_int, [_ctx_p, _stream, C.c_void_p, C.POINTER(er_buffer)]),
+    "er_gguf_tensor_storage": (C.c_int, [C.c_void_p, C.c_uint64, er_buffer,
+                                         C.POINTER(er_tensor_storage)]),
     "er_hip_encode_projection": (
         C.c_int, [_ctx_p, _stream, C.POINTER(er_tensor_storage), er_buffer, er_buffer, _u32]),
 }

@@ -67,11 +67,13 @@ def build_host_library(code_object: Path = CODE_OBJECT, out: Path = LIB) -> Path
     blob_o = BUILD / "er_blob.o"
     host_o = BUILD / "er_hip.o"
     _run(["gcc", "-c", str(blob), "-o", str(blob_o)])
-    _run(["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
-          "-I", str(ROCM / "include"), "-I", str(ROOT / "include"), "-I", str(CSRC),
-          "-c", str(CSRC / "er_hip.cpp"), "-o", str(host_o)])
+    gguf_o = BUILD / "er_gguf.o"
+    for src, obj in ((CSRC / "er_hip.cpp", host_o), (CSRC / "er_gguf.cpp", gguf_o)):
+        _run(["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+              "-I", str(ROCM / "include"), "-I", str(ROOT / "include"), "-I", str(CSRC),
+              "-c", str(src), "-o", str(obj)])
     tmp = out.with_suffix(".so.tmp")
-    _run(["g++", "-shared", "-o", str(tmp), str(host_o), str(blob_o),
+    _run(["g++", "-shared", "-o", str(tmp), str(host_o), str(gguf_o), str(blob_o), "-pthread",
           "-L", str(ROCM / "lib"), "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
           "-Wl,--version-script=" + str(CSRC / "er_hip.map")])
     os.replace(tmp, out)

@@ -9,6 +9,7 @@
 // (Sources/EdgeRunnerMetal/GEMVKernel.swift:1276-1300, 1415-1432) and the
 // Dequant*Kernel.dequantise checks (Sources/EdgeRunnerIO/DequantQ4KMKernel.swift:23-29).
 #include "er_hip.h"
+#include "er_error.h"
 #include "er_gemv_cfg.h"
 
 #include <hip/hip_runtime_api.h>
@@ -23,7 +24,7 @@
 extern "C" const unsigned char er_kernels_blob[];
 extern "C" const unsigned char er_kernels_blob_end[];
 
-namespace {
+namespace er_detail {
 
 thread_local char g_last_error[512] = "";
 
@@ -34,6 +35,12 @@ er_status fail(er_status st, const char *fmt, ...) {
     va_end(ap);
     return st;
 }
+
+}  // namespace er_detail
+
+namespace {
+
+using er_detail::fail;
 
 // Kernel table: every kernel the library launches, resolved at create time.
 // The integer-dot GEMV kernels (one per er_gemv_cfg.h entry and format) are
@@ -620,7 +627,7 @@ extern "C" {
 
 int er_hip_abi_version(void) { return ER_HIP_ABI_VERSION; }
 
-const char *er_hip_last_error(void) { return g_last_error; }
+const char *er_hip_last_error(void) { return er_detail::g_last_error; }
 
 const char *er_status_string(er_status s) {
     switch (s) {
@@ -634,6 +641,13 @@ const char *er_status_string(er_status s) {
         case ER_ERR_ALLOCATION_FAILED: return "allocationFailed";
         case ER_ERR_INVALID_ARGUMENT: return "invalidArgument";
         case ER_ERR_DEVICE: return "deviceError";
+        case ER_ERR_FILE_NOT_FOUND: return "fileNotFound";
+        case ER_ERR_INVALID_FORMAT: return "invalidFormat";
+        case ER_ERR_UNSUPPORTED_VERSION: return "unsupportedVersion";
+        case ER_ERR_UNSUPPORTED_DATA_TYPE: return "unsupportedDataType";
+        case ER_ERR_MMAP_FAILED: return "mmapFailed";
+        case ER_ERR_MISSING_METADATA: return "missingMetadata";
+        case ER_ERR_TENSOR_NOT_FOUND: return "tensorNotFound";
     }
     return "unknown";
 }

@@ -171,6 +171,15 @@ class GEMVKernel:
                 b.free()
             xb.free()
 
+    def encodeTensor(self, stream: Optional[Stream], tensor, inputBuffer: Buffer,
+                     outputBuffer: Buffer, tokens: int = 1) -> None:
+        """encodeProjection on a loaded TensorStorage (edgerunner_amd.gguf):
+        its data type and GGUF shape [K, M] pick the kernel
+        (Gemma4LanguageModel.swift:4207-4285)."""
+        import ctypes as C
+        check(self.lib.er_hip_encode_projection(self.ctx.handle, _sh(stream), C.byref(tensor.storage),
+                                                inputBuffer.raw, outputBuffer.raw, tokens))
+
     def encodeProjection(self, stream: Optional[Stream], weightBuffer: Buffer, dataType: int,
                          inputBuffer: Buffer, outputBuffer: Buffer, M: int, K: int,
                          tokens: int = 1, byteOffset: int = 0) -> None:

@@ -78,9 +78,43 @@ class DeviceError(EdgeRunnerHIPError):
     status = 9
 
 
+class WeightLoaderError(EdgeRunnerHIPError):
+    """WeightLoaderError (Sources/EdgeRunnerIO/WeightLoaderError.swift:3-15)."""
+
+
+class FileNotFound(WeightLoaderError):
+    status = 10
+
+
+class InvalidFormat(WeightLoaderError):
+    status = 11
+
+
+class UnsupportedVersion(WeightLoaderError):
+    status = 12
+
+
+class UnsupportedDataType(WeightLoaderError):
+    status = 13
+
+
+class MmapFailed(WeightLoaderError):
+    status = 14
+
+
+class MissingMetadata(WeightLoaderError):
+    status = 15
+
+
+class TensorNotFound(WeightLoaderError):
+    status = 16
+
+
 _BY_STATUS = {cls.status: cls for cls in (
     LibraryNotFound, FunctionNotFound, EncodingFailed, InvalidMatrixShape, InvalidVectorShape,
-    InvalidBlockDataCount, AllocationFailed, InvalidArgument, DeviceError)}
+    InvalidBlockDataCount, AllocationFailed, InvalidArgument, DeviceError, FileNotFound,
+    InvalidFormat, UnsupportedVersion, UnsupportedDataType, MmapFailed, MissingMetadata,
+    TensorNotFound)}
 
 
 def check(status: int) -> None:

@@ -35,8 +35,9 @@ extern "C" {
 #define ER_HIP_ABI_VERSION 1
 
 /* Status codes.  Each maps 1:1 onto a Swift error case of the reference:
- * GEMVError (GEMVKernel.swift:1435-1441) and DequantKernelError
- * (Sources/EdgeRunnerIO/DequantKernel.swift:19-25). */
+ * GEMVError (GEMVKernel.swift:1435-1441), DequantKernelError
+ * (Sources/EdgeRunnerIO/DequantKernel.swift:19-25) and, for the GGUF loader,
+ * WeightLoaderError. */
 typedef enum er_status {
     ER_OK = 0,
     ER_ERR_LIBRARY_NOT_FOUND = 1,        /* GEMVError.libraryNotFound: code object missing/unloadable */
@@ -47,7 +48,15 @@ typedef enum er_status {
     ER_ERR_INVALID_BLOCK_DATA_COUNT = 6, /* DequantKernelError.invalidBlockDataCount(expected:actual:) */
     ER_ERR_ALLOCATION_FAILED = 7,        /* DequantKernelError.allocationFailed(byteCount:) */
     ER_ERR_INVALID_ARGUMENT = 8,         /* null context/pointer, misaligned device pointer */
-    ER_ERR_DEVICE = 9                    /* HIP runtime error (commandBuffer.error analogue) */
+    ER_ERR_DEVICE = 9,                   /* HIP runtime error (commandBuffer.error analogue) */
+    /* WeightLoaderError (Sources/EdgeRunnerIO/WeightLoaderError.swift:3-15), GGUF loader (er_gguf.h) */
+    ER_ERR_FILE_NOT_FOUND = 10,          /* fileNotFound(URL) */
+    ER_ERR_INVALID_FORMAT = 11,          /* invalidFormat(String) */
+    ER_ERR_UNSUPPORTED_VERSION = 12,     /* unsupportedVersion(UInt32) */
+    ER_ERR_UNSUPPORTED_DATA_TYPE = 13,   /* unsupportedDataType(UInt32) */
+    ER_ERR_MMAP_FAILED = 14,             /* mmapFailed(errno:) */
+    ER_ERR_MISSING_METADATA = 15,        /* missingMetadata(String) */
+    ER_ERR_TENSOR_NOT_FOUND = 16         /* tensorNotFound(String) */
 } er_status;
 
 /* TensorDataType raw values (Sources/EdgeRunnerIO/WeightMap.swift:69-91). */

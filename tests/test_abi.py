@@ -1,5 +1,5 @@
 """CPU checks of the C ABI: the library loads, exports exactly what
-include/er_hip.h declares, and validates shapes before touching a device
+include/*.h declares, and validates shapes before touching a device
 (GEMVKernel.swift:1415-1432 rules), so these run without a GPU."""
 import ctypes as C
 import re
@@ -17,7 +17,7 @@ def declared_symbols():
     for h in (ROOT / "include").glob("*.h"):
         text = h.read_text()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        for m in re.finditer(r"\b((?:er_hip|er_status)_\w+)\s*\(", text):
+        for m in re.finditer(r"\b((?:er_hip|er_status|er_gguf)_\w+)\s*\(", text):
             names.add(m.group(1))
     return sorted(names)
 
