@@ -12,11 +12,11 @@ from .runtime import (AllocationFailed, Buffer, Capture, Context, Graph, Dequant
                       WeightLoaderError, FileNotFound, InvalidFormat, UnsupportedVersion,
                       UnsupportedDataType, MmapFailed, MissingMetadata, TensorNotFound)
 from .gemv import (DequantQ4KMKernel, DequantQ6KKernel, DequantQ8_0Kernel,  # noqa: F401
-                   GEMVKernel, QuantGEMMKernel, QuantizeQ8RowsKernel, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0)
+                   FusedQ8Kernel, GEMVKernel, QuantGEMMKernel, QuantizeQ8RowsKernel, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0)
 
 __all__ = [
     "Context", "Buffer", "Stream", "Event", "Graph", "Capture", "default_context",
-    "GEMVKernel", "QuantGEMMKernel", "QuantizeQ8RowsKernel", "DequantQ8_0Kernel", "DequantQ4KMKernel", "DequantQ6KKernel",
+    "GEMVKernel", "FusedQ8Kernel", "QuantGEMMKernel", "QuantizeQ8RowsKernel", "DequantQ8_0Kernel", "DequantQ4KMKernel", "DequantQ6KKernel",
     "GEMVError", "DequantKernelError", "EdgeRunnerHIPError", "WeightLoaderError",
     "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q6_K",
 ]

@@ -137,6 +137,16 @@ SIGNATURES = {
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
     "er_hip_quantize_q8_0_rows": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, _u32, _u32, _u32, _u32]),
+    "er_hip_q8_0_fused_qkv": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer,
+                                        er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32,
+                                        _u32, C.c_float]),
+    "er_hip_q8_0_fused_gate_up_silu": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer,
+                                                 er_buffer, er_buffer, _u32, _u32, _u32, C.c_float]),
+    "er_hip_q8_0_fused_final_norm_gemv": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer,
+                                                    er_buffer, _u32, _u32, C.c_float]),
+    "er_hip_q8_0_gemv_f16out": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_q8_0_gemv_add": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer,
+                                       _u32, _u32]),
     "er_hip_encode_batched_q4k_weights": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32]),
     "er_hip_encode_batched_q6k_weights": (

@@ -289,6 +289,37 @@ ER_DEV void gemv_q4k_i8_geglu(const uint8_t *__restrict__ Wg, const uint8_t *__r
 // (4-byte aligned).  Dwords v0..v16: block A d = v0[15:0], qs = bytes 2..33
 // (realigned by 2 bytes), block B d = v8[31:16], qs = v9..v16.  The int8 qs
 // bytes feed v_dot4_i32_i8 as they are.
+struct Q8Slot {
+    u32x4 v0, v1, v2, v3;
+    uint32_t v4;
+};
+
+ER_DEV Q8Slot q8_slot_load(const uint8_t *p) {
+    return Q8Slot{ld16_a4(p), ld16_a4(p + 16), ld16_a4(p + 32), ld16_a4(p + 48), ld4_a4(p + 64)};
+}
+
+// acc + sg * (dA * (qA . x) + dB * (qB . x)) over the slot's 64 weights.
+ER_DEV float q8_slot_dot(const Q8Slot &w, const u32x4 (&xv)[ER_XL_PLANES][4], float sg, float acc) {
+    const uint32_t v[17] = {w.v0.x, w.v0.y, w.v0.z, w.v0.w, w.v1.x, w.v1.y, w.v1.z, w.v1.w, w.v2.x,
+                            w.v2.y, w.v2.z, w.v2.w, w.v3.x, w.v3.y, w.v3.z, w.v3.w, w.v4};
+    int cA[ER_XL_PLANES] = {}, cB[ER_XL_PLANES] = {};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int qa = (int)alignbyte(v[k + 1], v[k], 2);
+        const int qb = (int)v[9 + k];
+#pragma unroll
+        for (int l = 0; l < ER_XL_PLANES; ++l) {
+            cA[l] = __builtin_amdgcn_sdot4(qa, (int)xv[l][k >> 2][k & 3], cA[l], false);
+            cB[l] = __builtin_amdgcn_sdot4(qb, (int)xv[l][2 + (k >> 2)][k & 3], cB[l], false);
+        }
+    }
+    const float TA = xl_combine(cA[0], cA[1], cA[2]);
+    const float TB = xl_combine(cB[0], cB[1], cB[2]);
+    const float dA = f16_to_f32(v[0] & 0xffffu), dB = f16_to_f32(v[8] >> 16);
+    const float a = __builtin_fmaf(sg * dA, TA, acc);
+    return __builtin_fmaf(sg * dB, TB, a);
+}
+
 template <int LPR, int NS, int R>
 ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict__ x,
                          float *__restrict__ y, uint32_t M, uint32_t K) {
@@ -306,20 +337,13 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
     float4 xr[C::XG][4];
     xl_load<C::XG, NT>(x, K, xr);
     __builtin_amdgcn_sched_barrier(0);
-    u32x4 v0[NS][R], v1[NS][R], v2[NS][R], v3[NS][R];
-    uint32_t v4[NS][R];
+    Q8Slot w[NS][R];
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         const uint32_t s = min(li + (uint32_t)LPR * j, S - 1u);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint8_t *p = W + (size_t)min(row0 + (uint32_t)r, M - 1u) * rowBytes + (size_t)s * 68u;
-            v0[j][r] = ld16_a4(p);
-            v1[j][r] = ld16_a4(p + 16);
-            v2[j][r] = ld16_a4(p + 32);
-            v3[j][r] = ld16_a4(p + 48);
-            v4[j][r] = ld4_a4(p + 64);
-        }
+        for (int r = 0; r < R; ++r)
+            w[j][r] = q8_slot_load(W + (size_t)min(row0 + (uint32_t)r, M - 1u) * rowBytes + (size_t)s * 68u);
     }
     __builtin_amdgcn_sched_barrier(0);
     xl_store<C::XG, NT>(lds, K, xr);
@@ -339,26 +363,7 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
         xl_read_group(X, s, xv);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t v[17] = {v0[j][r].x, v0[j][r].y, v0[j][r].z, v0[j][r].w,
-                                    v1[j][r].x, v1[j][r].y, v1[j][r].z, v1[j][r].w,
-                                    v2[j][r].x, v2[j][r].y, v2[j][r].z, v2[j][r].w,
-                                    v3[j][r].x, v3[j][r].y, v3[j][r].z, v3[j][r].w, v4[j][r]};
-            int cA[ER_XL_PLANES] = {}, cB[ER_XL_PLANES] = {};
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int qa = (int)alignbyte(v[k + 1], v[k], 2);
-                const int qb = (int)v[9 + k];
-#pragma unroll
-                for (int l = 0; l < ER_XL_PLANES; ++l) {
-                    cA[l] = __builtin_amdgcn_sdot4(qa, (int)xv[l][k >> 2][k & 3], cA[l], false);
-                    cB[l] = __builtin_amdgcn_sdot4(qb, (int)xv[l][2 + (k >> 2)][k & 3], cB[l], false);
-                }
-            }
-            const float TA = xl_combine(cA[0], cA[1], cA[2]);
-            const float TB = xl_combine(cB[0], cB[1], cB[2]);
-            const float dA = f16_to_f32(v[0] & 0xffffu), dB = f16_to_f32(v[8] >> 16);
-            float a = __builtin_fmaf(sg * dA, TA, acc[r]);
-            acc[r] = __builtin_fmaf(sg * dB, TB, a);
+            acc[r] = q8_slot_dot(w[j][r], xv, sg, acc[r]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -369,6 +374,196 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
         for (int r = 0; r < R; ++r)
             if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
     }
+}
+
+// ---------------------------------------------------------------------------
+// Fused Q8_0 projections (the reference's Dequant_Q8_0.metal:199-586):
+// dequant_q8_0_fused_qkv, _fused_final_norm_gemv, _gemv_f16out, _gemv_add
+// (row-list kernel below) and _fused_gate_up_silu (pair kernel).
+//
+// RMSNorm prologue (when normW is set): the workgroup sums x^2 over the
+// token's row of x while the weight loads are in flight, then stages
+// x * (1 / sqrt(sum / K + eps)) * normW instead of x, as
+// normed = x * rmsScale * normWeight (Dequant_Q8_0.metal:275-286).  The
+// configurations used hold the whole of x in registers (LPR * NS * 64 >= K,
+// so XG * 4096 >= K): no chunk is staged outside the normalised set.
+
+#define ER_EPI_Q8_ROWS 0  // per row: + residual (optional), fp32 or fp16 store
+#define ER_EPI_Q8_SILU 1  // rows [0, R/2) gate, [R/2, R) up: silu(gate) * up
+
+ER_DEV float silu(float g) { return g / (1.0f + expf(-g)); }
+
+template <int LPR, int NS, int R, int EPI>
+ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const (&yrow)[R],
+                                    const bool (&rowLive)[R], const bool (&rowHalf)[R],
+                                    const float *const (&rowRes)[R], const float *__restrict__ x,
+                                    const float *__restrict__ normW, float eps, uint32_t K) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    __shared__ float red[ER_GEMV_WAVES];
+    using C = I8Cfg<LPR, NS>;
+    constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t li = lane % LPR;
+    const uint32_t S = K >> 6, C16 = K >> 4;
+
+    float4 xr[C::XG][4], wr[C::XG][4];
+    xl_load<C::XG, NT>(x, K, xr);
+    if (normW) xl_load<C::XG, NT>(normW, K, wr);
+    __builtin_amdgcn_sched_barrier(0);
+    Q8Slot w[NS][R];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t s = min(li + (uint32_t)LPR * j, S - 1u);
+#pragma unroll
+        for (int r = 0; r < R; ++r) w[j][r] = q8_slot_load(rowp[r] + (size_t)s * 68u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (normW) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C::XG; ++c)
+            if (threadIdx.x + NT * (uint32_t)c < C16)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    ss += xr[c][q].x * xr[c][q].x + xr[c][q].y * xr[c][q].y + xr[c][q].z * xr[c][q].z +
+                          xr[c][q].w * xr[c][q].w;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < ER_GEMV_WAVES; ++k) ss += red[k];
+        const float rms = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
+#pragma unroll
+        for (int c = 0; c < C::XG; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                xr[c][q].x = xr[c][q].x * rms * wr[c][q].x;
+                xr[c][q].y = xr[c][q].y * rms * wr[c][q].y;
+                xr[c][q].z = xr[c][q].z * rms * wr[c][q].z;
+                xr[c][q].w = xr[c][q].w * rms * wr[c][q].w;
+            }
+    }
+    xl_store<C::XG, NT>(lds, K, xr);
+    __syncthreads();
+
+    const XLimbs X = xl_view(lds, K);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const uint32_t sRaw = li + (uint32_t)LPR * j;
+        const uint32_t s = min(sRaw, S - 1u);
+        const float sg = sRaw < S ? X.sg64[s] : 0.0f;
+        u32x4 xv[ER_XL_PLANES][4];
+        xl_read_group(X, s, xv);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = q8_slot_dot(w[j][r], xv, sg, acc[r]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (li != 0) return;
+    if constexpr (EPI == ER_EPI_Q8_SILU) {
+#pragma unroll
+        for (int r = 0; r < R / 2; ++r)
+            if (rowLive[r]) *(float *)yrow[r] = silu(acc[r]) * acc[R / 2 + r];
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (!rowLive[r]) continue;
+            const float v = rowRes[r] ? acc[r] + *rowRes[r] : acc[r];
+            if (rowHalf[r])
+                *(_Float16 *)yrow[r] = (_Float16)v;
+            else
+                *(float *)yrow[r] = v;
+        }
+    }
+}
+
+// Up to three Q8_0 matrices sharing x and K, rows concatenated (Q | K | V);
+// token t = blockIdx.y reads x + t K and writes row i of matrix m at
+// y[m] + t M[m] + i (fp16 when bit m of halfMask is set), adding
+// res[m][t M[m] + i] when res[m] is set.
+struct Q8Multi {
+    const uint8_t *W[3];
+    void *y[3];
+    const float *res[3];
+    uint32_t M[3];
+    uint32_t halfMask;
+    const float *normW;
+    float eps;
+};
+
+template <int LPR, int NS, int R>
+ER_DEV void gemv_q8_0_i8_multi(const Q8Multi &mm, const float *__restrict__ x, uint32_t K) {
+    using C = I8Cfg<LPR, NS>;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR;
+    const uint32_t t = blockIdx.y;
+    const size_t rowBytes = (size_t)(K >> 6) * 68u;
+    const uint32_t Mt = mm.M[0] + mm.M[1] + mm.M[2];
+    const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+    const uint8_t *rowp[R];
+    void *yrow[R];
+    bool live[R], half[R];
+    const float *res[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        uint32_t v = min(row0 + (uint32_t)r, Mt - 1u);
+        int m = 0;
+        if (v >= mm.M[0]) {
+            v -= mm.M[0];
+            m = 1;
+            if (v >= mm.M[1]) {
+                v -= mm.M[1];
+                m = 2;
+            }
+        }
+        const size_t out = (size_t)t * mm.M[m] + v;
+        rowp[r] = mm.W[m] + (size_t)v * rowBytes;
+        half[r] = (mm.halfMask >> m) & 1u;
+        yrow[r] = (uint8_t *)mm.y[m] + out * (half[r] ? 2u : 4u);
+        res[r] = mm.res[m] ? mm.res[m] + out : nullptr;
+        live[r] = row0 + (uint32_t)r < Mt;
+    }
+    gemv_q8_0_i8_fused_core<LPR, NS, R, ER_EPI_Q8_ROWS>(rowp, yrow, live, half, res, x + (size_t)t * K,
+                                                         mm.normW, mm.eps, K);
+}
+
+// Gate/up pairs: y[t M + i] = silu(gate_i . n) * (up_i . n), n = RMSNorm(x_t)
+// (dequant_q8_0_fused_gate_up_silu, Dequant_Q8_0.metal:410-500).
+template <int LPR, int NS, int R>
+ER_DEV void gemv_q8_0_i8_silu(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
+                              const float *__restrict__ x, float *__restrict__ y,
+                              const float *__restrict__ normW, float eps, uint32_t M, uint32_t K) {
+    static_assert(R % 2 == 0, "SiLU pairs gate and up rows");
+    using C = I8Cfg<LPR, NS>;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR;
+    const uint32_t t = blockIdx.y;
+    const size_t rowBytes = (size_t)(K >> 6) * 68u;
+    const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)(R / 2);
+    const uint8_t *rowp[R];
+    void *yrow[R];
+    bool live[R], half[R];
+    const float *res[R];
+#pragma unroll
+    for (int r = 0; r < R / 2; ++r) {
+        const uint32_t row = min(row0 + (uint32_t)r, M - 1u);
+        rowp[r] = Wg + (size_t)row * rowBytes;
+        rowp[R / 2 + r] = Wu + (size_t)row * rowBytes;
+        yrow[r] = yrow[R / 2 + r] = y + (size_t)t * M + row;
+        live[r] = live[R / 2 + r] = row0 + (uint32_t)r < M;
+        half[r] = half[R / 2 + r] = false;
+        res[r] = res[R / 2 + r] = nullptr;
+    }
+    gemv_q8_0_i8_fused_core<LPR, NS, R, ER_EPI_Q8_SILU>(rowp, yrow, live, half, res, x + (size_t)t * K,
+                                                         normW, eps, K);
 }
 
 // ---------------------------------------------------------------------------
@@ -957,6 +1152,20 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
                                                 const float *__restrict__ x,                   \
                                                 float *__restrict__ y, uint32_t M, uint32_t K) { \
         gemv_q4k_i8_geglu<LPR, NS, R>(Wg, Wu, x, y, M, K);                                    \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q8_0_multi_l##LPR##_n##NS##_r##R(Q8Multi mm, const float *__restrict__ x,      \
+                                                 uint32_t K) {                                \
+        gemv_q8_0_i8_multi<LPR, NS, R>(mm, x, K);                                             \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q8_0_silu_l##LPR##_n##NS##_r##R(const uint8_t *__restrict__ Wg,                \
+                                                const uint8_t *__restrict__ Wu,                \
+                                                const float *__restrict__ x,                   \
+                                                float *__restrict__ y,                         \
+                                                const float *__restrict__ normW, float eps,    \
+                                                uint32_t M, uint32_t K) {                      \
+        gemv_q8_0_i8_silu<LPR, NS, R>(Wg, Wu, x, y, normW, eps, M, K);                        \
     }
 ER_I8_MULTI_CONFIGS(ER_I8_MULTI_ENTRY)
 

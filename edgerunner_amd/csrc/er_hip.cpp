@@ -122,6 +122,17 @@ struct Q4MultiArgs {
     uint32_t M[3];
 };
 
+// Kernel argument block of er_gemv_q8_0_multi_* (matches Q8Multi in er_gemv.hip).
+struct Q8MultiArgs {
+    const void *W[3];
+    void *y[3];
+    const float *res[3];
+    uint32_t M[3];
+    uint32_t halfMask;
+    const float *normW;
+    float eps;
+};
+
 }  // namespace
 
 struct er_hip_ctx {
@@ -134,6 +145,8 @@ struct er_hip_ctx {
     hipFunction_t fnQ6KTop1[kI8Count] = {};
     hipFunction_t fnQ4KMulti[kI8MultiCount] = {};
     hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
+    hipFunction_t fnQ8Multi[kI8MultiCount] = {};
+    hipFunction_t fnQ8Silu[kI8MultiCount] = {};
     int cu_count = 0;
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
     int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1 selects the non-pipelined GEMM (benchmark comparison)
@@ -591,6 +604,106 @@ er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_b
                      stream, args);
 }
 
+// Fused Q8_0 projections (Dequant_Q8_0.metal:199-586, encoded by name in
+// LlamaLanguageModel.swift:260-275).  The reference dispatches them without
+// checks; here every buffer must hold what the shapes imply (weights
+// INVALID_MATRIX_SHAPE, vectors ENCODING_FAILED), and the integer-dot kernels
+// need K % 64 == 0 and K <= 16384 (INVALID_VECTOR_SHAPE).
+struct Q8FusedSpec {
+    const char *name;
+    int count;          // matrices (1..3); 2 for gate/up
+    er_buffer W[3], y[3], res[3];
+    uint32_t M[3];
+    uint32_t halfMask;  // bit m: matrix m's output is fp16
+    er_buffer normW;    // data == nullptr: no RMSNorm
+    float eps;
+    bool silu;          // gate/up pairs, output silu(gate) * up
+};
+
+er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &f, er_buffer x,
+                          uint32_t tokens, uint32_t K) {
+    if (K == 0 || K % 32u != 0)
+        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s: K=%u must be a positive multiple of 32", f.name, K);
+    if (K % 64u != 0 || K > kI8MaxK)
+        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s: the fused kernels need K %% 64 == 0 and K <= %u (K=%u)",
+                    f.name, kI8MaxK, K);
+    if (tokens == 0 || tokens > 65535u)
+        return fail(ER_ERR_ENCODING_FAILED, "%s: tokenCount %u outside [1, 65535]", f.name, tokens);
+    uint64_t Mt = 0;
+    for (int m = 0; m < f.count; ++m) {
+        const uint64_t need = (uint64_t)f.M[m] * (K / 32u) * 34u;
+        if (f.W[m].length < need)
+            return fail(ER_ERR_INVALID_MATRIX_SHAPE, "%s: weight %d holds %llu bytes, %u rows need %llu", f.name, m,
+                        (unsigned long long)f.W[m].length, f.M[m], (unsigned long long)need);
+        const uint64_t outNeed = (uint64_t)tokens * f.M[m] * ((f.halfMask >> m) & 1u ? 2u : 4u);
+        if (!f.silu || m == 0) {
+            if (f.y[m].length < outNeed)
+                return fail(ER_ERR_ENCODING_FAILED, "%s: output %d holds %llu bytes, needs %llu", f.name, m,
+                            (unsigned long long)f.y[m].length, (unsigned long long)outNeed);
+        }
+        if (f.res[m].data && f.res[m].length < (uint64_t)tokens * f.M[m] * 4u)
+            return fail(ER_ERR_ENCODING_FAILED, "%s: residual holds %llu bytes, needs %llu", f.name,
+                        (unsigned long long)f.res[m].length, (unsigned long long)tokens * f.M[m] * 4u);
+        Mt += f.M[m];
+    }
+    if (x.length < (uint64_t)tokens * K * 4u)
+        return fail(ER_ERR_ENCODING_FAILED, "%s: input holds %llu bytes, needs %llu", f.name,
+                    (unsigned long long)x.length, (unsigned long long)tokens * K * 4u);
+    if (f.normW.data && f.normW.length < (uint64_t)K * 4u)
+        return fail(ER_ERR_ENCODING_FAILED, "%s: norm weight holds %llu bytes, needs %llu", f.name,
+                    (unsigned long long)f.normW.length, (unsigned long long)K * 4u);
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (f.silu) Mt = f.M[0];
+    if (Mt == 0) return ER_OK;
+    if (Mt > 0x7fffffffull) return fail(ER_ERR_INVALID_MATRIX_SHAPE, "%s: too many rows", f.name);
+    if (!x.data || !aligned(x.data, 16) || (f.normW.data && !aligned(f.normW.data, 16)))
+        return fail(ER_ERR_INVALID_ARGUMENT, "%s: input and norm weight must be 16-byte aligned", f.name);
+    for (int m = 0; m < f.count; ++m) {
+        if (f.M[m] == 0) continue;
+        if (!f.W[m].data || !aligned(f.W[m].data, 4) || ((!f.silu || m == 0) && !f.y[m].data) ||
+            (f.res[m].data && !aligned(f.res[m].data, 4)))
+            return fail(ER_ERR_INVALID_ARGUMENT, "%s: null or misaligned buffer (weights and residual 4-byte aligned)",
+                        f.name);
+        if ((!f.silu || m == 0) && !aligned(f.y[m].data, (f.halfMask >> m) & 1u ? 2 : 4))
+            return fail(ER_ERR_INVALID_ARGUMENT, "%s: misaligned output", f.name);
+    }
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    const uint32_t S = K / 64u;
+    const int ci = pick_i8_multi(S, (uint32_t)(f.silu ? 2u * Mt : Mt), ctx->cu_count);
+    if (ci < 0) return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s: no configuration for K=%u", f.name, K);
+    const I8Cfg &c = kI8MultiCfg[ci];
+    const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+    const float *normW = (const float *)f.normW.data;
+    float eps = f.eps;
+    if (f.silu) {
+        const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * (c.r / 2u);
+        uint32_t M = f.M[0];
+        void *args[] = {(void *)&f.W[0].data, (void *)&f.W[1].data, &x.data, (void *)&f.y[0].data,
+                        &normW, &eps, &M, &K};
+        dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, tokens, 1);
+        return launch_fn(ctx->fnQ8Silu[ci], "er_gemv_q8_0_silu", grid, dim3(kGemvThreads, 1, 1), lds, stream,
+                         args);
+    }
+    Q8MultiArgs a{};
+    for (int m = 0; m < 3; ++m) {
+        const int j = m < f.count ? m : 0;
+        a.W[m] = f.W[j].data;
+        a.y[m] = f.y[j].data;
+        a.res[m] = m < f.count ? (const float *)f.res[m].data : nullptr;
+        a.M[m] = m < f.count ? f.M[m] : 0u;
+    }
+    a.halfMask = f.halfMask;
+    a.normW = normW;
+    a.eps = eps;
+    const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
+    void *args[] = {&a, &x.data, &K};
+    dim3 grid((uint32_t)((Mt + rowsPerBlock - 1) / rowsPerBlock), tokens, 1);
+    return launch_fn(ctx->fnQ8Multi[ci], "er_gemv_q8_0_multi", grid, dim3(kGemvThreads, 1, 1), lds, stream,
+                     args);
+}
+
 er_status encode_dequant(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer blocks,
                          uint64_t count, er_buffer out) {
     const uint64_t need = count * block_bytes(f);
@@ -709,11 +822,14 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
     }
     for (int i = 0; i < kI8MultiCount; ++i) {
         char name[64];
-        for (int kind = 0; kind < 2; ++kind) {
-            std::snprintf(name, sizeof(name), "er_gemv_q4k_%s_l%u_n%u_r%u", kind ? "geglu" : "multi",
+        static const char *const kinds[4] = {"q4k_multi", "q4k_geglu", "q8_0_multi", "q8_0_silu"};
+        hipFunction_t *const slots[4] = {&ctx->fnQ4KMulti[i], &ctx->fnQ4KGeglu[i], &ctx->fnQ8Multi[i],
+                                         &ctx->fnQ8Silu[i]};
+        for (int kind = 0; kind < 4; ++kind) {
+            std::snprintf(name, sizeof(name), "er_gemv_%s_l%u_n%u_r%u", kinds[kind],
                           (unsigned)kI8MultiCfg[i].lpr, (unsigned)kI8MultiCfg[i].ns,
                           (unsigned)kI8MultiCfg[i].r);
-            e = hipModuleGetFunction(kind ? &ctx->fnQ4KGeglu[i] : &ctx->fnQ4KMulti[i], ctx->module, name);
+            e = hipModuleGetFunction(slots[kind], ctx->module, name);
             if (e != hipSuccess) {
                 (void)hipModuleUnload(ctx->module);
                 delete ctx;
@@ -1041,6 +1157,80 @@ er_status er_hip_quantize_q8_0_rows(er_hip_ctx *ctx, er_stream stream, er_buffer
                                     uint32_t blocks_per_row) {
     return encode_quantize_q8_0(ctx, stream, source, destination, row_count, source_row_stride,
                                 destination_row_base, blocks_per_row);
+}
+
+er_status er_hip_q8_0_fused_qkv(er_hip_ctx *ctx, er_stream stream, er_buffer wq, er_buffer wk, er_buffer wv,
+                                er_buffer input, er_buffer out_q, er_buffer out_k, er_buffer out_v_f16,
+                                er_buffer norm_weight, uint32_t q_rows, uint32_t kv_rows, uint32_t cols,
+                                uint32_t token_count, float rms_eps) {
+    Q8FusedSpec f{};
+    f.name = "dequant_q8_0_fused_qkv";
+    f.count = 3;
+    f.W[0] = wq, f.W[1] = wk, f.W[2] = wv;
+    f.y[0] = out_q, f.y[1] = out_k, f.y[2] = out_v_f16;
+    f.M[0] = q_rows, f.M[1] = kv_rows, f.M[2] = kv_rows;
+    f.halfMask = 4u;
+    f.normW = norm_weight;
+    f.eps = rms_eps;
+    if (!norm_weight.data) return fail(ER_ERR_INVALID_ARGUMENT, "%s: null norm weight", f.name);
+    return encode_q8_fused(ctx, stream, f, input, token_count, cols);
+}
+
+er_status er_hip_q8_0_fused_gate_up_silu(er_hip_ctx *ctx, er_stream stream, er_buffer w_gate,
+                                         er_buffer w_up, er_buffer input, er_buffer activated,
+                                         er_buffer norm_weight, uint32_t rows, uint32_t cols,
+                                         uint32_t token_count, float rms_eps) {
+    Q8FusedSpec f{};
+    f.name = "dequant_q8_0_fused_gate_up_silu";
+    f.count = 2;
+    f.W[0] = w_gate, f.W[1] = w_up;
+    f.y[0] = activated;
+    f.M[0] = rows, f.M[1] = rows;
+    f.normW = norm_weight;
+    f.eps = rms_eps;
+    f.silu = true;
+    if (!norm_weight.data) return fail(ER_ERR_INVALID_ARGUMENT, "%s: null norm weight", f.name);
+    return encode_q8_fused(ctx, stream, f, input, token_count, cols);
+}
+
+er_status er_hip_q8_0_fused_final_norm_gemv(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                            er_buffer input, er_buffer output, er_buffer norm_weight,
+                                            uint32_t rows, uint32_t cols, float rms_eps) {
+    Q8FusedSpec f{};
+    f.name = "dequant_q8_0_fused_final_norm_gemv";
+    f.count = 1;
+    f.W[0] = weight;
+    f.y[0] = output;
+    f.M[0] = rows;
+    f.normW = norm_weight;
+    f.eps = rms_eps;
+    if (!norm_weight.data) return fail(ER_ERR_INVALID_ARGUMENT, "%s: null norm weight", f.name);
+    return encode_q8_fused(ctx, stream, f, input, 1, cols);
+}
+
+er_status er_hip_q8_0_gemv_f16out(er_hip_ctx *ctx, er_stream stream, er_buffer weight, er_buffer input,
+                                  er_buffer output_f16, uint32_t rows, uint32_t cols) {
+    Q8FusedSpec f{};
+    f.name = "dequant_q8_0_gemv_f16out";
+    f.count = 1;
+    f.W[0] = weight;
+    f.y[0] = output_f16;
+    f.M[0] = rows;
+    f.halfMask = 1u;
+    return encode_q8_fused(ctx, stream, f, input, 1, cols);
+}
+
+er_status er_hip_q8_0_gemv_add(er_hip_ctx *ctx, er_stream stream, er_buffer weight, er_buffer input,
+                               er_buffer residual, er_buffer output, uint32_t rows, uint32_t cols) {
+    Q8FusedSpec f{};
+    f.name = "dequant_q8_0_gemv_add";
+    f.count = 1;
+    f.W[0] = weight;
+    f.y[0] = output;
+    f.res[0] = residual;
+    f.M[0] = rows;
+    if (!residual.data) return fail(ER_ERR_INVALID_ARGUMENT, "%s: null residual", f.name);
+    return encode_q8_fused(ctx, stream, f, input, 1, cols);
 }
 
 er_status er_hip_encode_batched_q4k_weights(er_hip_ctx *ctx, er_stream stream, er_buffer weight,

@@ -381,3 +381,51 @@ class QuantizeQ8RowsKernel:
         finally:
             sb.free()
             db.free()
+
+
+class FusedQ8Kernel:
+    """Fused Q8_0 projections: the pipelines LlamaLanguageModel fetches by name
+    (LlamaLanguageModel.swift:260-275; kernels Dequant_Q8_0.metal:199-586).
+    encode* append to a stream; the RMSNorm-fused ones normalise each token's
+    x with norm weight and eps as RMSNorm does (x * rmsScale * w)."""
+
+    def __init__(self, ctx: Optional[Context] = None):
+        self.ctx = ctx or default_context()
+        self.lib = self.ctx.lib
+
+    def encodeFusedQKV(self, stream: Optional[Stream], wq: Buffer, wk: Buffer, wv: Buffer,
+                       inputBuffer: Buffer, outQ: Buffer, outK: Buffer, outVHalf: Buffer,
+                       normWeight: Buffer, qRows: int, kvRows: int, cols: int, tokenCount: int,
+                       rmsEps: float) -> None:
+        """dequant_q8_0_fused_qkv: q, k fp32; v fp16."""
+        check(self.lib.er_hip_q8_0_fused_qkv(self.ctx.handle, _sh(stream), wq.raw, wk.raw, wv.raw,
+                                             inputBuffer.raw, outQ.raw, outK.raw, outVHalf.raw,
+                                             normWeight.raw, qRows, kvRows, cols, tokenCount, rmsEps))
+
+    def encodeFusedGateUpSilu(self, stream: Optional[Stream], wGate: Buffer, wUp: Buffer,
+                              inputBuffer: Buffer, activated: Buffer, normWeight: Buffer, rows: int,
+                              cols: int, tokenCount: int, rmsEps: float) -> None:
+        """dequant_q8_0_fused_gate_up_silu: silu(gate . n) * (up . n)."""
+        check(self.lib.er_hip_q8_0_fused_gate_up_silu(self.ctx.handle, _sh(stream), wGate.raw, wUp.raw,
+                                                      inputBuffer.raw, activated.raw, normWeight.raw,
+                                                      rows, cols, tokenCount, rmsEps))
+
+    def encodeFusedFinalNormGEMV(self, stream: Optional[Stream], weight: Buffer, inputBuffer: Buffer,
+                                 outputBuffer: Buffer, normWeight: Buffer, rows: int, cols: int,
+                                 rmsEps: float) -> None:
+        """dequant_q8_0_fused_final_norm_gemv: y = W . RMSNorm(x)."""
+        check(self.lib.er_hip_q8_0_fused_final_norm_gemv(self.ctx.handle, _sh(stream), weight.raw,
+                                                         inputBuffer.raw, outputBuffer.raw,
+                                                         normWeight.raw, rows, cols, rmsEps))
+
+    def encodeGEMVF16Out(self, stream: Optional[Stream], weight: Buffer, inputBuffer: Buffer,
+                         outputHalf: Buffer, rows: int, cols: int) -> None:
+        """dequant_q8_0_gemv_f16out: y = W . x stored as fp16."""
+        check(self.lib.er_hip_q8_0_gemv_f16out(self.ctx.handle, _sh(stream), weight.raw,
+                                               inputBuffer.raw, outputHalf.raw, rows, cols))
+
+    def encodeGEMVAdd(self, stream: Optional[Stream], weight: Buffer, inputBuffer: Buffer,
+                      residual: Buffer, outputBuffer: Buffer, rows: int, cols: int) -> None:
+        """dequant_q8_0_gemv_add: y = W . x + residual."""
+        check(self.lib.er_hip_q8_0_gemv_add(self.ctx.handle, _sh(stream), weight.raw,
+                                            inputBuffer.raw, residual.raw, outputBuffer.raw, rows, cols))

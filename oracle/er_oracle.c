@@ -21,6 +21,9 @@
  *   - quantize_q8_0_rows: closed-form checks (max |v| maps to +-127, rint
  *     ties-to-even, zero rows) and round-trip error bound.
  *   - argmax: brute force with lowest-index ties.
+ *   - rmsnorm: unit RMS of the output for w = 1, scale invariance, a
+ *     constant vector's closed form; silu: silu(0) = 0, silu(v) - silu(-v) = v,
+ *     the sigmoid limits.
  *   - top1: equals argmax on finite values (brute force); hand-derived
  *     answers for NaN candidates and all -inf inputs.
  *   - xoshiro256** / splitmix64: published reference outputs.
@@ -536,6 +539,19 @@ float er_ref_gelu_tanh(float v) {
     float inner = c * (v + 0.044715f * v * v * v);
     return v * 0.5f * (1.0f + tanhf(inner));
 }
+
+/* RMSNorm as FusedKernelTests.cpuRMSNorm (FusedKernelTests.swift:53-57):
+ * sequential fp32 sum of squares, scale = 1 / sqrt(sum / n + eps),
+ * out[i] = x[i] * scale * w[i] (left to right). */
+void er_ref_rmsnorm(const float *x, const float *w, uint32_t n, float eps, float *out) {
+    float sumSq = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) sumSq = sumSq + x[i] * x[i];
+    const float scale = 1.0f / sqrtf(sumSq / (float)n + eps);
+    for (uint32_t i = 0; i < n; ++i) out[i] = x[i] * scale * w[i];
+}
+
+/* FusedKernelTests.silu (FusedKernelTests.swift:85-87): x / (1 + exp(-x)). */
+float er_ref_silu(float v) { return v / (1.0f + expf(-v)); }
 
 /* ------------------------------------------------------------------------ */
 /* Greedy top-1 over logits: lowest index wins ties, as the reference's

@@ -63,6 +63,10 @@ def load():
     lib.er_ref_gelu_tanh.restype = C.c_float
     lib.er_ref_argmax.argtypes = [f32p, C.c_uint32]
     lib.er_ref_argmax.restype = C.c_uint32
+    lib.er_ref_rmsnorm.argtypes = [f32p, f32p, C.c_uint32, C.c_float, f32p]
+    lib.er_ref_rmsnorm.restype = None
+    lib.er_ref_silu.argtypes = [C.c_float]
+    lib.er_ref_silu.restype = C.c_float
     lib.er_ref_top1.argtypes = [f32p, C.c_uint32]
     lib.er_ref_top1.restype = C.c_uint32
     lib.er_ref_max_threads.argtypes = []
@@ -153,6 +157,20 @@ def gelu_tanh(v) -> np.ndarray:
 def argmax(v) -> int:
     a, ap = _f32(v)
     return int(load().er_ref_argmax(ap, a.size))
+
+
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    a, ap = _f32(x)
+    b, bp = _f32(w)
+    assert a.size == b.size
+    out = np.empty(a.size, np.float32)
+    load().er_ref_rmsnorm(ap, bp, a.size, eps, out.ctypes.data_as(f32p))
+    return out
+
+
+def silu(v) -> np.ndarray:
+    f = load().er_ref_silu
+    return np.array([f(float(t)) for t in np.asarray(v, np.float32).ravel()], np.float32)
 
 
 def top1(v) -> int:

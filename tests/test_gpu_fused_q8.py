@@ -1,0 +1,165 @@
+"""Fused Q8_0 projections (dequant_q8_0_fused_qkv / _fused_gate_up_silu /
+_fused_final_norm_gemv / _gemv_f16out / _gemv_add) against the CPU oracle:
+RMSNorm restated from FusedKernelTests.cpuRMSNorm, the Q8_0 GEMV oracle,
+silu from FusedKernelTests.silu.  Bar: relative L2 <= 1e-3 per output
+(fp16 outputs compared with the fp16 rounding of the oracle), on the
+reference tests' shapes (dim 128, q 64, kv 32, inter 96, 1 and 3 tokens) and
+on Llama-sized ones; batched calls equal per-token calls exactly."""
+import numpy as np
+import pytest
+
+import edgerunner_amd.synth as synth
+from edgerunner_amd import EncodingFailed, FusedQ8Kernel, GEMVKernel, InvalidVectorShape
+from oracle import ref
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+EPS = 1e-5
+
+
+@pytest.fixture(scope="module")
+def fk(ctx):
+    return FusedQ8Kernel(ctx)
+
+
+def q8(M, K, t):
+    return synth.q8_0(synth.seed(70, t), M, K)
+
+
+def norm_weight(K, t):
+    """U[0.5, 1.5) as the reference tests' normW (24-bit uniforms from the seeded generator)."""
+    u = (synth.rng_outputs(synth.seed(70, 50 + t), K) >> np.uint64(40)).astype(np.float32) / np.float32(2 ** 24)
+    return (np.float32(0.5) + u).astype(np.float32)
+
+
+def oracle_proj(W, x_t, nw, M, K):
+    n = ref.rmsnorm(x_t, nw, EPS) if nw is not None else x_t
+    return ref.gemv("q8_0", W, n, M, K, threads=ref.max_threads())
+
+
+@pytest.mark.parametrize("dim,qd,kvd,T", [(128, 64, 32, 1), (128, 64, 32, 3), (4096, 4096, 1024, 1),
+                                          (4096, 4096, 1024, 4), (2048, 2048, 512, 2)])
+def test_fused_qkv(ctx, fk, dim, qd, kvd, T):
+    Wq, Wk, Wv = q8(qd, dim, 1), q8(kvd, dim, 2), q8(kvd, dim, 3)
+    x = synth.normal_f32(synth.seed(70, 10 + T), T * dim)
+    nw = norm_weight(dim, 0)
+    bufs = [ctx.upload(a) for a in (Wq, Wk, Wv, x, nw)]
+    oq, ok, ov = ctx.alloc(4 * T * qd), ctx.alloc(4 * T * kvd), ctx.alloc(2 * T * kvd)
+    try:
+        fk.encodeFusedQKV(None, bufs[0], bufs[1], bufs[2], bufs[3], oq, ok, ov, bufs[4], qd, kvd, dim, T, EPS)
+        ctx.synchronize()
+        q = oq.download(np.float32).reshape(T, qd)
+        k = ok.download(np.float32).reshape(T, kvd)
+        v = ov.download(np.float16).reshape(T, kvd)
+    finally:
+        for b in bufs + [oq, ok, ov]:
+            b.free()
+    for t in range(T):
+        xt = x[t * dim:(t + 1) * dim]
+        assert rel_l2(q[t], oracle_proj(Wq, xt, nw, qd, dim)) < TOL
+        assert rel_l2(k[t], oracle_proj(Wk, xt, nw, kvd, dim)) < TOL
+        ev = oracle_proj(Wv, xt, nw, kvd, dim).astype(np.float16).astype(np.float32)
+        assert rel_l2(v[t].astype(np.float32), ev) < TOL
+
+
+@pytest.mark.parametrize("dim,inter,T", [(128, 96, 3), (128, 96, 1), (4096, 14336, 2), (1024, 3072, 5)])
+def test_fused_gate_up_silu(ctx, fk, dim, inter, T):
+    Wg, Wu = q8(inter, dim, 4), q8(inter, dim, 5)
+    x = synth.normal_f32(synth.seed(70, 20 + T), T * dim)
+    nw = norm_weight(dim, 1)
+    bufs = [ctx.upload(a) for a in (Wg, Wu, x, nw)]
+    out = ctx.alloc(4 * T * inter)
+    try:
+        fk.encodeFusedGateUpSilu(None, bufs[0], bufs[1], bufs[2], out, bufs[3], inter, dim, T, EPS)
+        ctx.synchronize()
+        got = out.download(np.float32).reshape(T, inter)
+    finally:
+        for b in bufs + [out]:
+            b.free()
+    for t in range(T):
+        xt = x[t * dim:(t + 1) * dim]
+        g = oracle_proj(Wg, xt, nw, inter, dim)
+        u = oracle_proj(Wu, xt, nw, inter, dim)
+        assert rel_l2(got[t], ref.silu(g) * u) < TOL
+
+
+@pytest.mark.parametrize("rows,dim", [(256, 128), (32000, 4096), (151936, 1024)])
+def test_fused_final_norm_gemv(ctx, fk, rows, dim):
+    W = q8(rows, dim, 6)
+    x = synth.normal_f32(synth.seed(70, 30), dim)
+    nw = norm_weight(dim, 2)
+    bufs = [ctx.upload(a) for a in (W, x, nw)]
+    out = ctx.alloc(4 * rows)
+    try:
+        fk.encodeFusedFinalNormGEMV(None, bufs[0], bufs[1], out, bufs[2], rows, dim, EPS)
+        ctx.synchronize()
+        got = out.download(np.float32)
+    finally:
+        for b in bufs + [out]:
+            b.free()
+    assert rel_l2(got, oracle_proj(W, x, nw, rows, dim)) < TOL
+
+
+@pytest.mark.parametrize("rows,dim", [(96, 128), (1024, 4096), (4096, 14336)])
+def test_gemv_f16out_and_add(ctx, fk, rows, dim):
+    W = q8(rows, dim, 7)
+    x = synth.normal_f32(synth.seed(70, 31), dim)
+    res = synth.normal_f32(synth.seed(70, 32), rows)
+    wb, xb, rb = ctx.upload(W), ctx.upload(x), ctx.upload(res)
+    yh, ya = ctx.alloc(2 * rows), ctx.alloc(4 * rows)
+    try:
+        fk.encodeGEMVF16Out(None, wb, xb, yh, rows, dim)
+        fk.encodeGEMVAdd(None, wb, xb, rb, ya, rows, dim)
+        ctx.synchronize()
+        h = yh.download(np.float16).astype(np.float32)
+        a = ya.download(np.float32)
+    finally:
+        for b in (wb, xb, rb, yh, ya):
+            b.free()
+    exp = oracle_proj(W, x, None, rows, dim)
+    assert rel_l2(h, exp.astype(np.float16).astype(np.float32)) < TOL
+    assert rel_l2(a, exp + res) < TOL
+    plain = GEMVKernel(ctx).executeQ8_0Weights(W, x, rows, dim)
+    assert np.allclose(a, plain + res, rtol=1e-5, atol=1e-5 * float(np.max(np.abs(plain))))
+
+
+def test_batched_equals_per_token(ctx, fk):
+    dim, qd, kvd, T = 1024, 1024, 256, 4
+    Wq, Wk, Wv = q8(qd, dim, 11), q8(kvd, dim, 12), q8(kvd, dim, 13)
+    x = synth.normal_f32(synth.seed(70, 40), T * dim)
+    nw = norm_weight(dim, 3)
+    bufs = [ctx.upload(a) for a in (Wq, Wk, Wv, x, nw)]
+    outs = [ctx.alloc(4 * T * qd), ctx.alloc(4 * T * kvd), ctx.alloc(2 * T * kvd)]
+    one = [ctx.alloc(4 * qd), ctx.alloc(4 * kvd), ctx.alloc(2 * kvd)]
+    try:
+        fk.encodeFusedQKV(None, *bufs[:4], *outs, bufs[4], qd, kvd, dim, T, EPS)
+        ctx.synchronize()
+        batched = [o.download(np.uint8) for o in outs]
+        for t in range(T):
+            xt = bufs[3].view(4 * t * dim, 4 * dim)
+            fk.encodeFusedQKV(None, *bufs[:3], xt, *one, bufs[4], qd, kvd, dim, 1, EPS)
+            ctx.synchronize()
+            for o, b, w in zip(one, batched, (4 * qd, 4 * kvd, 2 * kvd)):
+                assert np.array_equal(o.download(np.uint8), b[t * w:(t + 1) * w])
+    finally:
+        for b in bufs + outs + one:
+            b.free()
+
+
+def test_validation(ctx, fk):
+    W = q8(64, 128, 1)
+    wb, xb, nb = ctx.upload(W), ctx.alloc(4 * 128), ctx.alloc(4 * 128)
+    y, small = ctx.alloc(4 * 64), ctx.alloc(4 * 10)
+    try:
+        with pytest.raises(InvalidVectorShape):   # K % 64 != 0
+            fk.encodeFusedFinalNormGEMV(None, wb, xb, y, nb, 64, 96, EPS)
+        with pytest.raises(InvalidVectorShape):   # K > 16384
+            fk.encodeGEMVF16Out(None, wb, xb, y, 1, 16384 + 64)
+        with pytest.raises(EncodingFailed):       # output too small
+            fk.encodeGEMVAdd(None, wb, xb, y, small, 64, 128)
+        with pytest.raises(EncodingFailed):       # norm weight too small
+            fk.encodeFusedFinalNormGEMV(None, wb, xb, y, small, 64, 128, EPS)
+    finally:
+        for b in (wb, xb, nb, y, small):
+            b.free()

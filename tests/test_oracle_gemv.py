@@ -175,3 +175,27 @@ def test_top1_oracle_nan_and_infinity_rules():
     assert ref.top1([-inf] * 8) == 0
     assert ref.top1([-inf, -inf, -inf, -inf, -inf, -5.0, -inf, -inf]) == 5
     assert ref.top1([0, 0, 0, 0, inf, 0, 0, inf]) == 4
+
+
+def test_rmsnorm_oracle():
+    """cpuRMSNorm (FusedKernelTests.swift:53-57): with w = 1 the output has
+    unit RMS (eps small), scaling x does not change it, and a constant
+    vector c maps to c / sqrt(c^2 + eps) * w exactly as fp32 evaluates it."""
+    x = synth.normal_f32(11, 4096) * 3.0
+    ones = np.ones(4096, np.float32)
+    n = ref.rmsnorm(x, ones, 1e-6)
+    assert abs(float(np.sqrt(np.mean(n.astype(np.float64) ** 2))) - 1.0) < 1e-5
+    assert np.allclose(ref.rmsnorm(x * 8.0, ones, 0.0), ref.rmsnorm(x, ones, 0.0), rtol=1e-5, atol=1e-6)
+    w = np.linspace(0.5, 1.5, 64).astype(np.float32)
+    c = np.full(64, 0.25, np.float32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(0.0625) + np.float32(1e-5))
+    assert np.array_equal(ref.rmsnorm(c, w, 1e-5), (c * scale * w).astype(np.float32))
+
+
+def test_silu_oracle():
+    """silu (FusedKernelTests.swift:85-87): odd-part identity, zero, limits."""
+    xs = np.linspace(-20, 20, 401).astype(np.float32)
+    s, sm = ref.silu(xs), ref.silu(-xs)
+    assert np.allclose(s - sm, xs, atol=1e-5)
+    assert ref.silu([0.0])[0] == 0.0
+    assert abs(ref.silu([30.0])[0] - 30.0) < 1e-5 and abs(ref.silu([-30.0])[0]) < 1e-10
