@@ -140,6 +140,9 @@ SIGNATURES = {
     "er_hip_q8_0_fused_qkv": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer,
                                         er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32,
                                         _u32, C.c_float]),
+    "er_hip_q8_0_fused_qkv_turbo": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer,
+                                              er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32,
+                                              _u32, C.c_float]),
     "er_hip_q8_0_fused_gate_up_silu": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer,
                                                  er_buffer, er_buffer, _u32, _u32, _u32, C.c_float]),
     "er_hip_q8_0_fused_final_norm_gemv": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer,

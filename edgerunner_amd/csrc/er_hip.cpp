@@ -1159,21 +1159,37 @@ er_status er_hip_quantize_q8_0_rows(er_hip_ctx *ctx, er_stream stream, er_buffer
                                 destination_row_base, blocks_per_row);
 }
 
-er_status er_hip_q8_0_fused_qkv(er_hip_ctx *ctx, er_stream stream, er_buffer wq, er_buffer wk, er_buffer wv,
-                                er_buffer input, er_buffer out_q, er_buffer out_k, er_buffer out_v_f16,
-                                er_buffer norm_weight, uint32_t q_rows, uint32_t kv_rows, uint32_t cols,
-                                uint32_t token_count, float rms_eps) {
+er_status q8_fused_qkv(er_hip_ctx *ctx, er_stream stream, const char *name, bool vHalf, er_buffer wq,
+                       er_buffer wk, er_buffer wv, er_buffer input, er_buffer out_q, er_buffer out_k,
+                       er_buffer out_v, er_buffer norm_weight, uint32_t q_rows, uint32_t kv_rows, uint32_t cols,
+                       uint32_t token_count, float rms_eps) {
     Q8FusedSpec f{};
-    f.name = "dequant_q8_0_fused_qkv";
+    f.name = name;
     f.count = 3;
     f.W[0] = wq, f.W[1] = wk, f.W[2] = wv;
-    f.y[0] = out_q, f.y[1] = out_k, f.y[2] = out_v_f16;
+    f.y[0] = out_q, f.y[1] = out_k, f.y[2] = out_v;
     f.M[0] = q_rows, f.M[1] = kv_rows, f.M[2] = kv_rows;
-    f.halfMask = 4u;
+    f.halfMask = vHalf ? 4u : 0u;
     f.normW = norm_weight;
     f.eps = rms_eps;
     if (!norm_weight.data) return fail(ER_ERR_INVALID_ARGUMENT, "%s: null norm weight", f.name);
     return encode_q8_fused(ctx, stream, f, input, token_count, cols);
+}
+
+er_status er_hip_q8_0_fused_qkv(er_hip_ctx *ctx, er_stream stream, er_buffer wq, er_buffer wk, er_buffer wv,
+                                er_buffer input, er_buffer out_q, er_buffer out_k, er_buffer out_v_f16,
+                                er_buffer norm_weight, uint32_t q_rows, uint32_t kv_rows, uint32_t cols,
+                                uint32_t token_count, float rms_eps) {
+    return q8_fused_qkv(ctx, stream, "dequant_q8_0_fused_qkv", true, wq, wk, wv, input, out_q, out_k, out_v_f16,
+                        norm_weight, q_rows, kv_rows, cols, token_count, rms_eps);
+}
+
+er_status er_hip_q8_0_fused_qkv_turbo(er_hip_ctx *ctx, er_stream stream, er_buffer wq, er_buffer wk,
+                                      er_buffer wv, er_buffer input, er_buffer out_q, er_buffer out_k,
+                                      er_buffer out_v, er_buffer norm_weight, uint32_t q_rows,
+                                      uint32_t kv_rows, uint32_t cols, uint32_t token_count, float rms_eps) {
+    return q8_fused_qkv(ctx, stream, "dequant_q8_0_fused_qkv_turbo", false, wq, wk, wv, input, out_q, out_k,
+                        out_v, norm_weight, q_rows, kv_rows, cols, token_count, rms_eps);
 }
 
 er_status er_hip_q8_0_fused_gate_up_silu(er_hip_ctx *ctx, er_stream stream, er_buffer w_gate,

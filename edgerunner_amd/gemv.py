@@ -402,6 +402,15 @@ class FusedQ8Kernel:
                                              inputBuffer.raw, outQ.raw, outK.raw, outVHalf.raw,
                                              normWeight.raw, qRows, kvRows, cols, tokenCount, rmsEps))
 
+    def encodeFusedQKVTurbo(self, stream: Optional[Stream], wq: Buffer, wk: Buffer, wv: Buffer,
+                            inputBuffer: Buffer, outQ: Buffer, outK: Buffer, outV: Buffer,
+                            normWeight: Buffer, qRows: int, kvRows: int, cols: int, tokenCount: int,
+                            rmsEps: float) -> None:
+        """dequant_q8_0_fused_qkv_turbo: as encodeFusedQKV with v in fp32."""
+        check(self.lib.er_hip_q8_0_fused_qkv_turbo(self.ctx.handle, _sh(stream), wq.raw, wk.raw, wv.raw,
+                                                   inputBuffer.raw, outQ.raw, outK.raw, outV.raw,
+                                                   normWeight.raw, qRows, kvRows, cols, tokenCount, rmsEps))
+
     def encodeFusedGateUpSilu(self, stream: Optional[Stream], wGate: Buffer, wUp: Buffer,
                               inputBuffer: Buffer, activated: Buffer, normWeight: Buffer, rows: int,
                               cols: int, tokenCount: int, rmsEps: float) -> None:

@@ -252,27 +252,35 @@ er_status er_hip_quantize_q8_0_rows(er_hip_ctx *ctx, er_stream stream, er_buffer
  * a multiple of 64 no larger than 16384 (INVALID_VECTOR_SHAPE). ---- */
 
 /* dequant_q8_0_fused_qkv (ERFusedQKVParams{qRows, kvRows, cols, blocksPerRow,
- * tokenCount, rmsEps}, Dequant_Q8_0.metal:199-301): per token t, q = Wq.n,
+ * tokenCount, rmsEps}, Dequant_Q8_0.metal:199-314): per token t, q = Wq.n,
  * k = Wk.n (fp32), v = Wv.n written as fp16 (the KV-cache form). */
 er_status er_hip_q8_0_fused_qkv(er_hip_ctx *ctx, er_stream stream, er_buffer wq, er_buffer wk, er_buffer wv,
                                 er_buffer input, er_buffer out_q, er_buffer out_k, er_buffer out_v_f16,
                                 er_buffer norm_weight, uint32_t q_rows, uint32_t kv_rows, uint32_t cols,
                                 uint32_t token_count, float rms_eps);
+/* dequant_q8_0_fused_qkv_turbo (Dequant_Q8_0.metal:835-933): as
+ * er_hip_q8_0_fused_qkv with v kept in fp32 (out_v holds token_count*kv_rows
+ * floats).  dequant_q8_0_fused_qkv_turbo_hybrid_v (:935-1031) writes v as fp16
+ * and is er_hip_q8_0_fused_qkv itself. */
+er_status er_hip_q8_0_fused_qkv_turbo(er_hip_ctx *ctx, er_stream stream, er_buffer wq, er_buffer wk,
+                                      er_buffer wv, er_buffer input, er_buffer out_q, er_buffer out_k,
+                                      er_buffer out_v, er_buffer norm_weight, uint32_t q_rows,
+                                      uint32_t kv_rows, uint32_t cols, uint32_t token_count, float rms_eps);
 /* dequant_q8_0_fused_gate_up_silu (ERFusedGateUpSiluParams{rows, cols,
- * blocksPerRow, tokenCount, rmsEps}, Dequant_Q8_0.metal:410-500):
+ * blocksPerRow, tokenCount, rmsEps}, Dequant_Q8_0.metal:316-330, 399-483):
  * activated[t*rows + i] = silu(gate_i . n) * (up_i . n), silu(v) = v / (1 + exp(-v)). */
 er_status er_hip_q8_0_fused_gate_up_silu(er_hip_ctx *ctx, er_stream stream, er_buffer w_gate,
                                          er_buffer w_up, er_buffer input, er_buffer activated,
                                          er_buffer norm_weight, uint32_t rows, uint32_t cols,
                                          uint32_t token_count, float rms_eps);
-/* dequant_q8_0_fused_final_norm_gemv (Dequant_Q8_0.metal:320-389): y = W.n, one token. */
+/* dequant_q8_0_fused_final_norm_gemv (Dequant_Q8_0.metal:332-397): y = W.n, one token. */
 er_status er_hip_q8_0_fused_final_norm_gemv(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
                                             er_buffer input, er_buffer output, er_buffer norm_weight,
                                             uint32_t rows, uint32_t cols, float rms_eps);
-/* dequant_q8_0_gemv_f16out (Dequant_Q8_0.metal:502-541): y = W.x stored as fp16. */
+/* dequant_q8_0_gemv_f16out (Dequant_Q8_0.metal:485-534): y = W.x stored as fp16. */
 er_status er_hip_q8_0_gemv_f16out(er_hip_ctx *ctx, er_stream stream, er_buffer weight, er_buffer input,
                                   er_buffer output_f16, uint32_t rows, uint32_t cols);
-/* dequant_q8_0_gemv_add (Dequant_Q8_0.metal:543-586): y = W.x + residual. */
+/* dequant_q8_0_gemv_add (Dequant_Q8_0.metal:536-586): y = W.x + residual. */
 er_status er_hip_q8_0_gemv_add(er_hip_ctx *ctx, er_stream stream, er_buffer weight, er_buffer input,
                                er_buffer residual, er_buffer output, uint32_t rows, uint32_t cols);
 

@@ -124,6 +124,32 @@ def test_gemv_f16out_and_add(ctx, fk, rows, dim):
     assert np.allclose(a, plain + res, rtol=1e-5, atol=1e-5 * float(np.max(np.abs(plain))))
 
 
+def test_fused_qkv_turbo_keeps_v_fp32(ctx, fk):
+    """dequant_q8_0_fused_qkv_turbo: q and k equal the fp16-V kernel's exactly;
+    v is the fp32 value whose fp16 rounding the other kernel stores."""
+    dim, qd, kvd, T = 2048, 2048, 512, 3
+    Wq, Wk, Wv = q8(qd, dim, 21), q8(kvd, dim, 22), q8(kvd, dim, 23)
+    x = synth.normal_f32(synth.seed(70, 41), T * dim)
+    nw = norm_weight(dim, 4)
+    bufs = [ctx.upload(a) for a in (Wq, Wk, Wv, x, nw)]
+    a = [ctx.alloc(4 * T * qd), ctx.alloc(4 * T * kvd), ctx.alloc(2 * T * kvd)]
+    b = [ctx.alloc(4 * T * qd), ctx.alloc(4 * T * kvd), ctx.alloc(4 * T * kvd)]
+    try:
+        fk.encodeFusedQKV(None, *bufs[:4], *a, bufs[4], qd, kvd, dim, T, EPS)
+        fk.encodeFusedQKVTurbo(None, *bufs[:4], *b, bufs[4], qd, kvd, dim, T, EPS)
+        ctx.synchronize()
+        assert np.array_equal(a[0].download(np.float32), b[0].download(np.float32))
+        assert np.array_equal(a[1].download(np.float32), b[1].download(np.float32))
+        v32 = b[2].download(np.float32)
+        assert np.array_equal(a[2].download(np.float16), v32.astype(np.float16))
+        for t in range(T):
+            ev = oracle_proj(Wv, x[t * dim:(t + 1) * dim], nw, kvd, dim)
+            assert rel_l2(v32[t * kvd:(t + 1) * kvd], ev) < TOL
+    finally:
+        for buf in bufs + a + b:
+            buf.free()
+
+
 def test_batched_equals_per_token(ctx, fk):
     dim, qd, kvd, T = 1024, 1024, 256, 4
     Wq, Wk, Wv = q8(qd, dim, 11), q8(kvd, dim, 12), q8(kvd, dim, 13)
