@@ -6,16 +6,17 @@
 // int32 accumulation) instead of per-weight float conversions.
 //
 // Representation, per 64-value group g (positions [64g, 64g+64)):
-//   s_g  = smallest power of two with max|x| / s_g <= 2080768 = 127*2^14
-//          (0 for an all-zero group)
-//   xi   = rint(x / s_g)                   |xi| <= 2080768, exact scaling (s_g = 2^e)
-//   l0   = floor((xi + 8192) / 16384)      in [-127, 127]
-//   r    = xi - 16384 * l0                 in [-8192, 8191]
-//   l1   = floor((r + 64) / 128)           in [-64, 64]
-//   l2   = r - 128 * l1                    in [-64, 63]
-//   x   ~= s_g * (16384 * l0 + 128 * l1 + l2),   |error| <= s_g / 2 <= max|x_g| / 2^21
-// so every activation carries at least 21 significant bits relative to its
+//   s_g  = smallest power of two with max|x| / s_g <= 4161407 = 2^23 - C - 1
+//          (0 for an all-zero group), C = 64*2^16 + 128*2^8 + 128
+//   xi   = rint(x / s_g)                   exact scaling (s_g = 2^e)
+//   u    = xi + C                          in [0, 2^23): base-256 digits d0 d1 d2
+//   l0   = d0 - 64  in [-64, 63],  l1 = d1 - 128,  l2 = d2 - 128  in [-128, 127]
+//   x   ~= s_g * (65536 * l0 + 256 * l1 + l2),   |error| <= s_g / 2 <= max|x_g| / 2^22
+// so every activation carries at least 22 significant bits relative to its
 // group maximum (fp32-class), and a one-hot x is represented exactly.
+// u comes out of one FMA: x * (1/s_g) + (2^23 + C) lies in [2^23, 2^24), where
+// the fp32 spacing is 1, so the FMA's single rounding is rint and the low 23
+// bits of the result are u; its bytes are the digits (v_perm gathers them).
 //
 // LDS layout (K a multiple of 64):
 //   [0, 3K)        planes 0..2: limb bytes l0, l1, l2; 16-byte granules swizzled by xl_gswz
@@ -25,7 +26,8 @@
 
 #include "er_common.h"
 
-#define ER_XL_QMAX 2080768.0f
+#define ER_XL_QMAX 4161407.0f
+#define ER_XL_MAGIC 12615808.0f  // 2^23 + C, C = 4227200
 #define ER_XL_PLANES 3
 
 // 16-byte granule swizzle: the 8 lanes that one ds_read_b128 cycle serves read
@@ -99,17 +101,27 @@ ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uin
     mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
     float sg, inv;
     xl_scale(mx, &sg, &inv);
-    uint32_t lb[ER_XL_PLANES][4] = {};
+    // digits of u = xi + C are bytes 0..2 of fma(v, 1/s_g, 2^23 + C)
+    uint32_t u[16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const int xi = (int)__builtin_rintf(v[q] * inv);
-        const int l0 = (xi + 8192) >> 14;
-        const int r = xi - (l0 << 14);
-        const int l1 = (r + 64) >> 7;
-        const int l2 = r - (l1 << 7);
-        lb[0][q >> 2] |= ((uint32_t)l0 & 0xffu) << (8 * (q & 3));
-        lb[1][q >> 2] |= ((uint32_t)l1 & 0xffu) << (8 * (q & 3));
-        lb[2][q >> 2] |= ((uint32_t)l2 & 0xffu) << (8 * (q & 3));
+    for (int q = 0; q < 16; ++q) u[q] = __float_as_uint(__builtin_fmaf(v[q], inv, ER_XL_MAGIC));
+    uint32_t lb[ER_XL_PLANES][4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t a = u[4 * d], b = u[4 * d + 1], c = u[4 * d + 2], e = u[4 * d + 3];
+        // byte k of the result = byte `sel` of values a, b, c, e
+        const uint32_t d0 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(e, c, 0x0c0c0602u),
+                                                  __builtin_amdgcn_perm(b, a, 0x0c0c0602u), 0x05040100u);
+        const uint32_t d1 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(e, c, 0x0c0c0501u),
+                                                  __builtin_amdgcn_perm(b, a, 0x0c0c0501u), 0x05040100u);
+        const uint32_t d2 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(e, c, 0x0c0c0400u),
+                                                  __builtin_amdgcn_perm(b, a, 0x0c0c0400u), 0x05040100u);
+        // d - 128 as int8 is d ^ 0x80; d0 - 64 (d0 < 128) is d0 ^ 0x40 with bit 7
+        // set where bit 6 of d0 ^ 0x40 is set (sign extension of a 7-bit value)
+        const uint32_t t = d0 ^ 0x40404040u;
+        lb[0][d] = t ^ ((t & 0x40404040u) << 1);
+        lb[1][d] = d1 ^ 0x80808080u;
+        lb[2][d] = d2 ^ 0x80808080u;
     }
     // chunks past the end are clamped copies with a different group max: never stored
     if (tRaw < C16) {
@@ -159,7 +171,9 @@ ER_DEV void xl_read_group(const XLimbs &X, uint32_t grp, u32x4 (&xv)[ER_XL_PLANE
 }
 
 // Limb partial sums (each an exact int32 dot product) recombined into the
-// value of sum(q * xi): c0 * 2^14 + c1 * 2^7 + c2, rounded once to fp32.
+// value of sum(q * xi): c0 * 2^16 + c1 * 2^8 + c2.  c1 * 2^8 + c2 is exact in
+// int32 for every slot size used (|c1| <= 64 * 128 * 128); the result is
+// rounded to fp32 twice at most.
 ER_DEV float xl_combine(int c0, int c1, int c2) {
-    return __builtin_fmaf((float)c0, 16384.0f, (float)((c1 << 7) + c2));
+    return __builtin_fmaf((float)c0, 65536.0f, (float)((c1 << 8) + c2));
 }
