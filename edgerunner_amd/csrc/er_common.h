@@ -80,11 +80,50 @@ ER_DEV u32x2 ld8_a2(const uint8_t *p) {
 // 4 bytes at a 2-byte-aligned address (two 16-bit loads, never over-reads).
 ER_DEV uint32_t ld4_a2(const uint8_t *p) { return ld2(p) | (ld2(p + 2) << 16); }
 
-// Sum over the lanes of an aligned group of W lanes (W a power of two <= 64).
+// DPP lane moves (GFX9 encodings): quad permutations, row (16-lane) mirrors
+// and the row broadcasts of lane 15 / lane 31 into the next rows.
+#define ER_DPP_QUAD_XOR1 0xb1   // quad_perm [1,0,3,2]
+#define ER_DPP_QUAD_XOR2 0x4e   // quad_perm [2,3,0,1]
+#define ER_DPP_ROW_MIRROR 0x140
+#define ER_DPP_ROW_HALF_MIRROR 0x141
+#define ER_DPP_ROW_BCAST15 0x142
+#define ER_DPP_ROW_BCAST31 0x143
+
+// v + (v of the lane that `ctrl` selects), on the rows of `rowMask` (other
+// rows keep v).
+template <int CTRL, int ROWMASK = 0xf>
+ER_DEV float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWMASK, 0xf, false));
+}
+template <int CTRL>
+ER_DEV float dpp_max(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false)));
+}
+
+// Sum over the lanes of an aligned group of W lanes (W in {1, 2, 4, 8, 16,
+// 32, 64}); every lane of the group gets the sum.  Within a 16-lane row the
+// steps are DPP moves fused into the adds (quad swaps, then the half-row and
+// row mirrors, which pair each lane with one of the other half); rows are
+// joined by the lane-15 / lane-31 broadcasts and the total is read back from
+// the group's last lane.
 template <int W>
 ER_DEV float group_sum(float v) {
-#pragma unroll
-    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+    if constexpr (W >= 2) v = dpp_add<ER_DPP_QUAD_XOR1>(v);
+    if constexpr (W >= 4) v = dpp_add<ER_DPP_QUAD_XOR2>(v);
+    if constexpr (W >= 8) v = dpp_add<ER_DPP_ROW_HALF_MIRROR>(v);
+    if constexpr (W >= 16) v = dpp_add<ER_DPP_ROW_MIRROR>(v);
+    if constexpr (W == 32) {
+        v = dpp_add<ER_DPP_ROW_BCAST15, 0xa>(v);  // rows 1 and 3 hold the two group sums
+        const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+        const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+        v = (threadIdx.x & 32u) ? hi : lo;
+    }
+    if constexpr (W == 64) {
+        v = dpp_add<ER_DPP_ROW_BCAST15, 0xa>(v);
+        v = dpp_add<ER_DPP_ROW_BCAST31, 0xc>(v);  // row 3 holds the total
+        v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    }
     return v;
 }
 

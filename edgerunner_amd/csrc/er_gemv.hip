@@ -771,6 +771,196 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 }
 
 // ===========================================================================
+// Family 3: CU-resident integer-dot kernels (Q4_K, Q8_0; K % 256 == 0)
+// ===========================================================================
+//
+// The family-1 kernels run ~3.5 workgroups per CU, and each stages x on its
+// own.  A CU's vector-memory path returns data in request order, so the x
+// loads of every workgroup after the first on a CU wait behind the weight
+// loads of those before it, and per-workgroup barriers tie each wave's first
+// dot product to the slowest weight-load issue of its workgroup.  Here one
+// 8-wave workgroup owns a CU-sized share of the rows (grid ~ one workgroup per
+// CU), and:
+//   - waves 4..7 copy x into LDS with global_load_lds (issued before a
+//     workgroup barrier that precedes every weight load, so the x requests
+//     leave the CU first), convert it to limbs (er_xlimbs.h) and each bump an
+//     LDS counter;
+//   - every wave walks its rows with PD rows of weight loads in flight (row
+//     i + PD is issued after row i is consumed) and waits on the counter, not
+//     on a barrier, before its first dot product.
+// Row assignment: step i of lane group (wave, g) is row
+// rb + (i * ER_CU_WAVES + wave) * G + g, G = 64 / LPR rows per wave step.
+// Per-row arithmetic (slot order, lane reduction) is that of the family-1
+// kernel with the same LPR and NS.
+
+#define ER_CU_STAGERS 4               // waves ER_CU_WAVES - 4 .. ER_CU_WAVES - 1 stage x
+#define ER_CU_SPIN_LIMIT (1u << 22)   // bound on the staging-counter wait (s_sleep 1 per poll)
+
+// Per-format slot access: weights of one slot (Wt), the x side of one slot
+// (Xs), and the slot's contribution.
+struct CuQ4K {
+    struct Wt {
+        u32x4 h, qa, qb;
+    };
+    struct Xs {
+        u32x4 xv[ER_XL_PLANES][4];
+        float XL, XH, sg, live;
+        Q4Sel sel;
+    };
+    static ER_DEV size_t row_bytes(uint32_t K) { return (size_t)(K >> 8) * 144u; }
+    static ER_DEV Wt load(const uint8_t *row, uint32_t s) {
+        const uint8_t *bp = row + (s >> 2) * 144u;
+        const uint32_t p = s & 3u;
+        return Wt{ld16_a16(bp), ld16_a16(bp + 16u + 32u * p), ld16_a16(bp + 32u + 32u * p)};
+    }
+    static ER_DEV Xs xside(const XLimbs &X, uint32_t s, float live) {
+        Xs o;
+        xl_read_group(X, s, o.xv);
+        const float4 c16 = *(const float4 *)__builtin_assume_aligned(X.x16 + 4u * s, 16);
+        o.XL = c16.x + c16.y;
+        o.XH = c16.z + c16.w;
+        o.sg = live * X.sg64[s];
+        o.live = live;
+        o.sel = q4k_sel(s & 3u);
+        return o;
+    }
+    static ER_DEV float dot(const Wt &w, const Xs &xs, float acc, uint32_t M0F) {
+        return acc + q4k_slot_dot(w.h, w.qa, w.qb, xs.xv, xs.XL, xs.XH, xs.sg, xs.live, xs.sel, M0F);
+    }
+};
+
+struct CuQ8 {
+    using Wt = Q8Slot;
+    struct Xs {
+        u32x4 xv[ER_XL_PLANES][4];
+        float sg;
+    };
+    static ER_DEV size_t row_bytes(uint32_t K) { return (size_t)(K >> 6) * 68u; }
+    static ER_DEV Wt load(const uint8_t *row, uint32_t s) { return q8_slot_load(row + (size_t)s * 68u); }
+    static ER_DEV Xs xside(const XLimbs &X, uint32_t s, float live) {
+        Xs o;
+        xl_read_group(X, s, o.xv);
+        o.sg = live > 0.0f ? X.sg64[s] : 0.0f;
+        return o;
+    }
+    static ER_DEV float dot(const Wt &w, const Xs &xs, float acc, uint32_t) { return q8_slot_dot(w, xs.xv, xs.sg, acc); }
+};
+
+// LDS bytes of the family: limbs, then K fp32 values of raw x.
+ER_DEV uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
+
+template <class F, int LPR, int NS, int PD, int JC>
+ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
+                    uint32_t M, uint32_t K) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    __shared__ uint32_t staged;  // staging waves done
+    constexpr uint32_t G = 64u / LPR;
+    constexpr uint32_t STEP = ER_CU_WAVES * G;  // rows per workgroup step
+    constexpr uint32_t ROWS = STEP * JC;        // rows per workgroup
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    // wave index as a scalar: the staging branch is wave-uniform
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t g = lane / LPR, li = lane % LPR;
+    const uint32_t S = K >> 6, C16 = K >> 4;
+    const uint32_t rb = blockIdx.x * ROWS, re = min(rb + ROWS, M);  // rb < M (grid = ceil(M / ROWS))
+    const uint32_t first = rb + wave * G + g;  // row of step 0; step i adds i * STEP
+    const size_t rowBytes = F::row_bytes(K);
+    uint32_t *xraw = lds + xl_lds_bytes(K) / 4u;  // 16-byte aligned for K % 256 == 0
+
+    // Every step is loaded and computed (steps past the workgroup's rows
+    // re-read its last row and are not stored), so the loads form one
+    // straight-line sequence and each wait covers exactly the loads it needs.
+    typename F::Wt wb[PD][NS];
+    auto issue = [&](int i) {
+        const uint32_t row = min(first + (uint32_t)i * STEP, re - 1u);
+        const uint8_t *rp = W + (size_t)row * rowBytes;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) wb[i % PD][j] = F::load(rp, min(li + (uint32_t)LPR * j, S - 1u));
+    };
+
+    const uint32_t nPieces = K >> 8;               // 1 KB pieces of x
+    const uint32_t nBlocks = (nPieces + 3u) >> 2;  // 4 KB blocks: 64 chunks, one conversion pass
+    if (wave >= ER_CU_WAVES - ER_CU_STAGERS) {
+        const uint32_t si = wave - (ER_CU_WAVES - ER_CU_STAGERS);
+        if (si == 0 && lane == 0) staged = 0u;
+        for (uint32_t b = si; b < nBlocks; b += ER_CU_STAGERS)
+            for (uint32_t q = 4u * b; q < min(4u * b + 4u, nPieces); ++q)
+                __builtin_amdgcn_global_load_lds((const void *)(x + 256u * q + 4u * lane), (void *)(xraw + 256u * q),
+                                                 16, 0, 0);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the counter reset has landed
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();  // x requests of the workgroup precede its weight requests
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's x pieces are in LDS
+        __builtin_amdgcn_sched_barrier(0);
+        for (uint32_t b = si; b < nBlocks; b += ER_CU_STAGERS) {
+            const uint32_t t = 64u * b + lane;  // 16-value chunk; lanes 4k..4k+3 hold one 64-group
+            const uint32_t tc = min(t, C16 - 1u);
+            float4 xr[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xr[q] = *(const float4 *)(xraw + 16u * tc + 4u * q);
+            xl_store_chunk(lds, K, xr, t);  // stores only chunks t < C16
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's limb stores have landed
+        if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+        for (int i = 0; i < PD && i < JC; ++i) issue(i);
+    } else {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < PD && i < JC; ++i) issue(i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the staging waves always finish; the bound only keeps a wave from
+    // spinning forever should that ever fail
+    for (uint32_t n = 0; __hip_atomic_load(&staged, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < ER_CU_STAGERS &&
+                         n < ER_CU_SPIN_LIMIT;
+         ++n)
+        __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const XLimbs X = xl_view(lds, K);
+    const uint32_t M0F = vreg_const(0x0f0f0f0fu);
+    typename F::Xs xs0;
+    if constexpr (NS == 1) xs0 = F::xside(X, min(li, S - 1u), li < S ? 1.0f : 0.0f);
+    float acc[JC];
+#pragma unroll
+    for (int i = 0; i < JC; ++i) {
+        acc[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            if constexpr (NS == 1) {
+                acc[i] = F::dot(wb[i % PD][0], xs0, acc[i], M0F);
+            } else {
+                // re-read per row: the opaque slot index keeps the compiler from
+                // hoisting NS slots of x limbs out of the row loop into registers
+                const uint32_t sRaw = li + (uint32_t)LPR * j;
+                uint32_t sx = min(sRaw, S - 1u);
+                asm volatile("" : "+v"(sx));
+                const typename F::Xs xs = F::xside(X, sx, sRaw < S ? 1.0f : 0.0f);
+                acc[i] = F::dot(wb[i % PD][j], xs, acc[i], M0F);
+                __builtin_amdgcn_sched_barrier(0);  // one slot of x limbs live at a time
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + PD < JC) issue(i + PD);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < JC; ++i) acc[i] = group_sum<LPR>(acc[i]);
+    if (li == 0) {
+#pragma unroll
+        for (int i = 0; i < JC; ++i) {
+            const uint32_t row = first + (uint32_t)i * STEP;
+            if (row < re) y[row] = acc[i];
+        }
+    }
+}
+
+// ===========================================================================
 // Family 2: fp32 kernels
 // ===========================================================================
 
@@ -1137,6 +1327,25 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
         gemv_q6k_i8<LPR, NS, R, true>(W, x, nullptr, M, K, pv, pi);                          \
     }
 ER_I8_CONFIGS(ER_I8_ENTRY)
+
+// CU-resident family: er_gemv_<fmt>_cu_l<LPR>_n<NS>_j<JC>, JC row steps per
+// wave, grid (ceil(M / (ER_CU_WAVES * 64 / LPR * JC)), batch).
+#define ER_CU_PD(NS) ((NS) <= 1 ? 3 : 2)
+#define ER_CU_ENTRY_J(fmt, F, LPR, NS, JC)                                                     \
+    extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                           \
+        er_gemv_##fmt##_cu_l##LPR##_n##NS##_j##JC(const uint8_t *__restrict__ W,               \
+                                                  const float *__restrict__ x,                \
+                                                  float *__restrict__ y, uint32_t M, uint32_t K) { \
+        gemv_cu<F, LPR, NS, ER_CU_PD(NS), JC>(W, x, y, M, K);                                  \
+    }
+#define ER_CU_ENTRIES(fmt, F, LPR, NS)                                                               \
+    ER_CU_ENTRY_J(fmt, F, LPR, NS, 1) ER_CU_ENTRY_J(fmt, F, LPR, NS, 2) ER_CU_ENTRY_J(fmt, F, LPR, NS, 3) \
+    ER_CU_ENTRY_J(fmt, F, LPR, NS, 4) ER_CU_ENTRY_J(fmt, F, LPR, NS, 5) ER_CU_ENTRY_J(fmt, F, LPR, NS, 6) \
+    ER_CU_ENTRY_J(fmt, F, LPR, NS, 7) ER_CU_ENTRY_J(fmt, F, LPR, NS, 8)
+#define ER_CU_ENTRY_Q4K(LPR, NS) ER_CU_ENTRIES(q4k, CuQ4K, LPR, NS)
+#define ER_CU_ENTRY_Q8(LPR, NS) ER_CU_ENTRIES(q8_0, CuQ8, LPR, NS)
+ER_CU_CONFIGS_Q4K(ER_CU_ENTRY_Q4K)
+ER_CU_CONFIGS_Q8(ER_CU_ENTRY_Q8)
 
 // Multi-matrix and GeGLU Q4_K kernels: R counts row computations per lane
 // group (GeGLU: R/2 gate rows + the matching up rows).

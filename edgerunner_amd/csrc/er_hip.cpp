@@ -109,6 +109,22 @@ constexpr int kI8Count = (int)(sizeof(kI8Cfg) / sizeof(kI8Cfg[0]));
 // length use them (the default dynamic LDS limit is 64 KiB).
 constexpr uint32_t kI8MaxK = 16384;
 
+// CU-resident Q4_K / Q8_0 configurations {LPR, NS} (er_gemv_cfg.h).
+struct CuCfg {
+    uint8_t lpr, ns;
+};
+#define ER_CU_ROW(LPR, NS) {LPR, NS},
+constexpr CuCfg kCuCfgQ4K[] = {ER_CU_CONFIGS_Q4K(ER_CU_ROW)};
+constexpr CuCfg kCuCfgQ8[] = {ER_CU_CONFIGS_Q8(ER_CU_ROW)};
+#undef ER_CU_ROW
+constexpr int kCuCountQ4K = (int)(sizeof(kCuCfgQ4K) / sizeof(kCuCfgQ4K[0]));
+constexpr int kCuCountQ8 = (int)(sizeof(kCuCfgQ8) / sizeof(kCuCfgQ8[0]));
+// The CU-resident family covers Q4_K rows of up to 128 slots and Q8_0 rows of
+// up to 64 (pick_cu finds no configuration beyond), and holds limbs plus raw x
+// in LDS: 3K + K/4 + K/16 + 4K bytes.
+constexpr uint32_t kCuMaxK = 8192;
+constexpr uint32_t cu_lds_bytes(uint32_t K) { return 3u * K + K / 16u * 4u + K / 64u * 4u + 4u * K; }
+
 // Multi-matrix / GeGLU Q4_K configurations {LPR, NS, R} (er_gemv_cfg.h).
 #define ER_I8_ROW(LPR, NS, R) {LPR, NS, R},
 constexpr I8Cfg kI8MultiCfg[] = {ER_I8_MULTI_CONFIGS(ER_I8_ROW)};
@@ -143,12 +159,15 @@ struct er_hip_ctx {
     hipFunction_t fnQ8I8[kI8Count] = {};
     hipFunction_t fnQ6KI8[kI8Count] = {};
     hipFunction_t fnQ6KTop1[kI8Count] = {};
+    hipFunction_t fnQ4KCu[kCuCountQ4K][ER_CU_MAX_STEPS] = {};
+    hipFunction_t fnQ8Cu[kCuCountQ8][ER_CU_MAX_STEPS] = {};
     hipFunction_t fnQ4KMulti[kI8MultiCount] = {};
     hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
     hipFunction_t fnQ8Multi[kI8MultiCount] = {};
     hipFunction_t fnQ8Silu[kI8MultiCount] = {};
     int cu_count = 0;
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
+    int cu_mode = -1;      // ER_HIP_GEMV_CU: 0 never, 1 whenever it applies, unset: by shape
     int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1 selects the non-pipelined GEMM (benchmark comparison)
     uint32_t gemm_tt = 0, gemm_sk = 0;  // ER_HIP_GEMM_TILE=tt:sk (benchmark sweeps only)
     int gemv_fp32 = 0;  // ER_HIP_GEMV_FP32=1 selects the fp32 GEMV family (benchmark comparison)
@@ -264,6 +283,24 @@ int pick_i8_multi(uint32_t S, uint32_t Mt, int cu) {
     return fallback;
 }
 
+// CU-resident configuration for S slots from cfg[0..count): the fewest idle
+// slot lanes per row (LPR * NS - S), wider rows first on ties.  -1 when none
+// covers S.
+int pick_cu(const CuCfg *cfg, int count, uint32_t S) {
+    int best = -1;
+    uint32_t bestWaste = 0xffffffffu;
+    for (int i = 0; i < count; ++i) {
+        const uint32_t cover = (uint32_t)cfg[i].lpr * cfg[i].ns;
+        if (cover < S) continue;
+        const uint32_t waste = cover - S;
+        if (best < 0 || waste < bestWaste || (waste == bestWaste && cfg[i].lpr > cfg[best].lpr)) {
+            best = i;
+            bestWaste = waste;
+        }
+    }
+    return best;
+}
+
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 // Largest power of two in [4, 64] dividing the slot count (4 when none does).
@@ -348,6 +385,29 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
 
     void *args[] = {&W.data, &x.data, &y.data, &M, &K};
     const bool q8Aligned = f == Fmt::Q8_0 && K % 64u == 0;
+    // CU-resident family: Q4_K / Q8_0 rows of K % 256 == 0 up to kCuMaxK, when
+    // the matrix gives every CU at least kCuMinRows rows per token
+    constexpr uint32_t kCuMinRows = 32;
+    const bool cuFits = f != Fmt::Q6_K && K % 256u == 0 && K <= kCuMaxK && ctx->gemv_fp32 == 0 &&
+                        ctx->i8_override < 0 &&
+                        (uint64_t)cu_lds_bytes(K) + 1024u <= ctx->info.lds_per_workgroup;
+    if (cuFits && (ctx->cu_mode == 1 || (ctx->cu_mode < 0 && M >= kCuMinRows * (uint32_t)ctx->cu_count))) {
+        const int ci = f == Fmt::Q4_K ? pick_cu(kCuCfgQ4K, kCuCountQ4K, K / 64u) : pick_cu(kCuCfgQ8, kCuCountQ8, K / 64u);
+        if (ci >= 0) {
+            const CuCfg &c = f == Fmt::Q4_K ? kCuCfgQ4K[ci] : kCuCfgQ8[ci];
+            // about one workgroup per CU over all tokens: steps (ER_CU_WAVES lane
+            // groups of rows) per workgroup for that, at most ER_CU_MAX_STEPS
+            const uint32_t step = ER_CU_WAVES * (64u / c.lpr);
+            const uint32_t perToken = std::max<uint32_t>(1u, (uint32_t)ctx->cu_count / batch);
+            const uint32_t steps =
+                std::min<uint32_t>(ER_CU_MAX_STEPS, ((M + perToken - 1u) / perToken + step - 1u) / step);
+            const uint32_t rowsPerWg = step * steps;
+            dim3 grid((M + rowsPerWg - 1u) / rowsPerWg, batch, 1);
+            return launch_fn(f == Fmt::Q4_K ? ctx->fnQ4KCu[ci][steps - 1] : ctx->fnQ8Cu[ci][steps - 1],
+                             f == Fmt::Q4_K ? "er_gemv_q4k_cu" : "er_gemv_q8_0_cu", grid,
+                             dim3(64u * ER_CU_WAVES, 1, 1), cu_lds_bytes(K), stream, args);
+        }
+    }
     if ((f != Fmt::Q8_0 || q8Aligned) && K <= kI8MaxK && ctx->gemv_fp32 == 0) {
         int ci = pick_i8(K / 64u, M, ctx->cu_count);
         if (ctx->i8_override >= 0 && (uint32_t)kI8Cfg[ctx->i8_override].lpr *
@@ -820,6 +880,24 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
             }
         }
     }
+    for (int fmt = 0; fmt < 2; ++fmt) {
+        const CuCfg *cfg = fmt == 0 ? kCuCfgQ4K : kCuCfgQ8;
+        const int count = fmt == 0 ? kCuCountQ4K : kCuCountQ8;
+        for (int i = 0; i < count; ++i)
+            for (int jc = 1; jc <= ER_CU_MAX_STEPS; ++jc) {
+                char name[64];
+                std::snprintf(name, sizeof(name), "er_gemv_%s_cu_l%u_n%u_j%d", fmt == 0 ? "q4k" : "q8_0",
+                              (unsigned)cfg[i].lpr, (unsigned)cfg[i].ns, jc);
+                hipFunction_t *slot = fmt == 0 ? &ctx->fnQ4KCu[i][jc - 1] : &ctx->fnQ8Cu[i][jc - 1];
+                e = hipModuleGetFunction(slot, ctx->module, name);
+                if (e != hipSuccess) {
+                    (void)hipModuleUnload(ctx->module);
+                    delete ctx;
+                    return fail(ER_ERR_FUNCTION_NOT_FOUND, "functionNotFound(%s): %s", name,
+                                hipGetErrorString(e));
+                }
+            }
+    }
     for (int i = 0; i < kI8MultiCount; ++i) {
         char name[64];
         static const char *const kinds[4] = {"q4k_multi", "q4k_geglu", "q8_0_multi", "q8_0_silu"};
@@ -847,6 +925,7 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
             ctx->gemm_sk = b;
         }
     }
+    if (const char *cv = std::getenv("ER_HIP_GEMV_CU")) ctx->cu_mode = std::atoi(cv) != 0 ? 1 : 0;
     if (const char *ov = std::getenv("ER_HIP_GEMV_CONFIG")) {
         unsigned l = 0, n = 0, r = 0;
         if (std::sscanf(ov, "%u:%u:%u", &l, &n, &r) == 3)

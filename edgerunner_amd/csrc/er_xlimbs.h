@@ -97,8 +97,8 @@ ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uin
         mx = fmaxf(mx, fabsf(v[q]));
         sm += v[q];
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    mx = dpp_max<ER_DPP_QUAD_XOR1>(mx);
+    mx = dpp_max<ER_DPP_QUAD_XOR2>(mx);
     float sg, inv;
     xl_scale(mx, &sg, &inv);
     // digits of u = xi + C are bytes 0..2 of fma(v, 1/s_g, 2^23 + C)
