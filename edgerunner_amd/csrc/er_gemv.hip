@@ -793,7 +793,9 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // Per-row arithmetic (slot order, lane reduction) is that of the family-1
 // kernel with the same LPR and NS.
 
+#ifndef ER_CU_STAGERS
 #define ER_CU_STAGERS 4               // waves ER_CU_WAVES - 4 .. ER_CU_WAVES - 1 stage x
+#endif
 #define ER_CU_SPIN_LIMIT (1u << 22)   // bound on the staging-counter wait (s_sleep 1 per poll)
 
 // Per-format slot access: weights of one slot (Wt), the x side of one slot
@@ -807,13 +809,13 @@ struct CuQ4K {
         float XL, XH, sg, live;
         Q4Sel sel;
     };
-    static ER_DEV size_t row_bytes(uint32_t K) { return (size_t)(K >> 8) * 144u; }
-    static ER_DEV Wt load(const uint8_t *row, uint32_t s) {
+    ER_DEV size_t row_bytes(uint32_t K) { return (size_t)(K >> 8) * 144u; }
+    ER_DEV Wt load(const uint8_t *row, uint32_t s) {
         const uint8_t *bp = row + (s >> 2) * 144u;
         const uint32_t p = s & 3u;
         return Wt{ld16_a16(bp), ld16_a16(bp + 16u + 32u * p), ld16_a16(bp + 32u + 32u * p)};
     }
-    static ER_DEV Xs xside(const XLimbs &X, uint32_t s, float live) {
+    ER_DEV Xs xside(const XLimbs &X, uint32_t s, float live) {
         Xs o;
         xl_read_group(X, s, o.xv);
         const float4 c16 = *(const float4 *)__builtin_assume_aligned(X.x16 + 4u * s, 16);
@@ -824,7 +826,7 @@ struct CuQ4K {
         o.sel = q4k_sel(s & 3u);
         return o;
     }
-    static ER_DEV float dot(const Wt &w, const Xs &xs, float acc, uint32_t M0F) {
+    ER_DEV float dot(const Wt &w, const Xs &xs, float acc, uint32_t M0F) {
         return acc + q4k_slot_dot(w.h, w.qa, w.qb, xs.xv, xs.XL, xs.XH, xs.sg, xs.live, xs.sel, M0F);
     }
 };
@@ -835,15 +837,15 @@ struct CuQ8 {
         u32x4 xv[ER_XL_PLANES][4];
         float sg;
     };
-    static ER_DEV size_t row_bytes(uint32_t K) { return (size_t)(K >> 6) * 68u; }
-    static ER_DEV Wt load(const uint8_t *row, uint32_t s) { return q8_slot_load(row + (size_t)s * 68u); }
-    static ER_DEV Xs xside(const XLimbs &X, uint32_t s, float live) {
+    ER_DEV size_t row_bytes(uint32_t K) { return (size_t)(K >> 6) * 68u; }
+    ER_DEV Wt load(const uint8_t *row, uint32_t s) { return q8_slot_load(row + (size_t)s * 68u); }
+    ER_DEV Xs xside(const XLimbs &X, uint32_t s, float live) {
         Xs o;
         xl_read_group(X, s, o.xv);
         o.sg = live > 0.0f ? X.sg64[s] : 0.0f;
         return o;
     }
-    static ER_DEV float dot(const Wt &w, const Xs &xs, float acc, uint32_t) { return q8_slot_dot(w, xs.xv, xs.sg, acc); }
+    ER_DEV float dot(const Wt &w, const Xs &xs, float acc, uint32_t) { return q8_slot_dot(w, xs.xv, xs.sg, acc); }
 };
 
 // LDS bytes of the family: limbs, then K fp32 values of raw x.
@@ -1330,7 +1332,7 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
 
 // CU-resident family: er_gemv_<fmt>_cu_l<LPR>_n<NS>_j<JC>, JC row steps per
 // wave, grid (ceil(M / (ER_CU_WAVES * 64 / LPR * JC)), batch).
-#define ER_CU_PD(NS) ((NS) <= 1 ? 3 : 2)
+#define ER_CU_PD(NS) 2  // rows of weight loads in flight per wave (2 measured best for 1 and 2 slots)
 #define ER_CU_ENTRY_J(fmt, F, LPR, NS, JC)                                                     \
     extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                           \
         er_gemv_##fmt##_cu_l##LPR##_n##NS##_j##JC(const uint8_t *__restrict__ W,               \

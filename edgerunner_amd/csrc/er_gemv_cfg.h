@@ -33,7 +33,9 @@
 // wave.  Q4_K: NS <= 2 (rows up to 8192 weights); Q8_0: NS = 1 (up to 4096).
 // Beyond that the unrolled steps keep too many slots of x limbs live and the
 // kernels spill.
+#ifndef ER_CU_WAVES
 #define ER_CU_WAVES 8
+#endif
 #define ER_CU_MAX_STEPS 8
 #define ER_CU_CONFIGS_Q4K(X) X(16, 1) X(16, 2) X(32, 1) X(32, 2) X(64, 1) X(64, 2)
 #define ER_CU_CONFIGS_Q8(X) X(16, 1) X(32, 1) X(64, 1)

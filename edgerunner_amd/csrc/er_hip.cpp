@@ -386,24 +386,31 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     void *args[] = {&W.data, &x.data, &y.data, &M, &K};
     const bool q8Aligned = f == Fmt::Q8_0 && K % 64u == 0;
     // CU-resident family: Q4_K / Q8_0 rows of K % 256 == 0 up to kCuMaxK, when
-    // the matrix gives every CU at least kCuMinRows rows per token
-    constexpr uint32_t kCuMinRows = 32;
+    // a CU's share of the rows is 2..2*ER_CU_MAX_STEPS row steps per token:
+    // below that the lane-group family, with more workgroups, is faster; above
+    // it the capped step count needs several workgroup rounds
     const bool cuFits = f != Fmt::Q6_K && K % 256u == 0 && K <= kCuMaxK && ctx->gemv_fp32 == 0 &&
-                        ctx->i8_override < 0 &&
+                        ctx->i8_override < 0 && ctx->cu_mode != 0 &&
                         (uint64_t)cu_lds_bytes(K) + 1024u <= ctx->info.lds_per_workgroup;
-    if (cuFits && (ctx->cu_mode == 1 || (ctx->cu_mode < 0 && M >= kCuMinRows * (uint32_t)ctx->cu_count))) {
-        const int ci = f == Fmt::Q4_K ? pick_cu(kCuCfgQ4K, kCuCountQ4K, K / 64u) : pick_cu(kCuCfgQ8, kCuCountQ8, K / 64u);
-        if (ci >= 0) {
-            const CuCfg &c = f == Fmt::Q4_K ? kCuCfgQ4K[ci] : kCuCfgQ8[ci];
-            // about one workgroup per CU over all tokens: steps (ER_CU_WAVES lane
-            // groups of rows) per workgroup for that, at most ER_CU_MAX_STEPS
-            const uint32_t step = ER_CU_WAVES * (64u / c.lpr);
-            const uint32_t perToken = std::max<uint32_t>(1u, (uint32_t)ctx->cu_count / batch);
+    const int cuCi = !cuFits ? -1
+                     : f == Fmt::Q4_K ? pick_cu(kCuCfgQ4K, kCuCountQ4K, K / 64u)
+                                      : pick_cu(kCuCfgQ8, kCuCountQ8, K / 64u);
+    if (cuCi >= 0) {
+        const CuCfg &c = f == Fmt::Q4_K ? kCuCfgQ4K[cuCi] : kCuCfgQ8[cuCi];
+        const uint32_t step = ER_CU_WAVES * (64u / c.lpr);  // rows per workgroup step
+        // The choice of family depends on M and K only, so a batched call and
+        // its per-token calls run the same per-row arithmetic (bit-identical
+        // outputs); the batch only changes the row partition.
+        const uint32_t cu = (uint32_t)ctx->cu_count;
+        const uint32_t needed1 = ((M + cu - 1u) / cu + step - 1u) / step;  // steps per CU, one token
+        if (ctx->cu_mode == 1 || (needed1 >= 2u && needed1 <= 2u * ER_CU_MAX_STEPS)) {
+            // about one workgroup per CU over all tokens, at most ER_CU_MAX_STEPS steps each
+            const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
             const uint32_t steps =
                 std::min<uint32_t>(ER_CU_MAX_STEPS, ((M + perToken - 1u) / perToken + step - 1u) / step);
             const uint32_t rowsPerWg = step * steps;
             dim3 grid((M + rowsPerWg - 1u) / rowsPerWg, batch, 1);
-            return launch_fn(f == Fmt::Q4_K ? ctx->fnQ4KCu[ci][steps - 1] : ctx->fnQ8Cu[ci][steps - 1],
+            return launch_fn(f == Fmt::Q4_K ? ctx->fnQ4KCu[cuCi][steps - 1] : ctx->fnQ8Cu[cuCi][steps - 1],
                              f == Fmt::Q4_K ? "er_gemv_q4k_cu" : "er_gemv_q8_0_cu", grid,
                              dim3(64u * ER_CU_WAVES, 1, 1), cu_lds_bytes(K), stream, args);
         }

@@ -110,3 +110,19 @@ def test_cu_family_equals_lane_matched_family1(cu_gemv, fmt):
         c0.close()
     y1 = getattr(cu_gemv, EXEC[fmt])(W, x, M, K)
     assert np.array_equal(y0, y1)
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("M,K,T", [(8192, 2048, 3), (16384, 1024, 2), (4096, 4096, 4)])
+def test_default_dispatch_batched_equals_per_token(gemv, fmt, M, K, T):
+    """Default dispatch on shapes the CU-resident family takes: the family is
+    chosen from M and K alone, so batched and per-token calls agree bit for
+    bit although the batch changes the row partition."""
+    W = synth.weights(fmt, synth.seed(84, 0), M, K, **DSCALE[fmt])
+    x = synth.normal_f32(synth.seed(84, 1), T * K)
+    yb = getattr(gemv, EXEC_B[fmt])(W, x, T, M, K).reshape(T, M)
+    for t in range(T):
+        single = getattr(gemv, EXEC[fmt])(W, x[t * K:(t + 1) * K], M, K)
+        assert np.array_equal(yb[t], single)
+    exp = ref.gemv(fmt, W, x[:K], M, K, threads=ref.max_threads())
+    assert rel_l2(yb[0], exp) < TOL
