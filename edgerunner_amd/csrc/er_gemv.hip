@@ -797,6 +797,8 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 #define ER_CU_STAGERS 4               // waves ER_CU_WAVES - 4 .. ER_CU_WAVES - 1 stage x
 #endif
 #define ER_CU_SPIN_LIMIT (1u << 22)   // bound on the staging-counter wait (s_sleep 1 per poll)
+#define ER_CU_PD 2                    // rows of weight loads in flight per wave (2 measured best)
+#define ER_CU_UNROLL 4                // unroll of the rolled step loop
 
 // Per-format slot access: weights of one slot (Wt), the x side of one slot
 // (Xs), and the slot's contribution.
@@ -851,34 +853,45 @@ struct CuQ8 {
 // LDS bytes of the family: limbs, then K fp32 values of raw x.
 ER_DEV uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 
+// JC > 0: exactly JC row steps per wave, fully unrolled (rowsPerWg = STEP * JC).
+// JC == 0: a runtime number of steps, at most 64 per lane group (rowsPerWg <=
+// STEP * 64), in a loop unrolled by ER_CU_UNROLL.  Either way every step is
+// loaded and computed (steps past the workgroup's rows re-read its last row
+// and are not stored), and the row sums are parked in lanes - step i's sum in
+// lane i % LPR of res[i / LPR] - and stored after the last step, so only
+// weight loads are outstanding while rows are computed and each wait covers
+// exactly the loads it needs.
 template <class F, int LPR, int NS, int PD, int JC>
 ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
-                    uint32_t M, uint32_t K) {
+                    uint32_t M, uint32_t K, uint32_t rowsPerWg) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     __shared__ uint32_t staged;  // staging waves done
     constexpr uint32_t G = 64u / LPR;
     constexpr uint32_t STEP = ER_CU_WAVES * G;  // rows per workgroup step
-    constexpr uint32_t ROWS = STEP * JC;        // rows per workgroup
+    constexpr int NPARK = JC > 0 ? (JC + LPR - 1) / LPR : 64 / LPR;
+    constexpr int UNR = JC > 0 ? JC : ER_CU_UNROLL;
+    static_assert(UNR % PD == 0 || JC > 0, "the rolled loop's unroll is a multiple of PD");
     x += (size_t)blockIdx.y * K;
     y += (size_t)blockIdx.y * M;
-    // wave index as a scalar: the staging branch is wave-uniform
+    // wave index as a scalar: the staging branch and the step count are wave-uniform
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t g = lane / LPR, li = lane % LPR;
     const uint32_t S = K >> 6, C16 = K >> 4;
-    const uint32_t rb = blockIdx.x * ROWS, re = min(rb + ROWS, M);  // rb < M (grid = ceil(M / ROWS))
+    const uint32_t rb = blockIdx.x * rowsPerWg, re = min(rb + rowsPerWg, M);  // rb < M (grid = ceil(M / rowsPerWg))
     const uint32_t first = rb + wave * G + g;  // row of step 0; step i adds i * STEP
+    const uint32_t firstW = rb + wave * G;     // the wave's first lane group
+    // steps with a live row for this wave, and the steps computed
+    const uint32_t J = firstW < re ? (re - firstW + STEP - 1u) / STEP : 0u;
+    const uint32_t JR = JC > 0 ? (uint32_t)JC : max((J + UNR - 1u) / UNR * UNR, (uint32_t)UNR);
     const size_t rowBytes = F::row_bytes(K);
     uint32_t *xraw = lds + xl_lds_bytes(K) / 4u;  // 16-byte aligned for K % 256 == 0
 
-    // Every step is loaded and computed (steps past the workgroup's rows
-    // re-read its last row and are not stored), so the loads form one
-    // straight-line sequence and each wait covers exactly the loads it needs.
     typename F::Wt wb[PD][NS];
-    auto issue = [&](int i) {
-        const uint32_t row = min(first + (uint32_t)i * STEP, re - 1u);
+    auto issue = [&](uint32_t i, int b) {
+        const uint32_t row = min(first + i * STEP, re - 1u);
         const uint8_t *rp = W + (size_t)row * rowBytes;
 #pragma unroll
-        for (int j = 0; j < NS; ++j) wb[i % PD][j] = F::load(rp, min(li + (uint32_t)LPR * j, S - 1u));
+        for (int j = 0; j < NS; ++j) wb[b][j] = F::load(rp, min(li + (uint32_t)LPR * j, S - 1u));
     };
 
     const uint32_t nPieces = K >> 8;               // 1 KB pieces of x
@@ -907,13 +920,13 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
         __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's limb stores have landed
         if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 #pragma unroll
-        for (int i = 0; i < PD && i < JC; ++i) issue(i);
+        for (int i = 0; i < PD && i < UNR; ++i) issue((uint32_t)i, i);
     } else {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < PD && i < JC; ++i) issue(i);
+        for (int i = 0; i < PD && i < UNR; ++i) issue((uint32_t)i, i);
     }
     __builtin_amdgcn_sched_barrier(0);
     // the staging waves always finish; the bound only keeps a wave from
@@ -928,14 +941,17 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     const uint32_t M0F = vreg_const(0x0f0f0f0fu);
     typename F::Xs xs0;
     if constexpr (NS == 1) xs0 = F::xside(X, min(li, S - 1u), li < S ? 1.0f : 0.0f);
-    float acc[JC];
+    float res[NPARK];
 #pragma unroll
-    for (int i = 0; i < JC; ++i) {
-        acc[i] = 0.0f;
+    for (int q = 0; q < NPARK; ++q) res[q] = 0.0f;
+    // step i (buffer u % PD): dot products, the refill of the buffer with step
+    // i + PD when `prefetch`, the lane reduction, and the parking of the sum
+    auto step = [&](uint32_t i, int u, bool prefetch) {
+        float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
             if constexpr (NS == 1) {
-                acc[i] = F::dot(wb[i % PD][0], xs0, acc[i], M0F);
+                acc = F::dot(wb[u % PD][0], xs0, acc, M0F);
             } else {
                 // re-read per row: the opaque slot index keeps the compiler from
                 // hoisting NS slots of x limbs out of the row loop into registers
@@ -943,22 +959,33 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
                 uint32_t sx = min(sRaw, S - 1u);
                 asm volatile("" : "+v"(sx));
                 const typename F::Xs xs = F::xside(X, sx, sRaw < S ? 1.0f : 0.0f);
-                acc[i] = F::dot(wb[i % PD][j], xs, acc[i], M0F);
+                acc = F::dot(wb[u % PD][j], xs, acc, M0F);
                 __builtin_amdgcn_sched_barrier(0);  // one slot of x limbs live at a time
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (i + PD < JC) issue(i + PD);
+        if (prefetch) issue(i + PD, u % PD);
         __builtin_amdgcn_sched_barrier(0);
+        acc = group_sum<LPR>(acc);
+        const bool mine = li == i % LPR;
+        const uint32_t q0 = i / LPR;
+#pragma unroll
+        for (int q = 0; q < NPARK; ++q) res[q] = (mine && q0 == (uint32_t)q) ? acc : res[q];
+    };
+    uint32_t i0 = 0;
+    if constexpr (JC == 0) {
+        for (; i0 + UNR < JR; i0 += UNR) {
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) step(i0 + (uint32_t)u, u, true);
+        }
     }
 #pragma unroll
-    for (int i = 0; i < JC; ++i) acc[i] = group_sum<LPR>(acc[i]);
-    if (li == 0) {
+    for (int u = 0; u < UNR; ++u) step(i0 + (uint32_t)u, u, u + PD < UNR);
 #pragma unroll
-        for (int i = 0; i < JC; ++i) {
-            const uint32_t row = first + (uint32_t)i * STEP;
-            if (row < re) y[row] = acc[i];
-        }
+    for (int q = 0; q < NPARK; ++q) {
+        const uint32_t st = (uint32_t)q * LPR + li;
+        const uint32_t row = first + st * STEP;
+        if (st < J && row < re) y[row] = res[q];
     }
 }
 
@@ -1330,20 +1357,21 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
     }
 ER_I8_CONFIGS(ER_I8_ENTRY)
 
-// CU-resident family: er_gemv_<fmt>_cu_l<LPR>_n<NS>_j<JC>, JC row steps per
-// wave, grid (ceil(M / (ER_CU_WAVES * 64 / LPR * JC)), batch).
-#define ER_CU_PD(NS) 2  // rows of weight loads in flight per wave (2 measured best for 1 and 2 slots)
-#define ER_CU_ENTRY_J(fmt, F, LPR, NS, JC)                                                     \
+// CU-resident family: er_gemv_<fmt>_cu_l<LPR>_n<NS>_j<JC> (JC row steps per
+// wave, unrolled) and _jr (rolled, up to 64 steps per lane group); grid
+// (ceil(M / rowsPerWg), batch), rowsPerWg = ER_CU_WAVES * 64 / LPR * steps.
+#define ER_CU_ENTRY_J(fmt, F, LPR, NS, JC, tag)                                                 \
     extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                           \
-        er_gemv_##fmt##_cu_l##LPR##_n##NS##_j##JC(const uint8_t *__restrict__ W,               \
-                                                  const float *__restrict__ x,                \
-                                                  float *__restrict__ y, uint32_t M, uint32_t K) { \
-        gemv_cu<F, LPR, NS, ER_CU_PD(NS), JC>(W, x, y, M, K);                                  \
+        er_gemv_##fmt##_cu_l##LPR##_n##NS##_j##tag(const uint8_t *__restrict__ W,              \
+                                                   const float *__restrict__ x,               \
+                                                   float *__restrict__ y, uint32_t M, uint32_t K, \
+                                                   uint32_t rowsPerWg) {                      \
+        gemv_cu<F, LPR, NS, ER_CU_PD, JC>(W, x, y, M, K, rowsPerWg);                          \
     }
-#define ER_CU_ENTRIES(fmt, F, LPR, NS)                                                               \
-    ER_CU_ENTRY_J(fmt, F, LPR, NS, 1) ER_CU_ENTRY_J(fmt, F, LPR, NS, 2) ER_CU_ENTRY_J(fmt, F, LPR, NS, 3) \
-    ER_CU_ENTRY_J(fmt, F, LPR, NS, 4) ER_CU_ENTRY_J(fmt, F, LPR, NS, 5) ER_CU_ENTRY_J(fmt, F, LPR, NS, 6) \
-    ER_CU_ENTRY_J(fmt, F, LPR, NS, 7) ER_CU_ENTRY_J(fmt, F, LPR, NS, 8)
+#define ER_CU_ENTRIES(fmt, F, LPR, NS)                                                                     \
+    ER_CU_ENTRY_J(fmt, F, LPR, NS, 1, 1) ER_CU_ENTRY_J(fmt, F, LPR, NS, 2, 2) ER_CU_ENTRY_J(fmt, F, LPR, NS, 3, 3) \
+    ER_CU_ENTRY_J(fmt, F, LPR, NS, 4, 4) ER_CU_ENTRY_J(fmt, F, LPR, NS, 5, 5) ER_CU_ENTRY_J(fmt, F, LPR, NS, 6, 6) \
+    ER_CU_ENTRY_J(fmt, F, LPR, NS, 7, 7) ER_CU_ENTRY_J(fmt, F, LPR, NS, 8, 8) ER_CU_ENTRY_J(fmt, F, LPR, NS, 0, r)
 #define ER_CU_ENTRY_Q4K(LPR, NS) ER_CU_ENTRIES(q4k, CuQ4K, LPR, NS)
 #define ER_CU_ENTRY_Q8(LPR, NS) ER_CU_ENTRIES(q8_0, CuQ8, LPR, NS)
 ER_CU_CONFIGS_Q4K(ER_CU_ENTRY_Q4K)

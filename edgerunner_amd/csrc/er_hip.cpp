@@ -159,8 +159,8 @@ struct er_hip_ctx {
     hipFunction_t fnQ8I8[kI8Count] = {};
     hipFunction_t fnQ6KI8[kI8Count] = {};
     hipFunction_t fnQ6KTop1[kI8Count] = {};
-    hipFunction_t fnQ4KCu[kCuCountQ4K][ER_CU_MAX_STEPS] = {};
-    hipFunction_t fnQ8Cu[kCuCountQ8][ER_CU_MAX_STEPS] = {};
+    hipFunction_t fnQ4KCu[kCuCountQ4K][ER_CU_MAX_STEPS + 1] = {};  // [steps - 1]; [ER_CU_MAX_STEPS]: rolled
+    hipFunction_t fnQ8Cu[kCuCountQ8][ER_CU_MAX_STEPS + 1] = {};
     hipFunction_t fnQ4KMulti[kI8MultiCount] = {};
     hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
     hipFunction_t fnQ8Multi[kI8MultiCount] = {};
@@ -386,9 +386,10 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     void *args[] = {&W.data, &x.data, &y.data, &M, &K};
     const bool q8Aligned = f == Fmt::Q8_0 && K % 64u == 0;
     // CU-resident family: Q4_K / Q8_0 rows of K % 256 == 0 up to kCuMaxK, when
-    // a CU's share of the rows is 2..2*ER_CU_MAX_STEPS row steps per token:
-    // below that the lane-group family, with more workgroups, is faster; above
-    // it the capped step count needs several workgroup rounds
+    // a CU's share of the rows is 3..ER_CU_MAX_STEPS row steps per token:
+    // below that the lane-group family, with more workgroups, is as fast or
+    // faster, and above it the rolled kernel measured no faster than it (the
+    // rolled kernels run when ER_HIP_GEMV_CU=1 forces the family)
     const bool cuFits = f != Fmt::Q6_K && K % 256u == 0 && K <= kCuMaxK && ctx->gemv_fp32 == 0 &&
                         ctx->i8_override < 0 && ctx->cu_mode != 0 &&
                         (uint64_t)cu_lds_bytes(K) + 1024u <= ctx->info.lds_per_workgroup;
@@ -403,16 +404,19 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
         // outputs); the batch only changes the row partition.
         const uint32_t cu = (uint32_t)ctx->cu_count;
         const uint32_t needed1 = ((M + cu - 1u) / cu + step - 1u) / step;  // steps per CU, one token
-        if (ctx->cu_mode == 1 || (needed1 >= 2u && needed1 <= 2u * ER_CU_MAX_STEPS)) {
-            // about one workgroup per CU over all tokens, at most ER_CU_MAX_STEPS steps each
+        if (ctx->cu_mode == 1 || (needed1 >= 3u && needed1 <= ER_CU_MAX_STEPS)) {
+            // about one workgroup per CU over all tokens; unrolled kernels up
+            // to ER_CU_MAX_STEPS steps, the rolled one up to ER_CU_MAX_ROLLED
             const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
-            const uint32_t steps =
-                std::min<uint32_t>(ER_CU_MAX_STEPS, ((M + perToken - 1u) / perToken + step - 1u) / step);
+            const uint32_t steps = std::min<uint32_t>(
+                ER_CU_MAX_ROLLED, ((M + perToken - 1u) / perToken + step - 1u) / step);
             const uint32_t rowsPerWg = step * steps;
+            const int slot = steps <= ER_CU_MAX_STEPS ? (int)steps - 1 : ER_CU_MAX_STEPS;
             dim3 grid((M + rowsPerWg - 1u) / rowsPerWg, batch, 1);
-            return launch_fn(f == Fmt::Q4_K ? ctx->fnQ4KCu[cuCi][steps - 1] : ctx->fnQ8Cu[cuCi][steps - 1],
+            void *cargs[] = {&W.data, &x.data, &y.data, &M, &K, (void *)&rowsPerWg};
+            return launch_fn(f == Fmt::Q4_K ? ctx->fnQ4KCu[cuCi][slot] : ctx->fnQ8Cu[cuCi][slot],
                              f == Fmt::Q4_K ? "er_gemv_q4k_cu" : "er_gemv_q8_0_cu", grid,
-                             dim3(64u * ER_CU_WAVES, 1, 1), cu_lds_bytes(K), stream, args);
+                             dim3(64u * ER_CU_WAVES, 1, 1), cu_lds_bytes(K), stream, cargs);
         }
     }
     if ((f != Fmt::Q8_0 || q8Aligned) && K <= kI8MaxK && ctx->gemv_fp32 == 0) {
@@ -891,10 +895,14 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
         const CuCfg *cfg = fmt == 0 ? kCuCfgQ4K : kCuCfgQ8;
         const int count = fmt == 0 ? kCuCountQ4K : kCuCountQ8;
         for (int i = 0; i < count; ++i)
-            for (int jc = 1; jc <= ER_CU_MAX_STEPS; ++jc) {
-                char name[64];
-                std::snprintf(name, sizeof(name), "er_gemv_%s_cu_l%u_n%u_j%d", fmt == 0 ? "q4k" : "q8_0",
-                              (unsigned)cfg[i].lpr, (unsigned)cfg[i].ns, jc);
+            for (int jc = 1; jc <= ER_CU_MAX_STEPS + 1; ++jc) {
+                char name[64], tag[8];
+                if (jc <= ER_CU_MAX_STEPS)
+                    std::snprintf(tag, sizeof(tag), "%d", jc);
+                else
+                    std::snprintf(tag, sizeof(tag), "r");
+                std::snprintf(name, sizeof(name), "er_gemv_%s_cu_l%u_n%u_j%s", fmt == 0 ? "q4k" : "q8_0",
+                              (unsigned)cfg[i].lpr, (unsigned)cfg[i].ns, tag);
                 hipFunction_t *slot = fmt == 0 ? &ctx->fnQ4KCu[i][jc - 1] : &ctx->fnQ8Cu[i][jc - 1];
                 e = hipModuleGetFunction(slot, ctx->module, name);
                 if (e != hipSuccess) {

@@ -50,6 +50,10 @@ def cu_gemv():
 # (24 slots); Q4_K 5120 -> 64x2, 8192 -> 64x2
 SHAPES = [(1, 256), (7, 1024), (100, 2048), (333, 3072), (1000, 4096), (64, 5120), (250, 1536),
           (513, 8192), (14336, 4096)]
+# more than 8 row steps per CU (rolled kernel): 28672 x 4096 (14 steps),
+# 151936 x 1024 (19 steps of 32 rows), 140000 x 256 (capped at 64 steps, more
+# workgroups than CUs)
+ROLLED = [(28672, 4096), (151936, 1024), (140000, 256)]
 
 
 @pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
@@ -57,6 +61,16 @@ SHAPES = [(1, 256), (7, 1024), (100, 2048), (333, 3072), (1000, 4096), (64, 5120
 def test_cu_family_matches_oracle(cu_gemv, fmt, M, K):
     W = synth.weights(fmt, synth.seed(80, M % 97), M, K, **DSCALE[fmt])
     x = synth.normal_f32(synth.seed(80, 200 + K % 89), K)
+    y = getattr(cu_gemv, EXEC[fmt])(W, x, M, K)
+    exp = ref.gemv(fmt, W, x, M, K, threads=ref.max_threads())
+    assert rel_l2(y, exp) < TOL
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("M,K", ROLLED)
+def test_cu_family_rolled_matches_oracle(cu_gemv, fmt, M, K):
+    W = synth.weights(fmt, synth.seed(85, M % 97), M, K, **DSCALE[fmt])
+    x = synth.normal_f32(synth.seed(85, 200 + K % 89), K)
     y = getattr(cu_gemv, EXEC[fmt])(W, x, M, K)
     exp = ref.gemv(fmt, W, x, M, K, threads=ref.max_threads())
     assert rel_l2(y, exp) < TOL
@@ -113,7 +127,7 @@ def test_cu_family_equals_lane_matched_family1(cu_gemv, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
-@pytest.mark.parametrize("M,K,T", [(8192, 2048, 3), (16384, 1024, 2), (4096, 4096, 4)])
+@pytest.mark.parametrize("M,K,T", [(12288, 2048, 3), (24576, 1024, 2), (6144, 4096, 4)])
 def test_default_dispatch_batched_equals_per_token(gemv, fmt, M, K, T):
     """Default dispatch on shapes the CU-resident family takes: the family is
     chosen from M and K alone, so batched and per-token calls agree bit for
