@@ -798,7 +798,9 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 #endif
 #define ER_CU_SPIN_LIMIT (1u << 22)   // bound on the staging-counter wait (s_sleep 1 per poll)
 #define ER_CU_PD 2                    // rows of weight loads in flight per wave (2 measured best)
+#ifndef ER_CU_UNROLL
 #define ER_CU_UNROLL 4                // unroll of the rolled step loop
+#endif
 
 // Per-format slot access: weights of one slot (Wt), the x side of one slot
 // (Xs), and the slot's contribution.
@@ -1368,12 +1370,14 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
                                                    uint32_t rowsPerWg) {                      \
         gemv_cu<F, LPR, NS, ER_CU_PD, JC>(W, x, y, M, K, rowsPerWg);                          \
     }
-#define ER_CU_ENTRIES(fmt, F, LPR, NS)                                                                     \
-    ER_CU_ENTRY_J(fmt, F, LPR, NS, 1, 1) ER_CU_ENTRY_J(fmt, F, LPR, NS, 2, 2) ER_CU_ENTRY_J(fmt, F, LPR, NS, 3, 3) \
-    ER_CU_ENTRY_J(fmt, F, LPR, NS, 4, 4) ER_CU_ENTRY_J(fmt, F, LPR, NS, 5, 5) ER_CU_ENTRY_J(fmt, F, LPR, NS, 6, 6) \
+#define ER_CU_STEPS_1(fmt, F, LPR, NS) ER_CU_ENTRY_J(fmt, F, LPR, NS, 1, 1)
+#define ER_CU_STEPS_2(fmt, F, LPR, NS) ER_CU_STEPS_1(fmt, F, LPR, NS) ER_CU_ENTRY_J(fmt, F, LPR, NS, 2, 2)
+#define ER_CU_STEPS_8(fmt, F, LPR, NS)                                                                       \
+    ER_CU_STEPS_2(fmt, F, LPR, NS) ER_CU_ENTRY_J(fmt, F, LPR, NS, 3, 3) ER_CU_ENTRY_J(fmt, F, LPR, NS, 4, 4)  \
+    ER_CU_ENTRY_J(fmt, F, LPR, NS, 5, 5) ER_CU_ENTRY_J(fmt, F, LPR, NS, 6, 6)                                \
     ER_CU_ENTRY_J(fmt, F, LPR, NS, 7, 7) ER_CU_ENTRY_J(fmt, F, LPR, NS, 8, 8) ER_CU_ENTRY_J(fmt, F, LPR, NS, 0, r)
-#define ER_CU_ENTRY_Q4K(LPR, NS) ER_CU_ENTRIES(q4k, CuQ4K, LPR, NS)
-#define ER_CU_ENTRY_Q8(LPR, NS) ER_CU_ENTRIES(q8_0, CuQ8, LPR, NS)
+#define ER_CU_ENTRY_Q4K(LPR, NS, MAXJ) ER_CU_STEPS_##MAXJ(q4k, CuQ4K, LPR, NS)
+#define ER_CU_ENTRY_Q8(LPR, NS, MAXJ) ER_CU_STEPS_##MAXJ(q8_0, CuQ8, LPR, NS)
 ER_CU_CONFIGS_Q4K(ER_CU_ENTRY_Q4K)
 ER_CU_CONFIGS_Q8(ER_CU_ENTRY_Q8)
 

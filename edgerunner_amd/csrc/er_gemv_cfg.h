@@ -28,15 +28,16 @@
     ER_I8_MULTI_CONFIGS_L(X, 64) ER_I8_MULTI_CONFIGS_L(X, 32) ER_I8_MULTI_CONFIGS_L(X, 16) \
     ER_I8_MULTI_CONFIGS_L(X, 4)
 
-// CU-resident Q4_K / Q8_0 kernels (family 3): X(LPR, NS), one 8-wave workgroup
-// per CU-sized share of the rows, unrolled kernels for 1..ER_CU_MAX_STEPS row
-// steps per wave and a rolled one for up to ER_CU_MAX_ROLLED.  Q4_K: NS <= 2 (rows up to 8192 weights); Q8_0: NS = 1 (up to 4096).
-// Beyond that the unrolled steps keep too many slots of x limbs live and the
-// kernels spill.
+// CU-resident Q4_K / Q8_0 kernels (family 3): X(LPR, NS, MAXJ), one 8-wave
+// workgroup per CU-sized share of the rows, unrolled kernels for 1..MAXJ row
+// steps per wave, and for MAXJ == 8 a rolled one for up to ER_CU_MAX_ROLLED.
+// With more slots per lane than MAXJ allows, the unrolled steps keep too many
+// slots of x limbs or weights live and the kernels spill.
 #ifndef ER_CU_WAVES
 #define ER_CU_WAVES 8
 #endif
 #define ER_CU_MAX_STEPS 8
 #define ER_CU_MAX_ROLLED 64  // steps per lane group: one parked sum per lane per register
-#define ER_CU_CONFIGS_Q4K(X) X(16, 1) X(16, 2) X(32, 1) X(32, 2) X(64, 1) X(64, 2)
-#define ER_CU_CONFIGS_Q8(X) X(16, 1) X(32, 1) X(64, 1)
+#define ER_CU_CONFIGS_Q4K(X) \
+    X(16, 1, 8) X(16, 2, 8) X(32, 1, 8) X(32, 2, 8) X(64, 1, 8) X(64, 2, 8) X(64, 3, 2) X(64, 4, 2) X(32, 7, 1)
+#define ER_CU_CONFIGS_Q8(X) X(16, 1, 8) X(32, 1, 8) X(64, 1, 8)

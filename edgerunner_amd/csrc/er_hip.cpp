@@ -109,20 +109,21 @@ constexpr int kI8Count = (int)(sizeof(kI8Cfg) / sizeof(kI8Cfg[0]));
 // length use them (the default dynamic LDS limit is 64 KiB).
 constexpr uint32_t kI8MaxK = 16384;
 
-// CU-resident Q4_K / Q8_0 configurations {LPR, NS} (er_gemv_cfg.h).
+// CU-resident Q4_K / Q8_0 configurations {LPR, NS, MAXJ} (er_gemv_cfg.h): kernels
+// for 1..maxJ unrolled steps, and a rolled one when maxJ == ER_CU_MAX_STEPS.
 struct CuCfg {
-    uint8_t lpr, ns;
+    uint8_t lpr, ns, maxJ;
 };
-#define ER_CU_ROW(LPR, NS) {LPR, NS},
+#define ER_CU_ROW(LPR, NS, MAXJ) {LPR, NS, MAXJ},
 constexpr CuCfg kCuCfgQ4K[] = {ER_CU_CONFIGS_Q4K(ER_CU_ROW)};
 constexpr CuCfg kCuCfgQ8[] = {ER_CU_CONFIGS_Q8(ER_CU_ROW)};
 #undef ER_CU_ROW
 constexpr int kCuCountQ4K = (int)(sizeof(kCuCfgQ4K) / sizeof(kCuCfgQ4K[0]));
 constexpr int kCuCountQ8 = (int)(sizeof(kCuCfgQ8) / sizeof(kCuCfgQ8[0]));
-// The CU-resident family covers Q4_K rows of up to 128 slots and Q8_0 rows of
+// The CU-resident family covers Q4_K rows of up to 256 slots and Q8_0 rows of
 // up to 64 (pick_cu finds no configuration beyond), and holds limbs plus raw x
 // in LDS: 3K + K/4 + K/16 + 4K bytes.
-constexpr uint32_t kCuMaxK = 8192;
+constexpr uint32_t kCuMaxK = 16384;
 constexpr uint32_t cu_lds_bytes(uint32_t K) { return 3u * K + K / 16u * 4u + K / 64u * 4u + 4u * K; }
 
 // Multi-matrix / GeGLU Q4_K configurations {LPR, NS, R} (er_gemv_cfg.h).
@@ -385,11 +386,13 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
 
     void *args[] = {&W.data, &x.data, &y.data, &M, &K};
     const bool q8Aligned = f == Fmt::Q8_0 && K % 64u == 0;
-    // CU-resident family: Q4_K / Q8_0 rows of K % 256 == 0 up to kCuMaxK, when
-    // a CU's share of the rows is 3..ER_CU_MAX_STEPS row steps per token:
-    // below that the lane-group family, with more workgroups, is as fast or
-    // faster, and above it the rolled kernel measured no faster than it (the
-    // rolled kernels run when ER_HIP_GEMV_CU=1 forces the family)
+    // CU-resident family: Q4_K / Q8_0 rows of K % 256 == 0 up to kCuMaxK, when a
+    // CU's share of one token's rows is 3..ER_CU_MAX_STEPS row steps, or any
+    // share up to the configuration's unrolled steps for rows longer than 8192
+    // weights (whose per-workgroup x staging the lane-group family repeats
+    // ~512 times).  Below 3 steps of short rows the lane-group family, with
+    // more workgroups, is as fast; above 8 the rolled loop measured no faster
+    // than it (the rolled kernels run when ER_HIP_GEMV_CU=1 forces the family).
     const bool cuFits = f != Fmt::Q6_K && K % 256u == 0 && K <= kCuMaxK && ctx->gemv_fp32 == 0 &&
                         ctx->i8_override < 0 && ctx->cu_mode != 0 &&
                         (uint64_t)cu_lds_bytes(K) + 1024u <= ctx->info.lds_per_workgroup;
@@ -404,12 +407,16 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
         // outputs); the batch only changes the row partition.
         const uint32_t cu = (uint32_t)ctx->cu_count;
         const uint32_t needed1 = ((M + cu - 1u) / cu + step - 1u) / step;  // steps per CU, one token
-        if (ctx->cu_mode == 1 || (needed1 >= 3u && needed1 <= ER_CU_MAX_STEPS)) {
-            // about one workgroup per CU over all tokens; unrolled kernels up
-            // to ER_CU_MAX_STEPS steps, the rolled one up to ER_CU_MAX_ROLLED
+        const bool rolled = c.maxJ == ER_CU_MAX_STEPS;
+        const bool use = ctx->cu_mode == 1 ? (rolled || needed1 <= c.maxJ)
+                                           : (needed1 <= c.maxJ && (needed1 >= 3u || K > 8192u));
+        if (use) {
+            // about one workgroup per CU over all tokens: unrolled kernels up to
+            // maxJ steps, the rolled one up to ER_CU_MAX_ROLLED, more workgroups beyond
             const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
-            const uint32_t steps = std::min<uint32_t>(
-                ER_CU_MAX_ROLLED, ((M + perToken - 1u) / perToken + step - 1u) / step);
+            const uint32_t maxSteps = rolled ? ER_CU_MAX_ROLLED : c.maxJ;
+            const uint32_t steps =
+                std::min<uint32_t>(maxSteps, ((M + perToken - 1u) / perToken + step - 1u) / step);
             const uint32_t rowsPerWg = step * steps;
             const int slot = steps <= ER_CU_MAX_STEPS ? (int)steps - 1 : ER_CU_MAX_STEPS;
             dim3 grid((M + rowsPerWg - 1u) / rowsPerWg, batch, 1);
@@ -896,6 +903,9 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
         const int count = fmt == 0 ? kCuCountQ4K : kCuCountQ8;
         for (int i = 0; i < count; ++i)
             for (int jc = 1; jc <= ER_CU_MAX_STEPS + 1; ++jc) {
+                // kernels exist for steps 1..maxJ, and the rolled one (slot
+                // ER_CU_MAX_STEPS) when maxJ == ER_CU_MAX_STEPS
+                if (jc <= ER_CU_MAX_STEPS ? jc > cfg[i].maxJ : cfg[i].maxJ != ER_CU_MAX_STEPS) continue;
                 char name[64], tag[8];
                 if (jc <= ER_CU_MAX_STEPS)
                     std::snprintf(tag, sizeof(tag), "%d", jc);

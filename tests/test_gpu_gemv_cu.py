@@ -1,4 +1,4 @@
-"""CU-resident GEMV family (K % 256 == 0; Q4_K rows up to 8192 weights, Q8_0
+"""CU-resident GEMV family (K % 256 == 0; Q4_K rows up to 16384 weights, Q8_0
 rows up to 4096, longer Q8_0 rows fall back to the lane-group family):
 the GEMV parity bar of the other kernels (relative L2 <= 1e-3 against the CPU
 oracle, the reference test's absolute 1e-4 on its case, exact one-hot
@@ -47,9 +47,10 @@ def cu_gemv():
 
 # K -> configuration picked (lanes per row x slots per lane): 256 -> 16x1,
 # 1024 -> 16x1, 2048 -> 32x1, 3072 -> 64x1, 4096 -> 64x1, 1536 -> 32x1
-# (24 slots); Q4_K 5120 -> 64x2, 8192 -> 64x2
+# (24 slots); Q4_K 5120 -> 64x2, 8192 -> 64x2, 12288 -> 64x3, 14336 -> 32x7,
+# 16384 -> 64x4 (one or two row steps per CU)
 SHAPES = [(1, 256), (7, 1024), (100, 2048), (333, 3072), (1000, 4096), (64, 5120), (250, 1536),
-          (513, 8192), (14336, 4096)]
+          (513, 8192), (14336, 4096), (64, 12288), (100, 14336), (4096, 14336), (2048, 16384)]
 # more than 8 row steps per CU (rolled kernel): 28672 x 4096 (14 steps),
 # 151936 x 1024 (19 steps of 32 rows), 140000 x 256 (capped at 64 steps, more
 # workgroups than CUs)
