@@ -66,6 +66,33 @@ ER_DEV void load_w(const uint8_t *__restrict__ W, size_t rowBytes, uint32_t row,
     }
 }
 
+// Loads at a uniform base plus a 32-bit per-lane byte offset: the compiler
+// forms them as SGPR-base + VGPR-offset loads, so the per-chunk address update
+// is scalar instead of 64-bit vector arithmetic per load.
+ER_DEV u32x4 ld16_off(const void *base, uint32_t off) { return *(const u32x4 *)((const uint8_t *)base + off); }
+ER_DEV u32x4 ld16_off_a4(const void *base, uint32_t off) {
+    const u32x4_a4 v = *(const u32x4_a4 *)((const uint8_t *)base + off);
+    return u32x4{v.x, v.y, v.z, v.w};
+}
+ER_DEV uint32_t ld4_off(const void *base, uint32_t off) { return *(const uint32_t *)((const uint8_t *)base + off); }
+
+// load_w with the row's byte offset from W precomputed (rowOff < 2^32, checked
+// by the host): the chunk's part of the offset is wave-uniform.
+template <bool Q4K>
+ER_DEV void load_w_off(const uint8_t *__restrict__ W, uint32_t rowOff, uint32_t chunk, uint32_t h, WRaw &r) {
+    if (Q4K) {
+        const uint32_t bp = rowOff + (chunk >> 2) * 144u;
+        r.a = ld16_off(W, bp);
+        r.b = ld16_off(W, bp + 16u + 32u * (chunk & 3u) + 16u * h);
+        r.c = 0;
+    } else {
+        const uint32_t wp = rowOff + chunk * 68u + 32u * h;
+        r.a = ld16_off_a4(W, wp);
+        r.b = ld16_off_a4(W, wp + 16u);
+        r.c = ld4_off(W, wp + 32u);
+    }
+}
+
 // Dequantises a thread's 32 weights into 16 packed bf16 pairs: out[0..7] are
 // chunk positions [16h, 16h+16), out[8..15] positions [32 + 16h, 32 + 16h + 16)
 // for Q4_K; for Q8_0 out[0..15] are positions [32h, 32h + 32).
@@ -249,13 +276,17 @@ ER_DEV void gemm_q_pipe(const uint8_t *__restrict__ W, const uint16_t *__restric
     const uint32_t cBeg = (uint32_t)(((uint64_t)NCall * ks0) / SK);
     const uint32_t NC = (uint32_t)(((uint64_t)NCall * (ks0 + 1u)) / SK) - cBeg;
     const uint32_t wRow = min(n0 + (tid >> 1), N - 1u), wh = tid & 1u;
+    const uint32_t wRowOff = wRow * (uint32_t)rowBytes;  // < 2^32 (host check)
+    // byte offsets of this thread's X pieces in chunk 0 (< 2^32, host check)
+    uint32_t xOff[XLOADS];
+#pragma unroll
+    for (int q = 0; q < XLOADS; ++q) {
+        const uint32_t p = tid + 256u * q;
+        xOff[q] = (min(t0 + (p >> 3), T - 1u) * K + 8u * (p & 7u)) * 2u;
+    }
     auto load_x = [&](uint32_t chunk, u32x4 (&xr)[XLOADS]) {
 #pragma unroll
-        for (int q = 0; q < XLOADS; ++q) {
-            const uint32_t p = tid + 256u * q;
-            const uint32_t row = min(t0 + (p >> 3), T - 1u);
-            xr[q] = *(const u32x4 *)(X + (size_t)row * K + chunk * ER_GEMM_KC + 8u * (p & 7u));
-        }
+        for (int q = 0; q < XLOADS; ++q) xr[q] = ld16_off(X, xOff[q] + chunk * (ER_GEMM_KC * 2u));
     };
     auto store_stage = [&](uint32_t stage, uint32_t chunk, const WRaw &wr, const u32x4 (&xr)[XLOADS]) {
         uint16_t *As = smem + stage * (ASZ + BSZ);
@@ -314,14 +345,14 @@ ER_DEV void gemm_q_pipe(const uint8_t *__restrict__ W, const uint16_t *__restric
         }
     };
     // chunk c's data sits in register buffer c % 3
-    load_w<Q4K>(W, rowBytes, wRow, cBeg, wh, wr[0]);
+    load_w_off<Q4K>(W, wRowOff, cBeg, wh, wr[0]);
     load_x(cBeg, xr[0]);
     if (NC > 1) {
-        load_w<Q4K>(W, rowBytes, wRow, cBeg + 1, wh, wr[1]);
+        load_w_off<Q4K>(W, wRowOff, cBeg + 1, wh, wr[1]);
         load_x(cBeg + 1, xr[1]);
     }
     if (NC > 2) {
-        load_w<Q4K>(W, rowBytes, wRow, cBeg + 2, wh, wr[2]);
+        load_w_off<Q4K>(W, wRowOff, cBeg + 2, wh, wr[2]);
         load_x(cBeg + 2, xr[2]);
     }
     store_stage(0, cBeg, wr[0], xr[0]);
@@ -337,7 +368,7 @@ ER_DEV void gemm_q_pipe(const uint8_t *__restrict__ W, const uint16_t *__restric
             mfma_stage(c & 1u);                                                          \
             if (c + 1 < NC) store_stage((c + 1) & 1u, cBeg + c + 1, wr[((B) + 1) % 3], xr[((B) + 1) % 3]); \
             if (c + 3 < NC) {                                                            \
-                load_w<Q4K>(W, rowBytes, wRow, cBeg + c + 3, wh, wr[(B)]);               \
+                load_w_off<Q4K>(W, wRowOff, cBeg + c + 3, wh, wr[(B)]);                  \
                 load_x(cBeg + c + 3, xr[(B)]);                                           \
             }                                                                            \
         }                                                                                \
@@ -369,6 +400,154 @@ ER_DEV void gemm_q_pipe(const uint8_t *__restrict__ W, const uint16_t *__restric
 extern "C" __global__ void __launch_bounds__(256) er_fill_zero(float4 *__restrict__ p, uint64_t n4) {
     for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n4; i += (uint64_t)gridDim.x * 256u)
         p[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+// ---------------------------------------------------------------------------
+// Warp-specialised variant (512 threads, TT = 128): waves 0-3 run the MFMAs of
+// chunk c from LDS stage c % 2 while waves 4-7 dequantise chunk c+1 into the
+// other stage; one barrier per chunk for all 8 waves.  The staging waves keep
+// 4 chunks of raw weights and X in registers and load unconditionally (chunk
+// indices past the split are clamped re-loads), so every vmcnt wait covers
+// exactly one chunk.  Requires the split's chunk count NC % 4 == 0 (host);
+// a workgroup whose split breaks that returns before any barrier.
+// ---------------------------------------------------------------------------
+template <bool Q4K>
+ER_DEV void gemm_q_ws(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
+                      uint32_t T, uint32_t N, uint32_t K, uint32_t SK) {
+    constexpr int TT = 128, WT = TT / 2, AI = WT / 32, NST = 2, NB = 4;
+    constexpr int XLOADS = TT * ER_GEMM_KC * 2 / 16 / 256;
+    constexpr int ASZ = TT * ER_GEMM_PITCH, BSZ = ER_GEMM_TN * ER_GEMM_PITCH;
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];  // NST x (A stage + B stage)
+    const uint32_t nT = (T + TT - 1) / TT, nN = (N + ER_GEMM_TN - 1) / ER_GEMM_TN;
+    const uint32_t total = nT * nN * SK, per = (total + 7u) / 8u;
+    const uint32_t L = blockIdx.x;
+    const uint32_t item = (L % 8u) * per + L / 8u;  // (N tile, K split, token tile), token tile fastest
+    if (item >= total) return;
+    const uint32_t tt = item % nT, rest = item / nT;
+    const uint32_t ks0 = rest % SK, nt = rest / SK;
+    const uint32_t n0 = nt * ER_GEMM_TN, t0 = tt * TT;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t NCall = K / ER_GEMM_KC;
+    const uint32_t cBeg = (uint32_t)(((uint64_t)NCall * ks0) / SK);
+    const uint32_t NC = (uint32_t)(((uint64_t)NCall * (ks0 + 1u)) / SK) - cBeg;
+    if (NC == 0 || NC % NB != 0) return;  // never launched so (host); keeps the barrier counts equal
+    const uint32_t rowBytes = Q4K ? (K >> 8) * 144u : (K >> 6) * 68u;
+
+    if (wave >= 4) {
+        // staging waves: thread d owns weight row n0 + d/2 (half d%2) and XLOADS X pieces
+        const uint32_t d = tid - 256u;
+        const uint32_t wRowOff = min(n0 + (d >> 1), N - 1u) * rowBytes, wh = d & 1u;
+        uint32_t xOff[XLOADS];
+#pragma unroll
+        for (int q = 0; q < XLOADS; ++q) {
+            const uint32_t p = d + 256u * q;
+            xOff[q] = (min(t0 + (p >> 3), T - 1u) * K + 8u * (p & 7u)) * 2u;
+        }
+        WRaw wr[NB];
+        u32x4 xr[NB][XLOADS];
+        const uint32_t cLast = cBeg + NC - 1u;
+        auto load = [&](uint32_t chunk, int b) {
+            chunk = min(chunk, cLast);
+            load_w_off<Q4K>(W, wRowOff, chunk, wh, wr[b]);
+#pragma unroll
+            for (int q = 0; q < XLOADS; ++q) xr[b][q] = ld16_off(X, xOff[q] + chunk * (ER_GEMM_KC * 2u));
+        };
+        auto store = [&](uint32_t stage, uint32_t chunk, int b) {
+            chunk = min(chunk, cLast);
+            uint16_t *As = smem + stage * (ASZ + BSZ);
+            uint16_t *Bs = As + ASZ;
+            uint32_t wd[16];
+            dequant_w<Q4K>(wr[b], chunk, wh, wd);
+            uint16_t *brow = Bs + (d >> 1) * ER_GEMM_PITCH;
+            if (Q4K) {
+                *(u32x4 *)(brow + 16u * wh) = u32x4{wd[0], wd[1], wd[2], wd[3]};
+                *(u32x4 *)(brow + 16u * wh + 8u) = u32x4{wd[4], wd[5], wd[6], wd[7]};
+                *(u32x4 *)(brow + 32u + 16u * wh) = u32x4{wd[8], wd[9], wd[10], wd[11]};
+                *(u32x4 *)(brow + 32u + 16u * wh + 8u) = u32x4{wd[12], wd[13], wd[14], wd[15]};
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *(u32x4 *)(brow + 32u * wh + 8u * q) = u32x4{wd[4 * q], wd[4 * q + 1], wd[4 * q + 2], wd[4 * q + 3]};
+            }
+#pragma unroll
+            for (int q = 0; q < XLOADS; ++q) {
+                const uint32_t p = d + 256u * q;
+                *(u32x4 *)(As + (p >> 3) * ER_GEMM_PITCH + 8u * (p & 7u)) = xr[b][q];
+            }
+        };
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load(cBeg + (uint32_t)b, b);
+        store(0, cBeg, 0);
+        __syncthreads();  // stage 0 ready
+        // iteration c: fill stage (c+1) % NST with chunk c+1 (buffer (c+1) % NB),
+        // refill buffer c % NB with chunk c+NB, barrier
+        for (uint32_t c0 = 0; c0 < NC; c0 += NB) {
+#pragma unroll
+            for (int B = 0; B < NB; ++B) {
+                const uint32_t c = c0 + (uint32_t)B;
+                store((c + 1u) % NST, cBeg + c + 1u, (B + 1) % NB);
+                load(cBeg + c + NB, B);
+                __syncthreads();
+            }
+        }
+    } else {
+        const uint32_t wt = wave >> 1, wn = wave & 1u;
+        f32x16 acc[AI][2];
+#pragma unroll
+        for (int i = 0; i < AI; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        __syncthreads();  // stage 0 ready
+        for (uint32_t c = 0; c < NC; ++c) {
+            const uint16_t *As = smem + (c % NST) * (ASZ + BSZ);
+            const uint16_t *Bs = As + ASZ;
+#pragma unroll
+            for (int ks = 0; ks < ER_GEMM_KC / 16; ++ks) {
+                const uint32_t kof = 16u * ks + 8u * (lane >> 5);
+                bf16x8 a[AI], b[2];
+#pragma unroll
+                for (int i = 0; i < AI; ++i)
+                    a[i] = *(const bf16x8 *)(As + (wt * WT + 32u * i + (lane & 31u)) * ER_GEMM_PITCH + kof);
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    b[j] = *(const bf16x8 *)(Bs + (wn * 64u + 32u * j + (lane & 31u)) * ER_GEMM_PITCH + kof);
+#pragma unroll
+                for (int i = 0; i < AI; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int i = 0; i < AI; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t n = n0 + wn * 64u + 32u * j + (lane & 31u);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t t = t0 + wt * WT + 32u * i + 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3);
+                    if (t < T && n < N) {
+                        if (SK == 1) Y[(size_t)t * N + n] = acc[i][j][r];
+                        else atomicAdd(Y + (size_t)t * N + n, acc[i][j][r]);  // Y zero-filled by er_fill_zero
+                    }
+                }
+            }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(512)
+    er_gemmw_q4k_t128(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
+                      uint32_t T, uint32_t N, uint32_t K, uint32_t SK) {
+    gemm_q_ws<true>(W, X, Y, T, N, K, SK);
+}
+extern "C" __global__ void __launch_bounds__(512)
+    er_gemmw_q8_0_t128(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
+                       uint32_t T, uint32_t N, uint32_t K, uint32_t SK) {
+    gemm_q_ws<false>(W, X, Y, T, N, K, SK);
 }
 
 #define ER_GEMMP_ENTRY(fmt, q4k, tt)                                                             \

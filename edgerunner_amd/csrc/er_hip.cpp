@@ -75,7 +75,9 @@ using er_detail::fail;
     X(GEMMP_Q4K_T128, "er_gemmp_q4k_t128")                                             \
     X(GEMMP_Q4K_T256, "er_gemmp_q4k_t256")                                             \
     X(GEMMP_Q8_0_T128, "er_gemmp_q8_0_t128")                                           \
-    X(GEMMP_Q8_0_T256, "er_gemmp_q8_0_t256")
+    X(GEMMP_Q8_0_T256, "er_gemmp_q8_0_t256")                                           \
+    X(GEMMW_Q4K_T128, "er_gemmw_q4k_t128")                                             \
+    X(GEMMW_Q8_0_T128, "er_gemmw_q8_0_t128")
 
 enum KernelId {
 #define ER_ENUM(id, name) K_##id,
@@ -169,7 +171,7 @@ struct er_hip_ctx {
     int cu_count = 0;
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
     int cu_mode = -1;      // ER_HIP_GEMV_CU: 0 never, 1 whenever it applies, unset: by shape
-    int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1 selects the non-pipelined GEMM (benchmark comparison)
+    int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1: non-pipelined GEMM, =2: 256-thread pipelined (comparisons)
     uint32_t gemm_tt = 0, gemm_sk = 0;  // ER_HIP_GEMM_TILE=tt:sk (benchmark sweeps only)
     int gemv_fp32 = 0;  // ER_HIP_GEMV_FP32=1 selects the fp32 GEMV family (benchmark comparison)
     er_device_info info{};
@@ -574,6 +576,10 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
         return fail(ER_ERR_INVALID_ARGUMENT, "GEMM: weight and x must be 16-byte, y 4-byte aligned");
     if ((T + 127u) / 128u > 65535u)
         return fail(ER_ERR_ENCODING_FAILED, "GEMM: %u tokens exceed the grid limit", T);
+    // the pipelined kernels address W and X with 32-bit byte offsets
+    if (need >= (1ull << 32) || (uint64_t)T * K * 2u >= (1ull << 32))
+        return fail(ER_ERR_INVALID_MATRIX_SHAPE, "%s GEMM: W (%llu B) and X (%llu B) must each be under 4 GiB",
+                    fmt_name(f), (unsigned long long)need, (unsigned long long)T * K * 2u);
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     // Tile height TT (tokens) and K split SK: 128-token tiles (64 for short
@@ -616,6 +622,11 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     const uint32_t items = nN * ((T + TT - 1u) / TT) * SK;
     void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K, &SK};
     dim3 grid(8u * ((items + 7u) / 8u), 1, 1);
+    // warp-specialised kernel (512 threads): 128-token tiles whose every K split
+    // has a multiple of 4 chunks
+    if (TT == 128u && ctx->gemm_variant != 2 && NC % (4u * SK) == 0u)
+        return launch(ctx, f == Fmt::Q4_K ? K_GEMMW_Q4K_T128 : K_GEMMW_Q8_0_T128, grid, dim3(512, 1, 1), lds,
+                      stream, args);
     return launch(ctx, k, grid, dim3(256, 1, 1), lds, stream, args);
 }
 

@@ -1,5 +1,8 @@
 """Prefill GEMM parity: Y = X (bf16) . W^T over raw Q4_K / Q8_0 weights on the
-matrix cores.  Bars: relative L2 <= 1e-2 against the CPU oracle (per-token GEMV
+matrix cores.  Shapes cover both kernels: the warp-specialised one (128-token
+tiles whose K splits hold a multiple of 4 chunks: 256x256x2048, 200x300x4096,
+384x8192x1024 and the BASELINE shapes) and the 256-thread pipelined one (the
+rest), with partial token and weight-row tiles.  Bars: relative L2 <= 1e-2 against the CPU oracle (per-token GEMV
 on bf16-widened X; the north-star bound for bf16-MFMA GEMM), and <= 1e-5
 against a float64 product of X and the bf16-rounded dequantised weights --
 the kernel's own arithmetic, which pins the MFMA operand and accumulator
@@ -56,7 +59,7 @@ def check(gemm, fmt, T, N, K, seed=0, rows=None):
 
 @pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
 @pytest.mark.parametrize("T,N,K", [(128, 128, 256), (1, 128, 512), (37, 100, 1024), (200, 300, 768),
-                                   (256, 256, 2048), (300, 130, 1280)])
+                                   (256, 256, 2048), (300, 130, 1280), (200, 300, 4096), (384, 8192, 1024)])
 def test_shapes(gemm, fmt, T, N, K):
     if fmt == "q4_k" and K % 256:
         pytest.skip("Q4_K needs K % 256 == 0")
