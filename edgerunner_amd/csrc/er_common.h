@@ -77,6 +77,14 @@ ER_DEV u32x2 ld8_a2(const uint8_t *p) {
     return u32x2{alignbyte(v.y, v.x, sh), alignbyte(v2, v.y, sh)};
 }
 
+// 16 / 8 bytes at a 2-byte-aligned address as one vector load (the global
+// memory path's unaligned access mode, which the compiler itself relies on
+// for under-aligned vector loads).  Reads exactly [p, p + 16) / [p, p + 8).
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+ER_DEV u32x4 ld16_u2(const uint8_t *p) { return *(const u32x4_a2 *)p; }
+ER_DEV u32x2 ld8_u2(const uint8_t *p) { return *(const u32x2_a2 *)p; }
+
 // 4 bytes at a 2-byte-aligned address (two 16-bit loads, never over-reads).
 ER_DEV uint32_t ld4_a2(const uint8_t *p) { return ld2(p) | (ld2(p + 2) << 16); }
 

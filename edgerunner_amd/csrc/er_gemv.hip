@@ -595,6 +595,33 @@ ER_DEV void top1_wave_merge(float &v, uint32_t &i) {
     }
 }
 
+// Wave 0 of the workgroup: the quads of rows first + [0, 4 * nq), whose values
+// are tv[0 .. 4 * nq), merged into the partial (pv, pi)[blockIdx.x].
+ER_DEV void top1_partial(const float *tv, uint32_t first, uint32_t nq, float *__restrict__ pv,
+                         uint32_t *__restrict__ pi) {
+    if (threadIdx.x < 64u) {
+        float bv = -__builtin_inff();
+        uint32_t bi = 0;
+        for (uint32_t q = threadIdx.x; q < nq; q += 64u) {
+            const uint32_t r0 = first + 4u * q;
+            float v = tv[4u * q];
+            uint32_t i = r0;
+#pragma unroll
+            for (uint32_t k = 1; k < 4; ++k)
+                if (tv[4u * q + k] > v) {
+                    v = tv[4u * q + k];
+                    i = r0 + k;
+                }
+            top1_merge(bv, bi, v, i);
+        }
+        top1_wave_merge(bv, bi);
+        if (threadIdx.x == 0) {
+            pv[blockIdx.x] = bv;
+            pi[blockIdx.x] = bi;
+        }
+    }
+}
+
 // Workgroup epilogue: RPW row values of this workgroup (rows blockIdx.x * RPW
 // + [0, RPW), RPW a multiple of 4, M a multiple of 4) -> partial
 // (pv, pi)[blockIdx.x].  `mine` lanes hold acc[0..R) for local rows
@@ -606,30 +633,8 @@ ER_DEV void top1_epilogue(const float *acc, int R, uint32_t base, bool mine, uin
     if (mine)
         for (int r = 0; r < R; ++r) tv[base + (uint32_t)r] = acc[r];
     __syncthreads();
-    if (threadIdx.x < 64u) {
-        const uint32_t first = blockIdx.x * RPW;
-        float bv = -__builtin_inff();
-        uint32_t bi = 0;
-        for (uint32_t q = threadIdx.x; q < RPW / 4u; q += 64u) {
-            const uint32_t r0 = first + 4u * q;
-            if (r0 < M) {
-                float v = tv[4u * q];
-                uint32_t i = r0;
-#pragma unroll
-                for (uint32_t k = 1; k < 4; ++k)
-                    if (tv[4u * q + k] > v) {
-                        v = tv[4u * q + k];
-                        i = r0 + k;
-                    }
-                top1_merge(bv, bi, v, i);
-            }
-        }
-        top1_wave_merge(bv, bi);
-        if (threadIdx.x == 0) {
-            pv[blockIdx.x] = bv;
-            pi[blockIdx.x] = bi;
-        }
-    }
+    const uint32_t first = blockIdx.x * RPW;
+    top1_partial(tv, first, min(RPW, M - first) / 4u, pv, pi);
 }
 
 // One workgroup of 256 lanes: merges `count` partials into out[0].
@@ -661,7 +666,12 @@ extern "C" __global__ void __launch_bounds__(256)
 // q1..q4), scales sc[8h+2m+c] (m = 0..3) and d.  Its weights are positions
 // 256b + 128h + 32m + 16c + [0, 16): x granules G0 + 2m with G0 = 16b+8h+c,
 // 64-groups 4b+2h (m < 2) and 4b+2h+1.  Blocks are 2-byte aligned: the
-// fields are fetched with the aligned-window loads (ld16_a2 / ld8_a2).
+// fields are fetched with one 2-byte-aligned vector load each (ld16_u2 /
+// ld8_u2): 5 loads per slot and row, so with R = 4 rows the x loads issued
+// before them stay within the 63 outstanding loads a wave can count, and the
+// x conversion waits for x alone.  (4-byte-aligned windows plus a realigning
+// v_alignbyte, 9 loads per slot, measured 2-5% slower in the CU-resident
+// kernel.)
 // Value = d * sc * (q6 - 32): the -32 is applied through the x chunk sums.
 template <int LPR, int NS, int R, bool TOP1 = false>
 ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__ x,
@@ -691,10 +701,10 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint8_t *blk = W + (size_t)min(row0 + (uint32_t)r, M - 1u) * rowBytes + (s >> 2) * 210u;
-            fa[j][r] = ld16_a2(blk + 64u * h + 16u * c);
-            fb[j][r] = ld16_a2(blk + 64u * h + 32u + 16u * c);
-            fh[j][r] = ld16_a2(blk + 128u + 32u * h + 16u * c);
-            fs[j][r] = ld8_a2(blk + 192u + 8u * h);
+            fa[j][r] = ld16_u2(blk + 64u * h + 16u * c);
+            fb[j][r] = ld16_u2(blk + 64u * h + 32u + 16u * c);
+            fh[j][r] = ld16_u2(blk + 128u + 32u * h + 16u * c);
+            fs[j][r] = ld8_u2(blk + 192u + 8u * h);
             fd[j][r] = ld2(blk + 208u);
         }
     }
@@ -771,7 +781,7 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 }
 
 // ===========================================================================
-// Family 3: CU-resident integer-dot kernels (Q4_K, Q8_0; K % 256 == 0)
+// Family 3: CU-resident integer-dot kernels (Q4_K, Q8_0, Q6_K; K % 256 == 0)
 // ===========================================================================
 //
 // The family-1 kernels run ~3.5 workgroups per CU, and each stages x on its
@@ -852,6 +862,74 @@ struct CuQ8 {
     ER_DEV float dot(const Wt &w, const Xs &xs, float acc, uint32_t) { return q8_slot_dot(w, xs.xv, xs.sg, acc); }
 };
 
+// Q6_K, slot layout, loads and per-slot arithmetic of gemv_q6k_i8: one
+// 2-byte-aligned vector load per field (ld16_u2 / ld8_u2).
+struct CuQ6K {
+    struct Wt {
+        u32x4 a, b, h;  // ql (q1 / q3 nibbles), ql (q2 / q4), qh
+        u32x2 s;        // scales sc[8h .. 8h + 8)
+        uint32_t d;
+    };
+    struct Xs {
+        u32x4 xv[ER_XL_PLANES][4];
+        float X32[4], sgA, sgB, live;
+        uint32_t c;
+    };
+    ER_DEV size_t row_bytes(uint32_t K) { return (size_t)(K >> 8) * 210u; }
+    ER_DEV Wt load(const uint8_t *row, uint32_t s) {
+        const uint8_t *blk = row + (s >> 2) * 210u;
+        const uint32_t h = (s >> 1) & 1u, c = s & 1u;
+        return Wt{ld16_u2(blk + 64u * h + 16u * c), ld16_u2(blk + 64u * h + 32u + 16u * c),
+                  ld16_u2(blk + 128u + 32u * h + 16u * c), ld8_u2(blk + 192u + 8u * h), ld2(blk + 208u)};
+    }
+    ER_DEV Xs xside(const XLimbs &X, uint32_t s, float live) {
+        Xs o;
+        const uint32_t b = s >> 2, h = (s >> 1) & 1u, c = s & 1u;
+        const uint32_t G0 = 16u * b + 8u * h + c;  // granules G0 + 2m, m = 0..3
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t off = 16u * xl_gswz(G0 + 2u * m);
+#pragma unroll
+            for (int l = 0; l < ER_XL_PLANES; ++l)
+                o.xv[l][m] = *(const u32x4 *)__builtin_assume_aligned(X.planes + (size_t)l * X.K + off, 16);
+        }
+        o.sgA = live * X.sg64[4u * b + 2u * h];
+        o.sgB = live * X.sg64[4u * b + 2u * h + 1u];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) o.X32[m] = 32.0f * X.x16[G0 + 2u * m];
+        o.live = live;
+        o.c = c;
+        return o;
+    }
+    ER_DEV float dot(const Wt &w, const Xs &xs, float acc, uint32_t M0F) {
+        const uint32_t M30 = 0x30303030u;
+        const uint32_t A[4] = {w.a.x, w.a.y, w.a.z, w.a.w};
+        const uint32_t B[4] = {w.b.x, w.b.y, w.b.z, w.b.w};
+        const uint32_t H[4] = {w.h.x, w.h.y, w.h.z, w.h.w};
+        int cq[4][ER_XL_PLANES] = {};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q[4] = {(A[k] & M0F) | ((H[k] << 4) & M30), (B[k] & M0F) | ((H[k] << 2) & M30),
+                                   ((A[k] >> 4) & M0F) | (H[k] & M30), ((B[k] >> 4) & M0F) | ((H[k] >> 2) & M30)};
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int l = 0; l < ER_XL_PLANES; ++l)
+                    cq[m][l] = __builtin_amdgcn_sdot4((int)q[m], (int)xs.xv[l][m][k], cq[m][l], false);
+        }
+        // scales: m = 0, 1 in dword x (bytes c, 2 + c), m = 2, 3 in dword y
+        const float s0 = (float)(int8_t)(w.s.x >> (8u * xs.c));
+        const float s1 = (float)(int8_t)(w.s.x >> (8u * xs.c + 16u));
+        const float s2 = (float)(int8_t)(w.s.y >> (8u * xs.c));
+        const float s3 = (float)(int8_t)(w.s.y >> (8u * xs.c + 16u));
+        float v = s0 * __builtin_fmaf(xs.sgA, xl_combine(cq[0][0], cq[0][1], cq[0][2]), -xs.live * xs.X32[0]);
+        v = __builtin_fmaf(s1, __builtin_fmaf(xs.sgA, xl_combine(cq[1][0], cq[1][1], cq[1][2]), -xs.live * xs.X32[1]), v);
+        v = __builtin_fmaf(s2, __builtin_fmaf(xs.sgB, xl_combine(cq[2][0], cq[2][1], cq[2][2]), -xs.live * xs.X32[2]), v);
+        v = __builtin_fmaf(s3, __builtin_fmaf(xs.sgB, xl_combine(cq[3][0], cq[3][1], cq[3][2]), -xs.live * xs.X32[3]), v);
+        return __builtin_fmaf(f16_to_f32(w.d), v, acc);
+    }
+};
+
 // LDS bytes of the family: limbs, then K fp32 values of raw x.
 ER_DEV uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 
@@ -863,9 +941,14 @@ ER_DEV uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 // lane i % LPR of res[i / LPR] - and stored after the last step, so only
 // weight loads are outstanding while rows are computed and each wait covers
 // exactly the loads it needs.
-template <class F, int LPR, int NS, int PD, int JC>
+// TOP1: instead of storing y, the workgroup's row values go to LDS and wave 0
+// merges their quads into the partial (pv, pi)[blockIdx.x] (rowsPerWg and M
+// multiples of 4, so no quad spans two workgroups; the dynamic LDS holds at
+// least 4 * rowsPerWg bytes).
+template <class F, int LPR, int NS, int PD, int JC, bool TOP1 = false>
 ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
-                    uint32_t M, uint32_t K, uint32_t rowsPerWg) {
+                    uint32_t M, uint32_t K, uint32_t rowsPerWg, float *__restrict__ pv = nullptr,
+                    uint32_t *__restrict__ pi = nullptr) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     __shared__ uint32_t staged;  // staging waves done
     constexpr uint32_t G = 64u / LPR;
@@ -922,13 +1005,21 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
         __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's limb stores have landed
         if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 #pragma unroll
-        for (int i = 0; i < PD && i < UNR; ++i) issue((uint32_t)i, i);
+        for (int i = 0; i < PD && i < UNR; ++i) {
+            issue((uint32_t)i, i);
+            // rows leave in consumption order, so each step's wait covers its own row only
+            __builtin_amdgcn_sched_barrier(0);
+        }
     } else {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < PD && i < UNR; ++i) issue((uint32_t)i, i);
+        for (int i = 0; i < PD && i < UNR; ++i) {
+            issue((uint32_t)i, i);
+            // rows leave in consumption order, so each step's wait covers its own row only
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     // the staging waves always finish; the bound only keeps a wave from
@@ -983,11 +1074,24 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) step(i0 + (uint32_t)u, u, u + PD < UNR);
+    if constexpr (TOP1) {
+        __syncthreads();  // every wave is done with x: LDS now holds the row values
+        float *tv = (float *)lds;
 #pragma unroll
-    for (int q = 0; q < NPARK; ++q) {
-        const uint32_t st = (uint32_t)q * LPR + li;
-        const uint32_t row = first + st * STEP;
-        if (st < J && row < re) y[row] = res[q];
+        for (int q = 0; q < NPARK; ++q) {
+            const uint32_t st = (uint32_t)q * LPR + li;
+            const uint32_t row = first + st * STEP;
+            if (st < J && row < re) tv[row - rb] = res[q];
+        }
+        __syncthreads();
+        top1_partial(tv, rb, (re - rb) / 4u, pv, pi);
+    } else {
+#pragma unroll
+        for (int q = 0; q < NPARK; ++q) {
+            const uint32_t st = (uint32_t)q * LPR + li;
+            const uint32_t row = first + st * STEP;
+            if (st < J && row < re) y[row] = res[q];
+        }
     }
 }
 
@@ -1362,6 +1466,8 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
 // CU-resident family: er_gemv_<fmt>_cu_l<LPR>_n<NS>_j<JC> (JC row steps per
 // wave, unrolled) and _jr (rolled, up to 64 steps per lane group); grid
 // (ceil(M / rowsPerWg), batch), rowsPerWg = ER_CU_WAVES * 64 / LPR * steps.
+// er_gemv_q6k_top1_cu_*: the same kernels with the top-1 partial epilogue
+// (grid ceil(M / rowsPerWg), one partial per workgroup).
 #define ER_CU_ENTRY_J(fmt, F, LPR, NS, JC, tag)                                                 \
     extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                           \
         er_gemv_##fmt##_cu_l##LPR##_n##NS##_j##tag(const uint8_t *__restrict__ W,              \
@@ -1370,16 +1476,29 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
                                                    uint32_t rowsPerWg) {                      \
         gemv_cu<F, LPR, NS, ER_CU_PD, JC>(W, x, y, M, K, rowsPerWg);                          \
     }
-#define ER_CU_STEPS_1(fmt, F, LPR, NS) ER_CU_ENTRY_J(fmt, F, LPR, NS, 1, 1)
-#define ER_CU_STEPS_2(fmt, F, LPR, NS) ER_CU_STEPS_1(fmt, F, LPR, NS) ER_CU_ENTRY_J(fmt, F, LPR, NS, 2, 2)
-#define ER_CU_STEPS_8(fmt, F, LPR, NS)                                                                       \
-    ER_CU_STEPS_2(fmt, F, LPR, NS) ER_CU_ENTRY_J(fmt, F, LPR, NS, 3, 3) ER_CU_ENTRY_J(fmt, F, LPR, NS, 4, 4)  \
-    ER_CU_ENTRY_J(fmt, F, LPR, NS, 5, 5) ER_CU_ENTRY_J(fmt, F, LPR, NS, 6, 6)                                \
-    ER_CU_ENTRY_J(fmt, F, LPR, NS, 7, 7) ER_CU_ENTRY_J(fmt, F, LPR, NS, 8, 8) ER_CU_ENTRY_J(fmt, F, LPR, NS, 0, r)
-#define ER_CU_ENTRY_Q4K(LPR, NS, MAXJ) ER_CU_STEPS_##MAXJ(q4k, CuQ4K, LPR, NS)
-#define ER_CU_ENTRY_Q8(LPR, NS, MAXJ) ER_CU_STEPS_##MAXJ(q8_0, CuQ8, LPR, NS)
+#define ER_CU_TOP1_J(fmt, F, LPR, NS, JC, tag)                                                     \
+    extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                              \
+        er_gemv_##fmt##_top1_cu_l##LPR##_n##NS##_j##tag(const uint8_t *__restrict__ W,            \
+                                                        const float *__restrict__ x,             \
+                                                        float *__restrict__ pv,                  \
+                                                        uint32_t *__restrict__ pi, uint32_t M,   \
+                                                        uint32_t K, uint32_t rowsPerWg) {        \
+        gemv_cu<F, LPR, NS, ER_CU_PD, JC, true>(W, x, nullptr, M, K, rowsPerWg, pv, pi);         \
+    }
+#define ER_CU_STEPS_1(E, fmt, F, LPR, NS) E(fmt, F, LPR, NS, 1, 1)
+#define ER_CU_STEPS_2(E, fmt, F, LPR, NS) ER_CU_STEPS_1(E, fmt, F, LPR, NS) E(fmt, F, LPR, NS, 2, 2)
+#define ER_CU_STEPS_8(E, fmt, F, LPR, NS)                                                              \
+    ER_CU_STEPS_2(E, fmt, F, LPR, NS) E(fmt, F, LPR, NS, 3, 3) E(fmt, F, LPR, NS, 4, 4)                  \
+    E(fmt, F, LPR, NS, 5, 5) E(fmt, F, LPR, NS, 6, 6) E(fmt, F, LPR, NS, 7, 7) E(fmt, F, LPR, NS, 8, 8) \
+    E(fmt, F, LPR, NS, 0, r)
+#define ER_CU_ENTRY_Q4K(LPR, NS, MAXJ) ER_CU_STEPS_##MAXJ(ER_CU_ENTRY_J, q4k, CuQ4K, LPR, NS)
+#define ER_CU_ENTRY_Q8(LPR, NS, MAXJ) ER_CU_STEPS_##MAXJ(ER_CU_ENTRY_J, q8_0, CuQ8, LPR, NS)
+#define ER_CU_ENTRY_Q6K(LPR, NS, MAXJ)                        \
+    ER_CU_STEPS_##MAXJ(ER_CU_ENTRY_J, q6k, CuQ6K, LPR, NS) \
+    ER_CU_STEPS_##MAXJ(ER_CU_TOP1_J, q6k, CuQ6K, LPR, NS)
 ER_CU_CONFIGS_Q4K(ER_CU_ENTRY_Q4K)
 ER_CU_CONFIGS_Q8(ER_CU_ENTRY_Q8)
+ER_CU_CONFIGS_Q6K(ER_CU_ENTRY_Q6K)
 
 // Multi-matrix and GeGLU Q4_K kernels: R counts row computations per lane
 // group (GeGLU: R/2 gate rows + the matching up rows).

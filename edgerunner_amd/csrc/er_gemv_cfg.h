@@ -28,7 +28,7 @@
     ER_I8_MULTI_CONFIGS_L(X, 64) ER_I8_MULTI_CONFIGS_L(X, 32) ER_I8_MULTI_CONFIGS_L(X, 16) \
     ER_I8_MULTI_CONFIGS_L(X, 4)
 
-// CU-resident Q4_K / Q8_0 kernels (family 3): X(LPR, NS, MAXJ), one 8-wave
+// CU-resident Q4_K / Q8_0 / Q6_K kernels (family 3): X(LPR, NS, MAXJ), one 8-wave
 // workgroup per CU-sized share of the rows, unrolled kernels for 1..MAXJ row
 // steps per wave, and for MAXJ == 8 a rolled one for up to ER_CU_MAX_ROLLED.
 // With more slots per lane than MAXJ allows, the unrolled steps keep too many
@@ -41,3 +41,4 @@
 #define ER_CU_CONFIGS_Q4K(X) \
     X(16, 1, 8) X(16, 2, 8) X(32, 1, 8) X(32, 2, 8) X(64, 1, 8) X(64, 2, 8) X(64, 3, 2) X(64, 4, 2) X(32, 7, 1)
 #define ER_CU_CONFIGS_Q8(X) X(16, 1, 8) X(32, 1, 8) X(64, 1, 8)
+#define ER_CU_CONFIGS_Q6K(X) X(16, 1, 8) X(32, 1, 8) X(64, 1, 8)

@@ -111,7 +111,7 @@ constexpr int kI8Count = (int)(sizeof(kI8Cfg) / sizeof(kI8Cfg[0]));
 // length use them (the default dynamic LDS limit is 64 KiB).
 constexpr uint32_t kI8MaxK = 16384;
 
-// CU-resident Q4_K / Q8_0 configurations {LPR, NS, MAXJ} (er_gemv_cfg.h): kernels
+// CU-resident Q4_K / Q8_0 / Q6_K configurations {LPR, NS, MAXJ} (er_gemv_cfg.h): kernels
 // for 1..maxJ unrolled steps, and a rolled one when maxJ == ER_CU_MAX_STEPS.
 struct CuCfg {
     uint8_t lpr, ns, maxJ;
@@ -119,11 +119,13 @@ struct CuCfg {
 #define ER_CU_ROW(LPR, NS, MAXJ) {LPR, NS, MAXJ},
 constexpr CuCfg kCuCfgQ4K[] = {ER_CU_CONFIGS_Q4K(ER_CU_ROW)};
 constexpr CuCfg kCuCfgQ8[] = {ER_CU_CONFIGS_Q8(ER_CU_ROW)};
+constexpr CuCfg kCuCfgQ6K[] = {ER_CU_CONFIGS_Q6K(ER_CU_ROW)};
 #undef ER_CU_ROW
 constexpr int kCuCountQ4K = (int)(sizeof(kCuCfgQ4K) / sizeof(kCuCfgQ4K[0]));
 constexpr int kCuCountQ8 = (int)(sizeof(kCuCfgQ8) / sizeof(kCuCfgQ8[0]));
-// The CU-resident family covers Q4_K rows of up to 256 slots and Q8_0 rows of
-// up to 64 (pick_cu finds no configuration beyond), and holds limbs plus raw x
+constexpr int kCuCountQ6K = (int)(sizeof(kCuCfgQ6K) / sizeof(kCuCfgQ6K[0]));
+// The CU-resident family covers Q4_K rows of up to 256 slots and Q8_0 / Q6_K
+// rows of up to 64 (pick_cu finds no configuration beyond), and holds limbs plus raw x
 // in LDS: 3K + K/4 + K/16 + 4K bytes.
 constexpr uint32_t kCuMaxK = 16384;
 constexpr uint32_t cu_lds_bytes(uint32_t K) { return 3u * K + K / 16u * 4u + K / 64u * 4u + 4u * K; }
@@ -164,6 +166,8 @@ struct er_hip_ctx {
     hipFunction_t fnQ6KTop1[kI8Count] = {};
     hipFunction_t fnQ4KCu[kCuCountQ4K][ER_CU_MAX_STEPS + 1] = {};  // [steps - 1]; [ER_CU_MAX_STEPS]: rolled
     hipFunction_t fnQ8Cu[kCuCountQ8][ER_CU_MAX_STEPS + 1] = {};
+    hipFunction_t fnQ6KCu[kCuCountQ6K][ER_CU_MAX_STEPS + 1] = {};
+    hipFunction_t fnQ6KTop1Cu[kCuCountQ6K][ER_CU_MAX_STEPS + 1] = {};
     hipFunction_t fnQ4KMulti[kI8MultiCount] = {};
     hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
     hipFunction_t fnQ8Multi[kI8MultiCount] = {};
@@ -374,6 +378,51 @@ er_status validate_gemv(Fmt f, er_buffer W, er_buffer x, er_buffer y, uint32_t b
     return ER_OK;
 }
 
+// CU-resident family (er_gemv.hip gemv_cu) for one call: rows of K % 256 == 0
+// up to kCuMaxK with a configuration covering K / 64 slots.  Taken when a CU's
+// share of one token's rows is 3..ER_CU_MAX_STEPS row steps, or, for Q4_K /
+// Q8_0 rows longer than 8192 weights (whose per-workgroup x staging the
+// lane-group family repeats ~512 times), any share up to the unrolled steps.
+// Q6_K takes the rolled kernel beyond ER_CU_MAX_STEPS steps (the lane-group
+// Q6_K kernel waits for its weight loads before converting x); for Q4_K /
+// Q8_0 the rolled loop measured no faster than the lane-group family and runs
+// only when ER_HIP_GEMV_CU=1 forces the family.  The choice of configuration
+// and family depends on M and K only, so a batched call, its per-token calls
+// and the Q6_K top-1 over the same matrix run the same per-row arithmetic;
+// the batch only changes the row partition (about one workgroup per CU over
+// all tokens).
+struct CuPlan {
+    int ci = -1;             // configuration index
+    int slot = 0;            // steps - 1, or ER_CU_MAX_STEPS for the rolled kernel
+    uint32_t rowsPerWg = 0;  // step rows x steps
+};
+bool plan_cu(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batch, CuPlan &p) {
+    if (K % 256u != 0 || K > kCuMaxK || ctx->gemv_fp32 != 0 || ctx->i8_override >= 0 || ctx->cu_mode == 0 ||
+        (uint64_t)cu_lds_bytes(K) + 1024u > ctx->info.lds_per_workgroup || batch == 0)
+        return false;
+    const CuCfg *cfg = f == Fmt::Q4_K ? kCuCfgQ4K : (f == Fmt::Q8_0 ? kCuCfgQ8 : kCuCfgQ6K);
+    const int ci = pick_cu(cfg, f == Fmt::Q4_K ? kCuCountQ4K : (f == Fmt::Q8_0 ? kCuCountQ8 : kCuCountQ6K), K / 64u);
+    if (ci < 0) return false;
+    const CuCfg &c = cfg[ci];
+    const uint32_t step = ER_CU_WAVES * (64u / c.lpr);  // rows per workgroup step
+    const uint32_t cu = (uint32_t)ctx->cu_count;
+    const uint32_t needed1 = ((M + cu - 1u) / cu + step - 1u) / step;  // steps per CU, one token
+    const bool rolled = c.maxJ == ER_CU_MAX_STEPS;
+    const bool use = ctx->cu_mode == 1 ? (rolled || needed1 <= c.maxJ)
+                     : f == Fmt::Q6_K  ? (needed1 >= 3u && (rolled || needed1 <= c.maxJ))
+                                       : (needed1 <= c.maxJ && (needed1 >= 3u || K > 8192u));
+    if (!use) return false;
+    // unrolled kernels up to maxJ steps, the rolled one up to ER_CU_MAX_ROLLED,
+    // more workgroups beyond
+    const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
+    const uint32_t maxSteps = rolled ? ER_CU_MAX_ROLLED : c.maxJ;
+    const uint32_t steps = std::min<uint32_t>(maxSteps, ((M + perToken - 1u) / perToken + step - 1u) / step);
+    p.ci = ci;
+    p.rowsPerWg = step * steps;
+    p.slot = steps <= ER_CU_MAX_STEPS ? (int)steps - 1 : ER_CU_MAX_STEPS;
+    return true;
+}
+
 er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_buffer x,
                       er_buffer y, uint32_t batch, uint32_t M, uint32_t K) {
     // shape validation first (it needs no device), then the context
@@ -388,45 +437,15 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
 
     void *args[] = {&W.data, &x.data, &y.data, &M, &K};
     const bool q8Aligned = f == Fmt::Q8_0 && K % 64u == 0;
-    // CU-resident family: Q4_K / Q8_0 rows of K % 256 == 0 up to kCuMaxK, when a
-    // CU's share of one token's rows is 3..ER_CU_MAX_STEPS row steps, or any
-    // share up to the configuration's unrolled steps for rows longer than 8192
-    // weights (whose per-workgroup x staging the lane-group family repeats
-    // ~512 times).  Below 3 steps of short rows the lane-group family, with
-    // more workgroups, is as fast; above 8 the rolled loop measured no faster
-    // than it (the rolled kernels run when ER_HIP_GEMV_CU=1 forces the family).
-    const bool cuFits = f != Fmt::Q6_K && K % 256u == 0 && K <= kCuMaxK && ctx->gemv_fp32 == 0 &&
-                        ctx->i8_override < 0 && ctx->cu_mode != 0 &&
-                        (uint64_t)cu_lds_bytes(K) + 1024u <= ctx->info.lds_per_workgroup;
-    const int cuCi = !cuFits ? -1
-                     : f == Fmt::Q4_K ? pick_cu(kCuCfgQ4K, kCuCountQ4K, K / 64u)
-                                      : pick_cu(kCuCfgQ8, kCuCountQ8, K / 64u);
-    if (cuCi >= 0) {
-        const CuCfg &c = f == Fmt::Q4_K ? kCuCfgQ4K[cuCi] : kCuCfgQ8[cuCi];
-        const uint32_t step = ER_CU_WAVES * (64u / c.lpr);  // rows per workgroup step
-        // The choice of family depends on M and K only, so a batched call and
-        // its per-token calls run the same per-row arithmetic (bit-identical
-        // outputs); the batch only changes the row partition.
-        const uint32_t cu = (uint32_t)ctx->cu_count;
-        const uint32_t needed1 = ((M + cu - 1u) / cu + step - 1u) / step;  // steps per CU, one token
-        const bool rolled = c.maxJ == ER_CU_MAX_STEPS;
-        const bool use = ctx->cu_mode == 1 ? (rolled || needed1 <= c.maxJ)
-                                           : (needed1 <= c.maxJ && (needed1 >= 3u || K > 8192u));
-        if (use) {
-            // about one workgroup per CU over all tokens: unrolled kernels up to
-            // maxJ steps, the rolled one up to ER_CU_MAX_ROLLED, more workgroups beyond
-            const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
-            const uint32_t maxSteps = rolled ? ER_CU_MAX_ROLLED : c.maxJ;
-            const uint32_t steps =
-                std::min<uint32_t>(maxSteps, ((M + perToken - 1u) / perToken + step - 1u) / step);
-            const uint32_t rowsPerWg = step * steps;
-            const int slot = steps <= ER_CU_MAX_STEPS ? (int)steps - 1 : ER_CU_MAX_STEPS;
-            dim3 grid((M + rowsPerWg - 1u) / rowsPerWg, batch, 1);
-            void *cargs[] = {&W.data, &x.data, &y.data, &M, &K, (void *)&rowsPerWg};
-            return launch_fn(f == Fmt::Q4_K ? ctx->fnQ4KCu[cuCi][slot] : ctx->fnQ8Cu[cuCi][slot],
-                             f == Fmt::Q4_K ? "er_gemv_q4k_cu" : "er_gemv_q8_0_cu", grid,
-                             dim3(64u * ER_CU_WAVES, 1, 1), cu_lds_bytes(K), stream, cargs);
-        }
+    CuPlan cp;
+    if (plan_cu(ctx, f, M, K, batch, cp)) {
+        dim3 grid((M + cp.rowsPerWg - 1u) / cp.rowsPerWg, batch, 1);
+        void *cargs[] = {&W.data, &x.data, &y.data, &M, &K, (void *)&cp.rowsPerWg};
+        hipFunction_t fn = f == Fmt::Q4_K   ? ctx->fnQ4KCu[cp.ci][cp.slot]
+                           : f == Fmt::Q8_0 ? ctx->fnQ8Cu[cp.ci][cp.slot]
+                                            : ctx->fnQ6KCu[cp.ci][cp.slot];
+        return launch_fn(fn, f == Fmt::Q4_K ? "er_gemv_q4k_cu" : (f == Fmt::Q8_0 ? "er_gemv_q8_0_cu" : "er_gemv_q6k_cu"),
+                         grid, dim3(64u * ER_CU_WAVES, 1, 1), cu_lds_bytes(K), stream, cargs);
     }
     if ((f != Fmt::Q8_0 || q8Aligned) && K <= kI8MaxK && ctx->gemv_fp32 == 0) {
         int ci = pick_i8(K / 64u, M, ctx->cu_count);
@@ -471,9 +490,10 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
 // Greedy top-1 over a Q6_K head (GEMVKernel.encodeQ6KWeightsPackedTop1,
 // GEMVKernel.swift:1205-1265): M % 4 == 0 (INVALID_MATRIX_SHAPE), then the
 // K-quant shape rules, then partial buffers of >= M/4 entries and a 4-byte
-// index buffer (ENCODING_FAILED).  Two launches: the integer-dot Q6_K GEMV
-// with the top-1 epilogue (one partial per workgroup, at most M/4 of them)
-// and er_top1_reduce.
+// index buffer (ENCODING_FAILED).  Two launches: a Q6_K GEMV with the top-1
+// epilogue (the CU-resident kernel when the plain GEMV over this matrix takes
+// that family, else the lane-group one, so both compute the same row values;
+// one partial per workgroup, at most M/4 of them) and er_top1_reduce.
 er_status encode_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buffer x,
                           er_buffer pv, er_buffer pi, er_buffer out, uint32_t M, uint32_t K) {
     if (M % 4u != 0)
@@ -500,7 +520,17 @@ er_status encode_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buf
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     uint32_t count = 0;
-    if (M > 0) {
+    CuPlan cp;
+    if (M > 0 && plan_cu(ctx, Fmt::Q6_K, M, K, 1u, cp)) {
+        // one partial per workgroup (rowsPerWg >= 8, so at most M/4); the
+        // row values of a workgroup reuse its x area of LDS
+        count = (M + cp.rowsPerWg - 1u) / cp.rowsPerWg;
+        const uint32_t ldsTop1 = std::max<uint32_t>(cu_lds_bytes(K), 4u * cp.rowsPerWg);
+        void *args[] = {&W.data, &x.data, &pv.data, &pi.data, &M, &K, (void *)&cp.rowsPerWg};
+        st = launch_fn(ctx->fnQ6KTop1Cu[cp.ci][cp.slot], "er_gemv_q6k_top1_cu", dim3(count, 1, 1),
+                       dim3(64u * ER_CU_WAVES, 1, 1), ldsTop1, stream, args);
+        if (st != ER_OK) return st;
+    } else if (M > 0) {
         int ci = pick_i8(K / 64u, M, ctx->cu_count);
         if (ctx->i8_override >= 0 && (uint32_t)kI8Cfg[ctx->i8_override].lpr *
                                              kI8Cfg[ctx->i8_override].ns >= K / 64u)
@@ -909,9 +939,11 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
             }
         }
     }
-    for (int fmt = 0; fmt < 2; ++fmt) {
-        const CuCfg *cfg = fmt == 0 ? kCuCfgQ4K : kCuCfgQ8;
-        const int count = fmt == 0 ? kCuCountQ4K : kCuCountQ8;
+    for (int kind = 0; kind < 4; ++kind) {
+        // q4k, q8_0, q6k and the q6k top-1 kernels
+        static const char *const names[4] = {"q4k_cu", "q8_0_cu", "q6k_cu", "q6k_top1_cu"};
+        const CuCfg *cfg = kind == 0 ? kCuCfgQ4K : (kind == 1 ? kCuCfgQ8 : kCuCfgQ6K);
+        const int count = kind == 0 ? kCuCountQ4K : (kind == 1 ? kCuCountQ8 : kCuCountQ6K);
         for (int i = 0; i < count; ++i)
             for (int jc = 1; jc <= ER_CU_MAX_STEPS + 1; ++jc) {
                 // kernels exist for steps 1..maxJ, and the rolled one (slot
@@ -922,9 +954,12 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
                     std::snprintf(tag, sizeof(tag), "%d", jc);
                 else
                     std::snprintf(tag, sizeof(tag), "r");
-                std::snprintf(name, sizeof(name), "er_gemv_%s_cu_l%u_n%u_j%s", fmt == 0 ? "q4k" : "q8_0",
-                              (unsigned)cfg[i].lpr, (unsigned)cfg[i].ns, tag);
-                hipFunction_t *slot = fmt == 0 ? &ctx->fnQ4KCu[i][jc - 1] : &ctx->fnQ8Cu[i][jc - 1];
+                std::snprintf(name, sizeof(name), "er_gemv_%s_l%u_n%u_j%s", names[kind], (unsigned)cfg[i].lpr,
+                              (unsigned)cfg[i].ns, tag);
+                hipFunction_t *slot = kind == 0   ? &ctx->fnQ4KCu[i][jc - 1]
+                                      : kind == 1 ? &ctx->fnQ8Cu[i][jc - 1]
+                                      : kind == 2 ? &ctx->fnQ6KCu[i][jc - 1]
+                                                  : &ctx->fnQ6KTop1Cu[i][jc - 1];
                 e = hipModuleGetFunction(slot, ctx->module, name);
                 if (e != hipSuccess) {
                     (void)hipModuleUnload(ctx->module);

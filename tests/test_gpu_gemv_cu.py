@@ -1,5 +1,6 @@
 """CU-resident GEMV family (K % 256 == 0; Q4_K rows up to 16384 weights, Q8_0
-rows up to 4096, longer Q8_0 rows fall back to the lane-group family):
+and Q6_K rows up to 4096, longer rows of those fall back to the lane-group
+family):
 the GEMV parity bar of the other kernels (relative L2 <= 1e-3 against the CPU
 oracle, the reference test's absolute 1e-4 on its case, exact one-hot
 columns, batched equal to per-token) with the family forced on for every
@@ -21,9 +22,12 @@ from conftest import rel_l2
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
-DSCALE = {"q8_0": {"dscale": 0.02}, "q4_k": {"dscale": 0.01, "dminscale": 0.01}}
-EXEC = {"q8_0": "executeQ8_0Weights", "q4_k": "executeQ4KWeights"}
-EXEC_B = {"q8_0": "executeBatchedQ8_0Weights", "q4_k": "executeBatchedQ4KWeights"}
+DSCALE = {"q8_0": {"dscale": 0.02}, "q4_k": {"dscale": 0.01, "dminscale": 0.01},
+          "q6_k": {"dscale": 0.005}}
+EXEC = {"q8_0": "executeQ8_0Weights", "q4_k": "executeQ4KWeights", "q6_k": "executeQ6KWeights"}
+EXEC_B = {"q8_0": "executeBatchedQ8_0Weights", "q4_k": "executeBatchedQ4KWeights",
+          "q6_k": "executeBatchedQ6KWeights"}
+FMTS = ["q4_k", "q8_0", "q6_k"]
 
 
 def _context(mode: str) -> Context:
@@ -57,9 +61,11 @@ SHAPES = [(1, 256), (7, 1024), (100, 2048), (333, 3072), (1000, 4096), (64, 5120
 ROLLED = [(28672, 4096), (151936, 1024), (140000, 256)]
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M,K", SHAPES)
 def test_cu_family_matches_oracle(cu_gemv, fmt, M, K):
+    if fmt == "q6_k" and K > 4096:
+        pytest.skip("Q6_K rows above 4096 weights take the lane-group family")
     W = synth.weights(fmt, synth.seed(80, M % 97), M, K, **DSCALE[fmt])
     x = synth.normal_f32(synth.seed(80, 200 + K % 89), K)
     y = getattr(cu_gemv, EXEC[fmt])(W, x, M, K)
@@ -67,7 +73,7 @@ def test_cu_family_matches_oracle(cu_gemv, fmt, M, K):
     assert rel_l2(y, exp) < TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M,K", ROLLED)
 def test_cu_family_rolled_matches_oracle(cu_gemv, fmt, M, K):
     W = synth.weights(fmt, synth.seed(85, M % 97), M, K, **DSCALE[fmt])
@@ -87,9 +93,11 @@ def test_cu_family_reference_q4k_case(cu_gemv):
     assert np.max(np.abs(y - exp)) < 1e-4 and rel_l2(y, exp) < TOL
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("K", [1024, 4096, 8192])
 def test_cu_family_one_hot_columns(cu_gemv, fmt, K):
+    if fmt == "q6_k" and K > 4096:
+        pytest.skip("Q6_K rows above 4096 weights take the lane-group family")
     M = 40
     W = synth.weights(fmt, synth.seed(81, 0), M, K, **DSCALE[fmt])
     cols = rn.weights_f32(fmt, W, M, K)
@@ -100,9 +108,11 @@ def test_cu_family_one_hot_columns(cu_gemv, fmt, K):
         assert np.array_equal(y, cols[:, j]), j
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M,K,T", [(300, 1024, 5), (1000, 4096, 3), (77, 8192, 2)])
 def test_cu_family_batched_equals_per_token(cu_gemv, fmt, M, K, T):
+    if fmt == "q6_k" and K > 4096:
+        pytest.skip("Q6_K rows above 4096 weights take the lane-group family")
     W = synth.weights(fmt, synth.seed(82, 0), M, K, **DSCALE[fmt])
     x = synth.normal_f32(synth.seed(82, 1), T * K)
     yb = getattr(cu_gemv, EXEC_B[fmt])(W, x, T, M, K).reshape(T, M)
@@ -111,7 +121,7 @@ def test_cu_family_batched_equals_per_token(cu_gemv, fmt, M, K, T):
         assert np.array_equal(yb[t], single)
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS)
 def test_cu_family_equals_lane_matched_family1(cu_gemv, fmt):
     """At 64 lanes x 1 slot both families form each row's sum the same way
     (slot dot, then the 64-lane reduction), so they agree bit for bit."""
@@ -127,7 +137,7 @@ def test_cu_family_equals_lane_matched_family1(cu_gemv, fmt):
     assert np.array_equal(y0, y1)
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M,K,T", [(12288, 2048, 3), (24576, 1024, 2), (6144, 4096, 4)])
 def test_default_dispatch_batched_equals_per_token(gemv, fmt, M, K, T):
     """Default dispatch on shapes the CU-resident family takes: the family is
@@ -141,3 +151,50 @@ def test_default_dispatch_batched_equals_per_token(gemv, fmt, M, K, T):
         assert np.array_equal(yb[t], single)
     exp = ref.gemv(fmt, W, x[:K], M, K, threads=ref.max_threads())
     assert rel_l2(yb[0], exp) < TOL
+
+
+# Q6_K top-1 through the CU-resident kernels: the index equals the selection
+# rule applied to the same context's plain GEMV output (the same per-row
+# arithmetic), on shapes with 1..8 unrolled steps and rolled ones.
+@pytest.mark.parametrize("M,K", [(400, 256), (4096, 1024), (20000, 3072), (14336, 4096), (151936, 1024),
+                                 (128256, 4096)])
+def test_cu_top1_matches_rule(cu_gemv, M, K):
+    W = synth.weights("q6_k", synth.seed(86, M % 97), M, K, dscale=0.005)
+    x = synth.normal_f32(synth.seed(86, 200 + K % 89), K)
+    y = cu_gemv.executeQ6KWeights(W, x, M, K)
+    assert cu_gemv.executeQ6KWeightsTop1(W, x, M, K) == ref.top1(y)
+
+
+def test_cu_top1_ties_and_nan(cu_gemv):
+    """A copy of the winning row at a lower index wins the tie, at a higher one
+    loses it; identical rows give row 0, and all-NaN logits keep row 0."""
+    M, K = 8192, 1024
+    W = synth.weights("q6_k", synth.seed(87, 0), M, K, dscale=0.005).reshape(M, -1).copy()
+    x = synth.normal_f32(synth.seed(87, 1), K)
+    a = cu_gemv.executeQ6KWeightsTop1(W.reshape(-1), x, M, K)
+    for b in (0, 5, a // 2 if a > 0 else 3, a - 1 if a > 0 else 7):
+        if b >= a:
+            continue
+        Wt = W.copy()
+        Wt[b] = W[a]
+        assert cu_gemv.executeQ6KWeightsTop1(Wt.reshape(-1), x, M, K) == b
+    hi = min(M - 1, a + 1000)
+    Wt = W.copy()
+    Wt[hi] = W[a]
+    assert cu_gemv.executeQ6KWeightsTop1(Wt.reshape(-1), x, M, K) == min(a, hi)
+    Wsame = np.tile(W[a], (M, 1))
+    assert cu_gemv.executeQ6KWeightsTop1(Wsame.reshape(-1), x, M, K) == 0
+    xn = np.full(K, np.nan, np.float32)
+    assert cu_gemv.executeQ6KWeightsTop1(W.reshape(-1), xn, M, K) == 0
+
+
+def test_default_dispatch_q6k_head_top1_consistent(gemv):
+    """Default dispatch on the 128256 x 4096 head (rolled CU-resident kernels
+    for both the plain GEMV and the top-1)."""
+    M, K = 128256, 4096
+    W = synth.weights("q6_k", synth.seed(88, 0), M, K, dscale=0.005)
+    x = synth.normal_f32(synth.seed(88, 1), K)
+    y = gemv.executeQ6KWeights(W, x, M, K)
+    assert gemv.executeQ6KWeightsTop1(W, x, M, K) == ref.top1(y)
+    exp = ref.gemv("q6_k", W, x, M, K, threads=ref.max_threads())
+    assert rel_l2(y, exp) < TOL
