@@ -795,9 +795,12 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 //     workgroup barrier that precedes every weight load, so the x requests
 //     leave the CU first), convert it to limbs (er_xlimbs.h) and each bump an
 //     LDS counter;
-//   - every wave walks its rows with PD rows of weight loads in flight (row
-//     i + PD is issued after row i is consumed) and waits on the counter, not
-//     on a barrier, before its first dot product.
+//   - every wave walks its rows with D units of weight loads in flight (a
+//     unit is one slot of one row step: unit v + D is issued right after unit
+//     v is consumed) and waits on the counter, not on a barrier, before its
+//     first dot product.  Per-slot refills spread every wave's loads evenly
+//     over the launch, so the last data to arrive finds little compute
+//     behind it (rows of many slots gained most).
 // Row assignment: step i of lane group (wave, g) is row
 // rb + (i * ER_CU_WAVES + wave) * G + g, G = 64 / LPR rows per wave step.
 // Per-row arithmetic (slot order, lane reduction) is that of the family-1
@@ -807,7 +810,12 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 #define ER_CU_STAGERS 4               // waves ER_CU_WAVES - 4 .. ER_CU_WAVES - 1 stage x
 #endif
 #define ER_CU_SPIN_LIMIT (1u << 22)   // bound on the staging-counter wait (s_sleep 1 per poll)
-#define ER_CU_PD 2                    // rows of weight loads in flight per wave (2 measured best)
+// units of weight loads in flight per wave: 3 for the unrolled kernels (3
+// beat 2 and the former 2 whole rows), except two rows' worth for 4 slots per
+// lane (2, 3 and 4 units spill there, 8 does not); two rows' worth for the
+// rolled loop (whose body of ER_CU_UNROLL steps must hold a multiple of D
+// units).  tests/test_build_regs.py checks that no kernel spills.
+#define ER_CU_UNITS(NS, JC) ((JC) == 0 ? 2 * (NS) : (NS) == 4 ? 8 : 3)
 #ifndef ER_CU_UNROLL
 #define ER_CU_UNROLL 4                // unroll of the rolled step loop
 #endif
@@ -933,6 +941,7 @@ struct CuQ6K {
 // LDS bytes of the family: limbs, then K fp32 values of raw x.
 ER_DEV uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 
+// D: units (slot, row step) of weight loads in flight per wave.
 // JC > 0: exactly JC row steps per wave, fully unrolled (rowsPerWg = STEP * JC).
 // JC == 0: a runtime number of steps, at most 64 per lane group (rowsPerWg <=
 // STEP * 64), in a loop unrolled by ER_CU_UNROLL.  Either way every step is
@@ -945,7 +954,7 @@ ER_DEV uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 // merges their quads into the partial (pv, pi)[blockIdx.x] (rowsPerWg and M
 // multiples of 4, so no quad spans two workgroups; the dynamic LDS holds at
 // least 4 * rowsPerWg bytes).
-template <class F, int LPR, int NS, int PD, int JC, bool TOP1 = false>
+template <class F, int LPR, int NS, int D, int JC, bool TOP1 = false>
 ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
                     uint32_t M, uint32_t K, uint32_t rowsPerWg, float *__restrict__ pv = nullptr,
                     uint32_t *__restrict__ pi = nullptr) {
@@ -955,7 +964,9 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     constexpr uint32_t STEP = ER_CU_WAVES * G;  // rows per workgroup step
     constexpr int NPARK = JC > 0 ? (JC + LPR - 1) / LPR : 64 / LPR;
     constexpr int UNR = JC > 0 ? JC : ER_CU_UNROLL;
-    static_assert(UNR % PD == 0 || JC > 0, "the rolled loop's unroll is a multiple of PD");
+    constexpr int UPB = UNR * NS;                  // units (step, slot) per unrolled body
+    constexpr int D0 = D < UPB ? D : UPB;          // units issued before the first dot
+    static_assert(JC > 0 || UPB % D == 0, "the rolled body's unit count is a multiple of D");
     x += (size_t)blockIdx.y * K;
     y += (size_t)blockIdx.y * M;
     // wave index as a scalar: the staging branch and the step count are wave-uniform
@@ -971,12 +982,17 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     const size_t rowBytes = F::row_bytes(K);
     uint32_t *xraw = lds + xl_lds_bytes(K) / 4u;  // 16-byte aligned for K % 256 == 0
 
-    typename F::Wt wb[PD][NS];
-    auto issue = [&](uint32_t i, int b) {
+    typename F::Wt wb[D];
+    auto issue = [&](uint32_t i, int j, int b) {
         const uint32_t row = min(first + i * STEP, re - 1u);
-        const uint8_t *rp = W + (size_t)row * rowBytes;
+        wb[b] = F::load(W + (size_t)row * rowBytes, min(li + (uint32_t)LPR * j, S - 1u));
+    };
+    auto prologue = [&]() {
 #pragma unroll
-        for (int j = 0; j < NS; ++j) wb[b][j] = F::load(rp, min(li + (uint32_t)LPR * j, S - 1u));
+        for (int v = 0; v < D0; ++v) {
+            issue((uint32_t)(v / NS), v % NS, v);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     const uint32_t nPieces = K >> 8;               // 1 KB pieces of x
@@ -1004,22 +1020,12 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's limb stores have landed
         if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-#pragma unroll
-        for (int i = 0; i < PD && i < UNR; ++i) {
-            issue((uint32_t)i, i);
-            // rows leave in consumption order, so each step's wait covers its own row only
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        prologue();
     } else {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < PD && i < UNR; ++i) {
-            issue((uint32_t)i, i);
-            // rows leave in consumption order, so each step's wait covers its own row only
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        prologue();
     }
     __builtin_amdgcn_sched_barrier(0);
     // the staging waves always finish; the bound only keeps a wave from
@@ -1039,12 +1045,16 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     for (int q = 0; q < NPARK; ++q) res[q] = 0.0f;
     // step i (buffer u % PD): dot products, the refill of the buffer with step
     // i + PD when `prefetch`, the lane reduction, and the parking of the sum
-    auto step = [&](uint32_t i, int u, bool prefetch) {
+    // step i0 + u of a body starting at step i0: unit v = u * NS + j in buffer
+    // v % D, refilled after its dot with unit v + D when `last` is false or
+    // that unit lies inside the body
+    auto step = [&](uint32_t i0, int u, bool last) {
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
+            const int v = u * NS + j;
             if constexpr (NS == 1) {
-                acc = F::dot(wb[u % PD][0], xs0, acc, M0F);
+                acc = F::dot(wb[v % D], xs0, acc, M0F);
             } else {
                 // re-read per row: the opaque slot index keeps the compiler from
                 // hoisting NS slots of x limbs out of the row loop into registers
@@ -1052,14 +1062,14 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
                 uint32_t sx = min(sRaw, S - 1u);
                 asm volatile("" : "+v"(sx));
                 const typename F::Xs xs = F::xside(X, sx, sRaw < S ? 1.0f : 0.0f);
-                acc = F::dot(wb[u % PD][j], xs, acc, M0F);
-                __builtin_amdgcn_sched_barrier(0);  // one slot of x limbs live at a time
+                acc = F::dot(wb[v % D], xs, acc, M0F);
             }
+            __builtin_amdgcn_sched_barrier(0);  // one slot of x limbs live at a time
+            if (!last || v + D < UPB) issue(i0 + (uint32_t)((v + D) / NS), (v + D) % NS, v % D);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        if (prefetch) issue(i + PD, u % PD);
-        __builtin_amdgcn_sched_barrier(0);
         acc = group_sum<LPR>(acc);
+        const uint32_t i = i0 + (uint32_t)u;
         const bool mine = li == i % LPR;
         const uint32_t q0 = i / LPR;
 #pragma unroll
@@ -1069,11 +1079,11 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     if constexpr (JC == 0) {
         for (; i0 + UNR < JR; i0 += UNR) {
 #pragma unroll
-            for (int u = 0; u < UNR; ++u) step(i0 + (uint32_t)u, u, true);
+            for (int u = 0; u < UNR; ++u) step(i0, u, false);
         }
     }
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) step(i0 + (uint32_t)u, u, u + PD < UNR);
+    for (int u = 0; u < UNR; ++u) step(i0, u, true);
     if constexpr (TOP1) {
         __syncthreads();  // every wave is done with x: LDS now holds the row values
         float *tv = (float *)lds;
@@ -1474,7 +1484,7 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
                                                    const float *__restrict__ x,               \
                                                    float *__restrict__ y, uint32_t M, uint32_t K, \
                                                    uint32_t rowsPerWg) {                      \
-        gemv_cu<F, LPR, NS, ER_CU_PD, JC>(W, x, y, M, K, rowsPerWg);                          \
+        gemv_cu<F, LPR, NS, ER_CU_UNITS(NS, JC), JC>(W, x, y, M, K, rowsPerWg);               \
     }
 #define ER_CU_TOP1_J(fmt, F, LPR, NS, JC, tag)                                                     \
     extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                              \
@@ -1483,7 +1493,7 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
                                                         float *__restrict__ pv,                  \
                                                         uint32_t *__restrict__ pi, uint32_t M,   \
                                                         uint32_t K, uint32_t rowsPerWg) {        \
-        gemv_cu<F, LPR, NS, ER_CU_PD, JC, true>(W, x, nullptr, M, K, rowsPerWg, pv, pi);         \
+        gemv_cu<F, LPR, NS, ER_CU_UNITS(NS, JC), JC, true>(W, x, nullptr, M, K, rowsPerWg, pv, pi); \
     }
 #define ER_CU_STEPS_1(E, fmt, F, LPR, NS) E(fmt, F, LPR, NS, 1, 1)
 #define ER_CU_STEPS_2(E, fmt, F, LPR, NS) ER_CU_STEPS_1(E, fmt, F, LPR, NS) E(fmt, F, LPR, NS, 2, 2)
