@@ -595,15 +595,19 @@ ER_DEV void top1_wave_merge(float &v, uint32_t &i) {
     }
 }
 
-// Wave 0 of the workgroup: the quads of rows first + [0, 4 * nq), whose values
-// are tv[0 .. 4 * nq), merged into the partial (pv, pi)[blockIdx.x].
-ER_DEV void top1_partial(const float *tv, uint32_t first, uint32_t nq, float *__restrict__ pv,
+// Wave 0 of the workgroup: the quads of local rows [0, 4 * nq), whose values
+// are tv[0 .. 4 * nq) and whose global rows are rowOf(l) (consecutive within
+// a quad), merged into the partial (pv, pi)[blockIdx.x]; quads at rows >= M
+// are skipped.
+template <class RowOf>
+ER_DEV void top1_partial(const float *tv, uint32_t nq, uint32_t M, RowOf rowOf, float *__restrict__ pv,
                          uint32_t *__restrict__ pi) {
     if (threadIdx.x < 64u) {
         float bv = -__builtin_inff();
         uint32_t bi = 0;
         for (uint32_t q = threadIdx.x; q < nq; q += 64u) {
-            const uint32_t r0 = first + 4u * q;
+            const uint32_t r0 = rowOf(4u * q);
+            if (r0 >= M) continue;
             float v = tv[4u * q];
             uint32_t i = r0;
 #pragma unroll
@@ -634,7 +638,7 @@ ER_DEV void top1_epilogue(const float *acc, int R, uint32_t base, bool mine, uin
         for (int r = 0; r < R; ++r) tv[base + (uint32_t)r] = acc[r];
     __syncthreads();
     const uint32_t first = blockIdx.x * RPW;
-    top1_partial(tv, first, min(RPW, M - first) / 4u, pv, pi);
+    top1_partial(tv, min(RPW, M - first) / 4u, M, [&](uint32_t l) { return first + l; }, pv, pi);
 }
 
 // One workgroup of 256 lanes: merges `count` partials into out[0].
@@ -801,8 +805,10 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 //     first dot product.  Per-slot refills spread every wave's loads evenly
 //     over the launch, so the last data to arrive finds little compute
 //     behind it (rows of many slots gained most).
-// Row assignment: step i of lane group (wave, g) is row
-// rb + (i * ER_CU_WAVES + wave) * G + g, G = 64 / LPR rows per wave step.
+// Row assignment: step i of lane group (wave, g) in workgroup b is row
+// (i * gridDim.x + b) * STEP + wave * G + g, G = 64 / LPR rows per wave step,
+// STEP = ER_CU_WAVES * G rows per workgroup step: the workgroups' steps
+// interleave over the matrix.
 // Per-row arithmetic (slot order, lane reduction) is that of the family-1
 // kernel with the same LPR and NS.
 
@@ -951,9 +957,9 @@ ER_DEV uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 // weight loads are outstanding while rows are computed and each wait covers
 // exactly the loads it needs.
 // TOP1: instead of storing y, the workgroup's row values go to LDS and wave 0
-// merges their quads into the partial (pv, pi)[blockIdx.x] (rowsPerWg and M
-// multiples of 4, so no quad spans two workgroups; the dynamic LDS holds at
-// least 4 * rowsPerWg bytes).
+// merges their quads into the partial (pv, pi)[blockIdx.x] (M a multiple of
+// 4 and quads inside one step, so no quad spans two workgroups; the dynamic
+// LDS holds at least 4 * rowsPerWg bytes).
 template <class F, int LPR, int NS, int D, int JC, bool TOP1 = false>
 ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
                     uint32_t M, uint32_t K, uint32_t rowsPerWg, float *__restrict__ pv = nullptr,
@@ -973,18 +979,21 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t g = lane / LPR, li = lane % LPR;
     const uint32_t S = K >> 6, C16 = K >> 4;
-    const uint32_t rb = blockIdx.x * rowsPerWg, re = min(rb + rowsPerWg, M);  // rb < M (grid = ceil(M / rowsPerWg))
-    const uint32_t first = rb + wave * G + g;  // row of step 0; step i adds i * STEP
-    const uint32_t firstW = rb + wave * G;     // the wave's first lane group
-    // steps with a live row for this wave, and the steps computed
-    const uint32_t J = firstW < re ? (re - firstW + STEP - 1u) / STEP : 0u;
+    // Step i of this workgroup is global step i * gridDim.x + blockIdx.x, so at
+    // any moment the CUs read rows spread over the whole matrix rather than
+    // each its own contiguous block (contiguous blocks ran 5-7% slower: some
+    // CUs' ranges were served more slowly and ended the launch late).  The
+    // grid is ceil(M / rowsPerWg), so the global steps cover every row.
+    const uint32_t J = rowsPerWg / STEP;  // steps per workgroup (rows past M are skipped)
     const uint32_t JR = JC > 0 ? (uint32_t)JC : max((J + UNR - 1u) / UNR * UNR, (uint32_t)UNR);
+    const uint32_t laneRow = wave * G + g;  // row within a step
+    auto rowOf = [&](uint32_t i) { return (i * gridDim.x + blockIdx.x) * STEP + laneRow; };
     const size_t rowBytes = F::row_bytes(K);
     uint32_t *xraw = lds + xl_lds_bytes(K) / 4u;  // 16-byte aligned for K % 256 == 0
 
     typename F::Wt wb[D];
     auto issue = [&](uint32_t i, int j, int b) {
-        const uint32_t row = min(first + i * STEP, re - 1u);
+        const uint32_t row = min(rowOf(i), M - 1u);
         wb[b] = F::load(W + (size_t)row * rowBytes, min(li + (uint32_t)LPR * j, S - 1u));
     };
     auto prologue = [&]() {
@@ -1086,21 +1095,22 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     for (int u = 0; u < UNR; ++u) step(i0, u, true);
     if constexpr (TOP1) {
         __syncthreads();  // every wave is done with x: LDS now holds the row values
-        float *tv = (float *)lds;
+        float *tv = (float *)lds;  // local row i * STEP + laneRow of step i
 #pragma unroll
         for (int q = 0; q < NPARK; ++q) {
             const uint32_t st = (uint32_t)q * LPR + li;
-            const uint32_t row = first + st * STEP;
-            if (st < J && row < re) tv[row - rb] = res[q];
+            if (st < J) tv[st * STEP + laneRow] = res[q];
         }
         __syncthreads();
-        top1_partial(tv, rb, (re - rb) / 4u, pv, pi);
+        // quads never straddle steps (STEP % 4 == 0); those past M are skipped
+        top1_partial(tv, J * STEP / 4u, M, [&](uint32_t l) { return ((l / STEP) * gridDim.x + blockIdx.x) * STEP + l % STEP; },
+                     pv, pi);
     } else {
 #pragma unroll
         for (int q = 0; q < NPARK; ++q) {
             const uint32_t st = (uint32_t)q * LPR + li;
-            const uint32_t row = first + st * STEP;
-            if (st < J && row < re) y[row] = res[q];
+            const uint32_t row = rowOf(st);
+            if (st < J && row < M) y[row] = res[q];
         }
     }
 }
