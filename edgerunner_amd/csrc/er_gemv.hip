@@ -795,10 +795,14 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // dot product to the slowest weight-load issue of its workgroup.  Here one
 // 8-wave workgroup owns a CU-sized share of the rows (grid ~ one workgroup per
 // CU), and:
-//   - waves 4..7 copy x into LDS with global_load_lds (issued before a
+//   - staging waves copy x into LDS with global_load_lds (issued before a
 //     workgroup barrier that precedes every weight load, so the x requests
 //     leave the CU first), convert it to limbs (er_xlimbs.h) and each bump an
-//     LDS counter;
+//     LDS counter.  With one slot per lane, or 5 and more, all 8 waves stage
+//     and issue their first weight loads before converting (waiting only for
+//     their x pieces, which precede those loads in the in-order load count);
+//     with 2-4 slots per lane waves 4..7 stage and issue their weights after
+//     converting (each measured best for its case);
 //   - every wave walks its rows with D units of weight loads in flight (a
 //     unit is one slot of one row step: unit v + D is issued right after unit
 //     v is consumed) and waits on the counter, not on a barrier, before its
@@ -812,9 +816,6 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // Per-row arithmetic (slot order, lane reduction) is that of the family-1
 // kernel with the same LPR and NS.
 
-#ifndef ER_CU_STAGERS
-#define ER_CU_STAGERS 4               // waves ER_CU_WAVES - 4 .. ER_CU_WAVES - 1 stage x
-#endif
 #define ER_CU_SPIN_LIMIT (1u << 22)   // bound on the staging-counter wait (s_sleep 1 per poll)
 // units of weight loads in flight per wave: 3 for the unrolled kernels (3
 // beat 2 and the former 2 whole rows), except two rows' worth for 4 slots per
@@ -829,6 +830,7 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // Per-format slot access: weights of one slot (Wt), the x side of one slot
 // (Xs), and the slot's contribution.
 struct CuQ4K {
+    static constexpr int NLD = 3;  // load instructions per slot
     struct Wt {
         u32x4 h, qa, qb;
     };
@@ -860,6 +862,7 @@ struct CuQ4K {
 };
 
 struct CuQ8 {
+    static constexpr int NLD = 5;
     using Wt = Q8Slot;
     struct Xs {
         u32x4 xv[ER_XL_PLANES][4];
@@ -879,6 +882,7 @@ struct CuQ8 {
 // Q6_K, slot layout, loads and per-slot arithmetic of gemv_q6k_i8: one
 // 2-byte-aligned vector load per field (ld16_u2 / ld8_u2).
 struct CuQ6K {
+    static constexpr int NLD = 5;
     struct Wt {
         u32x4 a, b, h;  // ql (q1 / q3 nibbles), ql (q2 / q4), qh
         u32x2 s;        // scales sc[8h .. 8h + 8)
@@ -947,6 +951,9 @@ struct CuQ6K {
 // LDS bytes of the family: limbs, then K fp32 values of raw x.
 ER_DEV uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 
+// s_waitcnt immediate for vmcnt(n), n < 64, with the other counters unconstrained.
+constexpr uint16_t vmcnt_imm(int n) { return (uint16_t)((n & 15) | ((n >> 4) << 14) | 0x0070 | 0x0f00); }
+
 // D: units (slot, row step) of weight loads in flight per wave.
 // JC > 0: exactly JC row steps per wave, fully unrolled (rowsPerWg = STEP * JC).
 // JC == 0: a runtime number of steps, at most 64 per lane group (rowsPerWg <=
@@ -973,6 +980,11 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     constexpr int UPB = UNR * NS;                  // units (step, slot) per unrolled body
     constexpr int D0 = D < UPB ? D : UPB;          // units issued before the first dot
     static_assert(JC > 0 || UPB % D == 0, "the rolled body's unit count is a multiple of D");
+    // staging waves (see the family comment); with all waves staging, the
+    // first D0 units are issued before the conversion
+    constexpr uint32_t STG = (NS == 1 || NS >= 5) ? ER_CU_WAVES : 4u;
+    constexpr bool EARLY = STG == ER_CU_WAVES;
+    static_assert(D0 * F::NLD < 64, "the early weight loads fit the load counter");
     x += (size_t)blockIdx.y * K;
     y += (size_t)blockIdx.y * M;
     // wave index as a scalar: the staging branch and the step count are wave-uniform
@@ -1006,10 +1018,10 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
 
     const uint32_t nPieces = K >> 8;               // 1 KB pieces of x
     const uint32_t nBlocks = (nPieces + 3u) >> 2;  // 4 KB blocks: 64 chunks, one conversion pass
-    if (wave >= ER_CU_WAVES - ER_CU_STAGERS) {
-        const uint32_t si = wave - (ER_CU_WAVES - ER_CU_STAGERS);
+    if (wave >= ER_CU_WAVES - STG) {
+        const uint32_t si = wave - (ER_CU_WAVES - STG);
         if (si == 0 && lane == 0) staged = 0u;
-        for (uint32_t b = si; b < nBlocks; b += ER_CU_STAGERS)
+        for (uint32_t b = si; b < nBlocks; b += STG)
             for (uint32_t q = 4u * b; q < min(4u * b + 4u, nPieces); ++q)
                 __builtin_amdgcn_global_load_lds((const void *)(x + 256u * q + 4u * lane), (void *)(xraw + 256u * q),
                                                  16, 0, 0);
@@ -1017,9 +1029,16 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();  // x requests of the workgroup precede its weight requests
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's x pieces are in LDS
+        if constexpr (EARLY) {
+            prologue();
+            // the D0 * NLD weight loads just issued are younger than this
+            // wave's x pieces: once at most that many are outstanding, x is in LDS
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(D0 * F::NLD));
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's x pieces are in LDS
+        }
         __builtin_amdgcn_sched_barrier(0);
-        for (uint32_t b = si; b < nBlocks; b += ER_CU_STAGERS) {
+        for (uint32_t b = si; b < nBlocks; b += STG) {
             const uint32_t t = 64u * b + lane;  // 16-value chunk; lanes 4k..4k+3 hold one 64-group
             const uint32_t tc = min(t, C16 - 1u);
             float4 xr[4];
@@ -1029,7 +1048,7 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's limb stores have landed
         if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        prologue();
+        if constexpr (!EARLY) prologue();
     } else {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
@@ -1039,7 +1058,7 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     __builtin_amdgcn_sched_barrier(0);
     // the staging waves always finish; the bound only keeps a wave from
     // spinning forever should that ever fail
-    for (uint32_t n = 0; __hip_atomic_load(&staged, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < ER_CU_STAGERS &&
+    for (uint32_t n = 0; __hip_atomic_load(&staged, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < STG &&
                          n < ER_CU_SPIN_LIMIT;
          ++n)
         __builtin_amdgcn_s_sleep(1);
