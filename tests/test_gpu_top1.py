@@ -133,3 +133,59 @@ def test_top1_graph_replays(ctx, gemv):
         for b in (wb, xb, pv, pi, ob):
             b.free()
         s.destroy()
+
+
+def _top1_setup(ctx, gemv, M, K, seed, stream):
+    W = q6(M, K, seed)
+    x = synth.normal_f32(synth.seed(41, seed), K)
+    n = gemv.q6KTop1PartialCount(M)
+    bufs = (ctx.upload(W, stream), ctx.upload(x, stream), ctx.alloc(4 * n), ctx.alloc(4 * n), ctx.alloc(4))
+    return W, x, bufs
+
+
+def test_top1_concurrent_streams(ctx, gemv):
+    """Top-1 launches in flight on two streams at once, CU-resident and
+    lane-group kernels mixed: every index matches its own logits."""
+    shapes = [(151936, 1024), (8192, 1024), (20000, 3072), (4096, 4096)]
+    streams = [ctx.stream(), ctx.stream()]
+    cases = []
+    try:
+        for i, (M, K) in enumerate(shapes):
+            cases.append((M, K) + _top1_setup(ctx, gemv, M, K, i, streams[i % 2]))
+        for s in streams:
+            s.synchronize()
+        for rep in range(3):
+            for i, (M, K, W, x, (wb, xb, pv, pi, ob)) in enumerate(cases):
+                gemv.encodeQ6KWeightsPackedTop1(streams[i % 2], wb, xb, pv, pi, ob, M, K)
+        for s in streams:
+            s.synchronize()
+        for i, (M, K, W, x, (wb, xb, pv, pi, ob)) in enumerate(cases):
+            y = gemv.executeQ6KWeights(W, x, M, K)
+            assert int(ob.download(np.uint32, 1)[0]) == ref.top1(y), (M, K)
+    finally:
+        for c in cases:
+            for b in c[4]:
+                b.free()
+        for s in streams:
+            s.destroy()
+
+
+def test_top1_many_launches_share_partials(ctx, gemv):
+    """1100 top-1 launches back to back on one stream, all over the same
+    partial buffers and four index buffers: each launch's partials are
+    complete before the next launch overwrites them."""
+    M, K = 4096, 1024
+    s = ctx.stream()
+    W, x, (wb, xb, pv, pi, ob) = _top1_setup(ctx, gemv, M, K, 9, s)
+    outs = [ctx.alloc(4) for _ in range(4)]
+    try:
+        for i in range(1100):
+            gemv.encodeQ6KWeightsPackedTop1(s, wb, xb, pv, pi, outs[i % 4], M, K)
+        s.synchronize()
+        exp = ref.top1(gemv.executeQ6KWeights(W, x, M, K))
+        for o in outs:
+            assert int(o.download(np.uint32, 1, stream=s)[0]) == exp
+    finally:
+        for b in (wb, xb, pv, pi, ob, *outs):
+            b.free()
+        s.destroy()
