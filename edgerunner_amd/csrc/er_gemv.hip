@@ -1071,11 +1071,10 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     float res[NPARK];
 #pragma unroll
     for (int q = 0; q < NPARK; ++q) res[q] = 0.0f;
-    // step i (buffer u % PD): dot products, the refill of the buffer with step
-    // i + PD when `prefetch`, the lane reduction, and the parking of the sum
     // step i0 + u of a body starting at step i0: unit v = u * NS + j in buffer
     // v % D, refilled after its dot with unit v + D when `last` is false or
-    // that unit lies inside the body
+    // that unit lies inside the body; then the lane reduction and the parking
+    // of the row sum
     auto step = [&](uint32_t i0, int u, bool last) {
         float acc = 0.0f;
 #pragma unroll
