@@ -990,7 +990,7 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     // wave index as a scalar: the staging branch and the step count are wave-uniform
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t g = lane / LPR, li = lane % LPR;
-    const uint32_t S = K >> 6, C16 = K >> 4;
+    const uint32_t S = K >> 6;
     // Step i of this workgroup is global step i * gridDim.x + blockIdx.x, so at
     // any moment the CUs read rows spread over the whole matrix rather than
     // each its own contiguous block (contiguous blocks ran 5-7% slower: some
@@ -1016,13 +1016,19 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
         }
     };
 
-    const uint32_t nPieces = K >> 8;               // 1 KB pieces of x
-    const uint32_t nBlocks = (nPieces + 3u) >> 2;  // 4 KB blocks: 64 chunks, one conversion pass
+    // x is converted in blocks of one pass per wave: 4 KB (16 values per lane,
+    // xl_store_chunk) or 2 KB (8 per lane, xl_store_half; the same bytes).
+    // Half blocks when that spreads short rows over more waves, or long rows
+    // over all 8 (measured: K = 1024 -5%, 14336 -2%; K = 4096 and 8192 +2-4%).
+    const bool halfBlocks = K <= 2048u || (STG == ER_CU_WAVES && K > 8192u);
+    const uint32_t nPieces = K >> 8;                      // 1 KB pieces of x
+    const uint32_t perBlock = halfBlocks ? 2u : 4u;       // pieces per block
+    const uint32_t nBlocks = (nPieces + perBlock - 1u) / perBlock;
     if (wave >= ER_CU_WAVES - STG) {
         const uint32_t si = wave - (ER_CU_WAVES - STG);
         if (si == 0 && lane == 0) staged = 0u;
         for (uint32_t b = si; b < nBlocks; b += STG)
-            for (uint32_t q = 4u * b; q < min(4u * b + 4u, nPieces); ++q)
+            for (uint32_t q = perBlock * b; q < min(perBlock * b + perBlock, nPieces); ++q)
                 __builtin_amdgcn_global_load_lds((const void *)(x + 256u * q + 4u * lane), (void *)(xraw + 256u * q),
                                                  16, 0, 0);
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the counter reset has landed
@@ -1038,13 +1044,24 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
             __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's x pieces are in LDS
         }
         __builtin_amdgcn_sched_barrier(0);
-        for (uint32_t b = si; b < nBlocks; b += STG) {
-            const uint32_t t = 64u * b + lane;  // 16-value chunk; lanes 4k..4k+3 hold one 64-group
-            const uint32_t tc = min(t, C16 - 1u);
-            float4 xr[4];
+        if (halfBlocks) {
+            for (uint32_t b = si; b < nBlocks; b += STG) {
+                const uint32_t t = 64u * b + lane;  // 8-value half-chunk; lanes 8k..8k+7 hold one 64-group
+                const uint32_t tc = min(t, (K >> 3) - 1u);
+                float4 xr[2];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) xr[q] = *(const float4 *)(xraw + 16u * tc + 4u * q);
-            xl_store_chunk(lds, K, xr, t);  // stores only chunks t < C16
+                for (int q = 0; q < 2; ++q) xr[q] = *(const float4 *)(xraw + 8u * tc + 4u * q);
+                xl_store_half(lds, K, xr, t);  // stores only half-chunks t < K / 8
+            }
+        } else {
+            for (uint32_t b = si; b < nBlocks; b += STG) {
+                const uint32_t t = 64u * b + lane;  // 16-value chunk; lanes 4k..4k+3 hold one 64-group
+                const uint32_t tc = min(t, (K >> 4) - 1u);
+                float4 xr[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) xr[q] = *(const float4 *)(xraw + 16u * tc + 4u * q);
+                xl_store_chunk(lds, K, xr, t);  // stores only chunks t < K / 16
+            }
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's limb stores have landed
         if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);

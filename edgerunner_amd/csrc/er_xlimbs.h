@@ -20,7 +20,8 @@
 //
 // LDS layout (K a multiple of 64):
 //   [0, 3K)        planes 0..2: limb bytes l0, l1, l2; 16-byte granules swizzled by xl_gswz
-//   [3K, 3K+K/4)   x16[K/16]  fp32 sums of each 16-value chunk (exact fp32 x)
+//   [3K, 3K+K/4)   x16[K/16]  fp32 sums of each 16-value chunk (exact fp32 x),
+//                  summed as (x0 + .. + x7) + (x8 + .. + x15), each half in order
 //   then           sg64[K/64] the group scales s_g
 #pragma once
 
@@ -91,12 +92,18 @@ ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uin
         v[4 * q + 2] = xr[q].z;
         v[4 * q + 3] = xr[q].w;
     }
-    float mx = 0.0f, sm = 0.0f;
+    float mx = 0.0f, sa = 0.0f, sb = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
+    for (int q = 0; q < 8; ++q) {
         mx = fmaxf(mx, fabsf(v[q]));
-        sm += v[q];
+        sa += v[q];
     }
+#pragma unroll
+    for (int q = 8; q < 16; ++q) {
+        mx = fmaxf(mx, fabsf(v[q]));
+        sb += v[q];
+    }
+    const float sm = sa + sb;
     mx = dpp_max<ER_DPP_QUAD_XOR1>(mx);
     mx = dpp_max<ER_DPP_QUAD_XOR2>(mx);
     float sg, inv;
@@ -135,6 +142,57 @@ ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uin
                 u32x4{lb[l][0], lb[l][1], lb[l][2], lb[l][3]};
         x16[tRaw] = sm;
         if ((tRaw & 3u) == 0) sg64[tRaw >> 2] = sg;
+    }
+}
+
+// Converts one 8-value half-chunk (index hRaw: values 8 hRaw .. 8 hRaw + 7,
+// in xr) into LDS, giving the same bytes, chunk sums and scales as
+// xl_store_chunk.  The 8 half-chunks of a 64-group are held by 8 consecutive
+// lanes, which exchange their maxima (and pairs their half sums); every lane
+// of the wave must call this together.
+ER_DEV void xl_store_half(uint32_t *lds, uint32_t K, const float4 (&xr)[2], uint32_t hRaw) {
+    const uint32_t C8 = K >> 3;
+    const float v[8] = {xr[0].x, xr[0].y, xr[0].z, xr[0].w, xr[1].x, xr[1].y, xr[1].z, xr[1].w};
+    float mx = 0.0f, sh = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        mx = fmaxf(mx, fabsf(v[q]));
+        sh += v[q];
+    }
+    const float sm = dpp_add<ER_DPP_QUAD_XOR1>(sh);  // even lane: own half + the odd lane's
+    mx = dpp_max<ER_DPP_QUAD_XOR1>(mx);
+    mx = dpp_max<ER_DPP_QUAD_XOR2>(mx);
+    mx = dpp_max<ER_DPP_ROW_HALF_MIRROR>(mx);  // quads 2k and 2k+1 of each 8 lanes
+    float sg, inv;
+    xl_scale(mx, &sg, &inv);
+    uint32_t u[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) u[q] = __float_as_uint(__builtin_fmaf(v[q], inv, ER_XL_MAGIC));
+    uint32_t lb[ER_XL_PLANES][2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        const uint32_t a = u[4 * d], b = u[4 * d + 1], c = u[4 * d + 2], e = u[4 * d + 3];
+        const uint32_t d0 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(e, c, 0x0c0c0602u),
+                                                  __builtin_amdgcn_perm(b, a, 0x0c0c0602u), 0x05040100u);
+        const uint32_t d1 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(e, c, 0x0c0c0501u),
+                                                  __builtin_amdgcn_perm(b, a, 0x0c0c0501u), 0x05040100u);
+        const uint32_t d2 = __builtin_amdgcn_perm(__builtin_amdgcn_perm(e, c, 0x0c0c0400u),
+                                                  __builtin_amdgcn_perm(b, a, 0x0c0c0400u), 0x05040100u);
+        const uint32_t t = d0 ^ 0x40404040u;
+        lb[0][d] = t ^ ((t & 0x40404040u) << 1);
+        lb[1][d] = d1 ^ 0x80808080u;
+        lb[2][d] = d2 ^ 0x80808080u;
+    }
+    if (hRaw < C8) {
+        uint8_t *planes = (uint8_t *)lds;
+        float *x16 = (float *)(lds + (ER_XL_PLANES * K) / 4u);
+        float *sg64 = x16 + (K >> 4);
+        const uint32_t off = 16u * xl_gswz(hRaw >> 1) + 8u * (hRaw & 1u);
+#pragma unroll
+        for (int l = 0; l < ER_XL_PLANES; ++l)
+            *(u32x2 *)__builtin_assume_aligned(planes + (size_t)l * K + off, 8) = u32x2{lb[l][0], lb[l][1]};
+        if ((hRaw & 1u) == 0) x16[hRaw >> 1] = sm;
+        if ((hRaw & 7u) == 0) sg64[hRaw >> 3] = sg;
     }
 }
 
