@@ -586,13 +586,28 @@ ER_DEV void top1_merge(float &v, uint32_t &i, float ov, uint32_t oi) {
     }
 }
 
+// (v, i) merged with the pair of the lane that CTRL selects, on the rows of
+// ROWMASK (other rows merge with their own pair, which changes nothing).
+template <int CTRL, int ROWMASK = 0xf>
+ER_DEV void top1_dpp_merge(float &v, uint32_t &i) {
+    const int vb = __float_as_int(v);
+    const float ov = __int_as_float(__builtin_amdgcn_update_dpp(vb, vb, CTRL, ROWMASK, 0xf, false));
+    const uint32_t oi = (uint32_t)__builtin_amdgcn_update_dpp((int)i, (int)i, CTRL, ROWMASK, 0xf, false);
+    top1_merge(v, i, ov, oi);
+}
+
+// Merge over the 64 lanes of pairs that are never NaN (each started from
+// (-inf, 0) and takes no NaN), where the merge is order-independent: DPP
+// steps as in group_sum leave the result in lane 63, read back into all lanes.
 ER_DEV void top1_wave_merge(float &v, uint32_t &i) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(v, off, 64);
-        const uint32_t oi = (uint32_t)__shfl_xor((int)i, off, 64);
-        top1_merge(v, i, ov, oi);
-    }
+    top1_dpp_merge<ER_DPP_QUAD_XOR1>(v, i);
+    top1_dpp_merge<ER_DPP_QUAD_XOR2>(v, i);
+    top1_dpp_merge<ER_DPP_ROW_HALF_MIRROR>(v, i);
+    top1_dpp_merge<ER_DPP_ROW_MIRROR>(v, i);
+    top1_dpp_merge<ER_DPP_ROW_BCAST15, 0xa>(v, i);  // rows 1 and 3 hold the two half-wave results
+    top1_dpp_merge<ER_DPP_ROW_BCAST31, 0xc>(v, i);  // row 3 holds the total
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    i = (uint32_t)__builtin_amdgcn_readlane((int)i, 63);
 }
 
 // Wave 0 of the workgroup: the quads of local rows [0, 4 * nq), whose values
