@@ -11,7 +11,7 @@
 //
 // Mapping: 8 lanes per block, 4 values per lane (a 16-byte load when the
 // source rows are 16-byte aligned, else 4 scalar loads); the block maximum is
-// a 3-step butterfly inside the 8-lane group.  A block is 34 bytes, so
+// 3 DPP steps inside the 8-lane group.  A block is 34 bytes, so
 // destination blocks are only 2-byte aligned: each lane stores its 4 q bytes
 // as two 16-bit stores and lane 0 of the group stores d.  HBM-bound: 128
 // bytes read and 34 written per block.
@@ -23,8 +23,10 @@
 // 4 sub .. 4 sub + 3); writes the block at blk.
 ER_DEV void quantize_block(const float v[4], uint32_t sub, uint8_t *__restrict__ blk) {
     float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    // maximum over the 8 lanes of the block: DPP quad swaps, then the half-row mirror
+    m = dpp_max<ER_DPP_QUAD_XOR1>(m);
+    m = dpp_max<ER_DPP_QUAD_XOR2>(m);
+    m = dpp_max<ER_DPP_ROW_HALF_MIRROR>(m);
     const float scale = m > 0.0f ? m / 127.0f : 0.0f;
     uint32_t packed = 0;
 #pragma unroll
