@@ -13,7 +13,7 @@
 // source rows are 16-byte aligned, else 4 scalar loads); the block maximum is
 // 3 DPP steps inside the 8-lane group.  A block is 34 bytes, so
 // destination blocks are only 2-byte aligned: each lane stores its 4 q bytes
-// as two 16-bit stores and lane 0 of the group stores d.  HBM-bound: 128
+// as one 2-byte-aligned dword and lane 0 of the group stores d.  HBM-bound: 128
 // bytes read and 34 written per block.
 #include "er_common.h"
 
@@ -38,9 +38,9 @@ ER_DEV void quantize_block(const float v[4], uint32_t sub, uint8_t *__restrict__
         }
         packed |= ((uint32_t)q & 0xffu) << (8 * i);
     }
-    uint16_t *q16 = (uint16_t *)(blk + 2u + 4u * sub);
-    q16[0] = (uint16_t)packed;
-    q16[1] = (uint16_t)(packed >> 16);
+    // one 2-byte-aligned dword store (the global memory path's unaligned access mode)
+    typedef uint32_t u32_a2 __attribute__((aligned(2)));
+    *(u32_a2 *)(blk + 2u + 4u * sub) = packed;
     if (sub == 0) *(uint16_t *)blk = __builtin_bit_cast(uint16_t, (_Float16)scale);
 }
 
