@@ -832,12 +832,15 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // kernel with the same LPR and NS.
 
 #define ER_CU_SPIN_LIMIT (1u << 22)   // bound on the staging-counter wait (s_sleep 1 per poll)
-// units of weight loads in flight per wave: 3 for the unrolled kernels (3
-// beat 2 and the former 2 whole rows), except two rows' worth for 4 slots per
-// lane (2, 3 and 4 units spill there, 8 does not); two rows' worth for the
-// rolled loop (whose body of ER_CU_UNROLL steps must hold a multiple of D
-// units).  tests/test_build_regs.py checks that no kernel spills.
-#define ER_CU_UNITS(NS, JC) ((JC) == 0 ? 2 * (NS) : (NS) == 4 ? 8 : 3)
+// units of weight loads in flight per wave in the unrolled kernels: the
+// format's choice (F::UNITS: 3 for Q4_K slots of 48 bytes, which beat 2 and 4
+// and the former 2 whole rows; 2 for Q8_0 slots of 68), except 2 for 7-slot
+// rows (which then reach their x conversion sooner; 5 and 6 spill, 7 is
+// slower) and two rows' worth for 4 slots per lane (2, 3 and 4 units spill
+// there, 8 does not); two rows' worth for the rolled loop (whose body of
+// ER_CU_UNROLL steps must hold a multiple of D units).  tests/test_build_regs.py
+// checks that no kernel spills.
+#define ER_CU_UNITS(F, NS, JC) ((JC) == 0 ? 2 * (NS) : (NS) == 4 ? 8 : (NS) >= 7 ? 2 : F::UNITS)
 #ifndef ER_CU_UNROLL
 #define ER_CU_UNROLL 4                // unroll of the rolled step loop
 #endif
@@ -845,7 +848,8 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // Per-format slot access: weights of one slot (Wt), the x side of one slot
 // (Xs), and the slot's contribution.
 struct CuQ4K {
-    static constexpr int NLD = 3;  // load instructions per slot
+    static constexpr int NLD = 3;    // load instructions per slot
+    static constexpr int UNITS = 3;  // units in flight (ER_CU_UNITS)
     struct Wt {
         u32x4 h, qa, qb;
     };
@@ -878,6 +882,7 @@ struct CuQ4K {
 
 struct CuQ8 {
     static constexpr int NLD = 5;
+    static constexpr int UNITS = 2;
     using Wt = Q8Slot;
     struct Xs {
         u32x4 xv[ER_XL_PLANES][4];
@@ -898,6 +903,7 @@ struct CuQ8 {
 // 2-byte-aligned vector load per field (ld16_u2 / ld8_u2).
 struct CuQ6K {
     static constexpr int NLD = 5;
+    static constexpr int UNITS = 3;
     struct Wt {
         u32x4 a, b, h;  // ql (q1 / q3 nibbles), ql (q2 / q4), qh
         u32x2 s;        // scales sc[8h .. 8h + 8)
@@ -1544,7 +1550,7 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
                                                    const float *__restrict__ x,               \
                                                    float *__restrict__ y, uint32_t M, uint32_t K, \
                                                    uint32_t rowsPerWg) {                      \
-        gemv_cu<F, LPR, NS, ER_CU_UNITS(NS, JC), JC>(W, x, y, M, K, rowsPerWg);               \
+        gemv_cu<F, LPR, NS, ER_CU_UNITS(F, NS, JC), JC>(W, x, y, M, K, rowsPerWg);               \
     }
 #define ER_CU_TOP1_J(fmt, F, LPR, NS, JC, tag)                                                     \
     extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                              \
@@ -1553,7 +1559,7 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
                                                         float *__restrict__ pv,                  \
                                                         uint32_t *__restrict__ pi, uint32_t M,   \
                                                         uint32_t K, uint32_t rowsPerWg) {        \
-        gemv_cu<F, LPR, NS, ER_CU_UNITS(NS, JC), JC, true>(W, x, nullptr, M, K, rowsPerWg, pv, pi); \
+        gemv_cu<F, LPR, NS, ER_CU_UNITS(F, NS, JC), JC, true>(W, x, nullptr, M, K, rowsPerWg, pv, pi); \
     }
 #define ER_CU_STEPS_1(E, fmt, F, LPR, NS) E(fmt, F, LPR, NS, 1, 1)
 #define ER_CU_STEPS_2(E, fmt, F, LPR, NS) ER_CU_STEPS_1(E, fmt, F, LPR, NS) E(fmt, F, LPR, NS, 2, 2)
