@@ -411,7 +411,7 @@ extern "C" __global__ void __launch_bounds__(256) er_fill_zero(float4 *__restric
 // exactly one chunk.  Requires the split's chunk count NC % 4 == 0 (host);
 // a workgroup whose split breaks that returns before any barrier.
 // ---------------------------------------------------------------------------
-template <bool Q4K>
+template <bool Q4K, bool FENCE>
 ER_DEV void gemm_q_ws(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
                       uint32_t T, uint32_t N, uint32_t K, uint32_t SK) {
     constexpr int TT = 128, WT = TT / 2, AI = WT / 32, NST = 2, NB = 4;
@@ -489,6 +489,13 @@ ER_DEV void gemm_q_ws(const uint8_t *__restrict__ W, const uint16_t *__restrict_
                 store((c + 1u) % NST, cBeg + c + 1u, (B + 1) % NB);
                 load(cBeg + c + NB, B);
                 __syncthreads();
+                // Register arithmetic moves freely across s_barrier: without
+                // this fence the scheduler hoists the next steps' Q4_K header
+                // decoding into this one, and its vmcnt waits then cover loads
+                // issued one or two chunks ago instead of three (512x14336x4096:
+                // 103 -> 95 us).  Q8_0 runs faster unfenced (48 -> 45 us at
+                // 512x4096x4096), its waits staying three chunks deep.
+                if (FENCE) __builtin_amdgcn_sched_barrier(0);
             }
         }
     } else {
@@ -542,12 +549,12 @@ ER_DEV void gemm_q_ws(const uint8_t *__restrict__ W, const uint16_t *__restrict_
 extern "C" __global__ void __launch_bounds__(512)
     er_gemmw_q4k_t128(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
                       uint32_t T, uint32_t N, uint32_t K, uint32_t SK) {
-    gemm_q_ws<true>(W, X, Y, T, N, K, SK);
+    gemm_q_ws<true, true>(W, X, Y, T, N, K, SK);
 }
 extern "C" __global__ void __launch_bounds__(512)
     er_gemmw_q8_0_t128(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
                        uint32_t T, uint32_t N, uint32_t K, uint32_t SK) {
-    gemm_q_ws<false>(W, X, Y, T, N, K, SK);
+    gemm_q_ws<false, false>(W, X, Y, T, N, K, SK);
 }
 
 #define ER_GEMMP_ENTRY(fmt, q4k, tt)                                                             \
