@@ -447,9 +447,9 @@ def _read_csv(path: Path):
 
 
 def summarize(root: Path) -> str:
-    """Markdown summary of a rocprofv3 output tree made by the profiling
-    commands in DESIGN.md: kernel stats (stats/), FETCH_SIZE (fetch/) and
-    WRITE_SIZE (write/) counter runs of `--probe`."""
+    """Markdown summary of a rocprofv3 output tree holding three runs: kernel
+    stats of the bench workloads (stats/, `--kernel-trace --stats`), and the
+    FETCH_SIZE (fetch/) and WRITE_SIZE (write/) counter runs of `--probe`."""
     out = []
     stats = sorted(root.glob("stats/**/*kernel_stats.csv"))
     if stats:

@@ -1,5 +1,5 @@
-"""The decode-chain configuration has the shapes and byte
-count SURVEY derives: 28 Qwen3-0.6B layers + 151936-row head = 398,060,544
+"""The decode-chain configuration has the expected shapes
+and byte count: 28 Qwen3-0.6B layers + 151936-row head = 398,060,544
 weight bytes per step, 197 projection launches (113 with fused q/k/v and
 gate/up)."""
 from edgerunner_amd.chain import ChainSpec
