@@ -198,3 +198,42 @@ def test_default_dispatch_q6k_head_top1_consistent(gemv):
     assert gemv.executeQ6KWeightsTop1(W, x, M, K) == ref.top1(y)
     exp = ref.gemv("q6_k", W, x, M, K, threads=ref.max_threads())
     assert rel_l2(y, exp) < TOL
+
+
+@pytest.fixture(scope="module")
+def lane_group_gemv():
+    c = _context("0")
+    yield GEMVKernel(c)
+    c.close()
+
+
+# Every unrolled step count is its own compiled kernel.  (fmt, K, lanes per
+# row, step counts): K picks the configuration (the planner's choice at that
+# row length), M = CUs x rows per step x steps picks the kernel.
+STEP_SWEEP = [("q4_k", 1024, 16, (1, 2, 3, 5, 8)), ("q4_k", 2048, 32, (1, 2, 4, 7, 8)),
+              ("q4_k", 4096, 64, (1, 2, 3, 5, 6, 8)), ("q4_k", 8192, 64, (1, 2, 4, 8)),
+              ("q4_k", 12288, 64, (1, 2)), ("q4_k", 14336, 32, (1,)), ("q4_k", 16384, 64, (1, 2)),
+              ("q8_0", 1024, 16, (1, 3, 8)), ("q8_0", 2048, 32, (2, 5, 8)), ("q8_0", 4096, 64, (1, 4, 7)),
+              ("q6_k", 1024, 16, (2, 6, 8)), ("q6_k", 2048, 32, (1, 3, 8)), ("q6_k", 4096, 64, (1, 5, 8))]
+
+
+@pytest.mark.parametrize("fmt,K,lpr,steps", STEP_SWEEP)
+def test_cu_family_every_step_count(cu_gemv, lane_group_gemv, fmt, K, lpr, steps):
+    """Each unrolled step count of each configuration: 61 rows spread over
+    the matrix (first and last included) against the CPU oracle at the parity
+    bar, and every row against the lane-group family, which forms the same
+    22-bit x products and fp32 sums in another order."""
+    cus = cu_gemv.ctx.compute_units
+    step_rows = 8 * (64 // lpr)
+    x = synth.normal_f32(synth.seed(86, K % 89), K)
+    for j in steps:
+        M = cus * step_rows * j
+        W = synth.weights(fmt, synth.seed(86, 10 * j + K % 7), M, K, **DSCALE[fmt])
+        y = getattr(cu_gemv, EXEC[fmt])(W, x, M, K)
+        assert np.all(np.isfinite(y)), (fmt, K, j)
+        rows = np.unique(np.linspace(0, M - 1, 61).astype(np.int64))
+        Wr = W.reshape(M, -1)[rows].reshape(-1)
+        exp = ref.gemv(fmt, Wr, x, len(rows), K)
+        assert rel_l2(y[rows], exp) < TOL, (fmt, K, j)
+        lg = getattr(lane_group_gemv, EXEC[fmt])(W, x, M, K)
+        assert rel_l2(y, lg) < 1e-5, (fmt, K, j, rel_l2(y, lg))
