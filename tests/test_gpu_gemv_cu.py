@@ -237,3 +237,24 @@ def test_cu_family_every_step_count(cu_gemv, lane_group_gemv, fmt, K, lpr, steps
         assert rel_l2(y[rows], exp) < TOL, (fmt, K, j)
         lg = getattr(lane_group_gemv, EXEC[fmt])(W, x, M, K)
         assert rel_l2(y, lg) < 1e-5, (fmt, K, j, rel_l2(y, lg))
+
+
+@pytest.mark.parametrize("K,lpr,steps", [(1024, 16, (1, 2, 3, 5, 8)), (2048, 32, (1, 4, 7, 8)),
+                                         (4096, 64, (1, 2, 6, 8))])
+def test_cu_top1_every_step_count(cu_gemv, K, lpr, steps):
+    """Each unrolled step count of the top-1 kernels: the index equals the
+    selection rule applied to the same context's GEMV logits (the same
+    arithmetic), including a winner planted in the last row."""
+    cus = cu_gemv.ctx.compute_units
+    step_rows = 8 * (64 // lpr)
+    x = synth.normal_f32(synth.seed(88, K % 89), K)
+    for j in steps:
+        M = cus * step_rows * j
+        W = synth.weights("q6_k", synth.seed(88, 10 * j + K % 7), M, K, dscale=0.005)
+        y = cu_gemv.executeQ6KWeights(W, x, M, K)
+        assert cu_gemv.executeQ6KWeightsTop1(W, x, M, K) == ref.top1(y), (K, j)
+        Wl = W.reshape(M, -1).copy()
+        Wl[M - 1] = Wl[ref.top1(y)]
+        Wl = Wl.reshape(-1)
+        yl = cu_gemv.executeQ6KWeights(Wl, x, M, K)
+        assert cu_gemv.executeQ6KWeightsTop1(Wl, x, M, K) == ref.top1(yl), (K, j)
