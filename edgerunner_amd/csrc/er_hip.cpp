@@ -174,6 +174,7 @@ struct er_hip_ctx {
     hipFunction_t fnQ8Silu[kI8MultiCount] = {};
     int cu_count = 0;
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
+    int multi_override = -1;  // ER_HIP_GEMV_MULTI_CONFIG=lpr:ns:r for the multi-matrix kernels (tests, sweeps)
     int cu_mode = -1;      // ER_HIP_GEMV_CU: 0 never, 1 whenever it applies, unset: by shape
     int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1: non-pipelined GEMM, =2: 256-thread pipelined (comparisons)
     uint32_t gemm_tt = 0, gemm_sk = 0;  // ER_HIP_GEMM_TILE=tt:sk (benchmark sweeps only)
@@ -288,6 +289,13 @@ int pick_i8_multi(uint32_t S, uint32_t Mt, int cu) {
         }
     }
     return fallback;
+}
+
+// pick_i8_multi, or the context's forced configuration when it covers S slots.
+int pick_multi(const er_hip_ctx *ctx, uint32_t S, uint32_t Mt) {
+    const int o = ctx->multi_override;
+    if (o >= 0 && (uint32_t)kI8MultiCfg[o].lpr * kI8MultiCfg[o].ns >= S) return o;
+    return pick_i8_multi(S, Mt, ctx->cu_count);
 }
 
 // CU-resident configuration for S slots from cfg[0..count): the fewest idle
@@ -676,7 +684,7 @@ er_status encode_q4k_multi(er_hip_ctx *ctx, er_stream stream, const er_buffer *W
     if (Mt > 0xffffffffull) return fail(ER_ERR_INVALID_MATRIX_SHAPE, "Q4_K multi: too many rows");
     st = bind_device(ctx);
     if (st != ER_OK) return st;
-    const int ci = K <= kI8MaxK ? pick_i8_multi(K / 64u, (uint32_t)Mt, ctx->cu_count) : -1;
+    const int ci = K <= kI8MaxK ? pick_multi(ctx, K / 64u, (uint32_t)Mt) : -1;
     if (ci < 0) {
         for (int i = 0; i < count; ++i) {
             st = encode_gemv(ctx, stream, Fmt::Q4_K, Ws[i], x, ys[i], 1, Ms[i], K);
@@ -708,7 +716,7 @@ er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_b
     if (st != ER_OK) return st;
     st = check_ctx(ctx);
     if (st != ER_OK || M == 0) return st;
-    const int ci = K <= kI8MaxK ? pick_i8_multi(K / 64u, 2u * M, ctx->cu_count) : -1;
+    const int ci = K <= kI8MaxK ? pick_multi(ctx, K / 64u, 2u * M) : -1;
     if (ci < 0)
         return fail(ER_ERR_INVALID_VECTOR_SHAPE, "Q4_K dual GeGLU: K=%u exceeds the fused kernel's %u", K,
                     kI8MaxK);
@@ -790,7 +798,7 @@ er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     const uint32_t S = K / 64u;
-    const int ci = pick_i8_multi(S, (uint32_t)(f.silu ? 2u * Mt : Mt), ctx->cu_count);
+    const int ci = pick_multi(ctx, S, (uint32_t)(f.silu ? 2u * Mt : Mt));
     if (ci < 0) return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s: no configuration for K=%u", f.name, K);
     const I8Cfg &c = kI8MultiCfg[ci];
     const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
@@ -997,6 +1005,12 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
         }
     }
     if (const char *cv = std::getenv("ER_HIP_GEMV_CU")) ctx->cu_mode = std::atoi(cv) != 0 ? 1 : 0;
+    if (const char *mv = std::getenv("ER_HIP_GEMV_MULTI_CONFIG")) {
+        unsigned l = 0, n = 0, r = 0;
+        if (std::sscanf(mv, "%u:%u:%u", &l, &n, &r) == 3)
+            for (int i = 0; i < kI8MultiCount; ++i)
+                if (kI8MultiCfg[i].lpr == l && kI8MultiCfg[i].ns == n && kI8MultiCfg[i].r == r) ctx->multi_override = i;
+    }
     if (const char *ov = std::getenv("ER_HIP_GEMV_CONFIG")) {
         unsigned l = 0, n = 0, r = 0;
         if (std::sscanf(ov, "%u:%u:%u", &l, &n, &r) == 3)
