@@ -407,10 +407,12 @@ def load_traffic(name: str):
 COPY_CAL_BYTES = 64 << 20
 
 
-def probe(ctx, todo, steps: int) -> None:
+def probe(ctx, todo, steps: int, gemm_todo=()) -> None:
     """Counter-collection driver (run under `rocprofv3 --pmc ...`): three
     device-to-device copies of COPY_CAL_BYTES (the calibration kernel of known
-    traffic), then `steps` launches of each workload over rotating weights."""
+    traffic), then `steps` launches of each GEMV workload over rotating
+    weights, then `steps` eager launches of each GEMM workload in
+    `gemm_todo`."""
     import edgerunner_amd.synth as synth
     from edgerunner_amd import GEMVKernel
 
@@ -437,6 +439,20 @@ def probe(ctx, todo, steps: int) -> None:
             b.free()
         xb.free()
         yb.free()
+    if gemm_todo:
+        from edgerunner_amd import QuantGEMMKernel
+        gemm = QuantGEMMKernel(ctx)
+    for name, fmt, T, N, K, cfg in gemm_todo:
+        W = synth.weights(fmt, synth.seed(cfg, 0), N, K, **DSCALE[fmt])
+        X = synth.normal_bf16(synth.seed(cfg, 1), T * K)
+        wb, xb, yb = ctx.upload(W, stream), ctx.upload(X, stream), ctx.alloc(4 * T * N)
+        enc = gemm.encodeQ4K if fmt == "q4_k" else gemm.encodeQ8_0
+        for _ in range(steps):
+            enc(stream, wb, xb, yb, T, N, K)
+        stream.synchronize()
+        log(f"probe {name}: {steps} launches")
+        for b in (wb, xb, yb):
+            b.free()
     stream.destroy()
 
 
@@ -579,7 +595,9 @@ def main() -> int:
         if head not in todo:
             todo = [head] + todo
     if args.probe:
-        probe(ctx, todo, args.steps)
+        gemm_todo = [w for w in GEMM_WORKLOADS if args.workloads not in ("all", "headline")
+                     and w[0] in args.workloads.split(",")]
+        probe(ctx, todo, args.steps, gemm_todo)
         return 0
     results = {}
     for name, fmt, M, K, cfg in todo:
