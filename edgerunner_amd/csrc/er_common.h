@@ -27,6 +27,10 @@ ER_DEV float f16_to_f32(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
+// Lane index within the wave, computed afresh from the exec-mask counters
+// (no register has to stay live to provide it).
+ER_DEV uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
 // A constant materialised in a VGPR that the compiler treats as opaque, so
 // that masks reach VOP3 forms from a register instead of being split into
 // literal-carrying VOP2 pairs.

@@ -27,6 +27,7 @@
 // gridDim.y is the token count of the batched form: token t reads x + t*K and
 // writes y + t*M (the reference's grid-y = token layout).
 #include "er_gemv_cfg.h"
+#include "er_nonfinite.h"
 #include "er_xlimbs.h"
 
 #ifndef ER_Q4K_ROWS
@@ -128,9 +129,11 @@ ER_DEV float gelu_tanh(float g) {
 // Integer-dot Q4_K GEMV over the R rows (given by pointer) of this thread's
 // lane group; x is staged by the whole workgroup.  Every lane of the
 // workgroup must call it (it contains a barrier).
-template <int LPR, int NS, int R, int EPI>
+// rowAt(lane, r): row r of lane `lane`'s group, recomputed for the
+// non-finite path so that no row pointer stays live across the dot products.
+template <int LPR, int NS, int R, int EPI, class RowAt>
 ER_DEV void gemv_q4k_i8_core(const uint8_t *const (&rowp)[R], float *const (&yrow)[R], const bool (&rowLive)[R],
-                             const float *__restrict__ x, uint32_t K) {
+                             const float *__restrict__ x, uint32_t K, RowAt rowAt) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     using C = I8Cfg<LPR, NS>;
     constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
@@ -183,6 +186,20 @@ ER_DEV void gemv_q4k_i8_core(const uint8_t *const (&rowp)[R], float *const (&yro
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (nf_any_chunk(X.x16, K >> 4)) {
+        float sp[R], hits = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sp[r] = 0.0f;
+        const uint32_t ln = lane_id();
+        nf_terms<R>([&](int r, uint32_t k) { return q4k_weight_at(rowAt(ln, r), k); },
+                    [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, ln % LPR, LPR, sp, hits);
+        hits = group_sum<LPR>(hits);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = group_sum<LPR>(sp[r]);
+            acc[r] = hits > 0.0f ? v : acc[r];
+        }
+    }
     if (li == 0) {
         if (EPI == ER_EPI_GEGLU) {
 #pragma unroll
@@ -206,6 +223,11 @@ ER_DEV void gemv_q4k_i8(const uint8_t *__restrict__ W, const float *__restrict__
     const uint32_t g = lane / LPR;
     const size_t rowBytes = (size_t)(K >> 8) * 144u;
     const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+    const uint32_t waveS = __builtin_amdgcn_readfirstlane(wave);
+    auto rowAt = [=](uint32_t ln, int r) {
+        const uint32_t row = ((blockIdx.x * ER_GEMV_WAVES + waveS) * C::G + ln / LPR) * (uint32_t)R + (uint32_t)r;
+        return W + (size_t)min(row, M - 1u) * rowBytes;
+    };
     const uint8_t *rowp[R];
     float *yrow[R];
     bool live[R];
@@ -216,7 +238,7 @@ ER_DEV void gemv_q4k_i8(const uint8_t *__restrict__ W, const float *__restrict__
         yrow[r] = y + row;
         live[r] = row0 + (uint32_t)r < M;
     }
-    gemv_q4k_i8_core<LPR, NS, R, ER_EPI_STORE>(rowp, yrow, live, x, K);
+    gemv_q4k_i8_core<LPR, NS, R, ER_EPI_STORE>(rowp, yrow, live, x, K, rowAt);
 }
 
 // Several Q4_K matrices sharing one x and K (the reference's dual / triple
@@ -237,6 +259,20 @@ ER_DEV void gemv_q4k_i8_multi(const Q4Multi &mm, const float *__restrict__ x, ui
     const size_t rowBytes = (size_t)(K >> 8) * 144u;
     const uint32_t Mt = mm.M[0] + mm.M[1] + mm.M[2];
     const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+    const uint32_t waveS = __builtin_amdgcn_readfirstlane(wave);
+    auto rowAt = [&](uint32_t ln, int r) {
+        uint32_t v = min(((blockIdx.x * ER_GEMV_WAVES + waveS) * C::G + ln / LPR) * (uint32_t)R + (uint32_t)r, Mt - 1u);
+        const uint8_t *base = mm.W[0];
+        if (v >= mm.M[0]) {
+            v -= mm.M[0];
+            base = mm.W[1];
+            if (v >= mm.M[1]) {
+                v -= mm.M[1];
+                base = mm.W[2];
+            }
+        }
+        return base + (size_t)v * rowBytes;
+    };
     const uint8_t *rowp[R];
     float *yrow[R];
     bool live[R];
@@ -256,7 +292,7 @@ ER_DEV void gemv_q4k_i8_multi(const Q4Multi &mm, const float *__restrict__ x, ui
         yrow[r] = mm.y[m] + v;
         live[r] = row0 + (uint32_t)r < Mt;
     }
-    gemv_q4k_i8_core<LPR, NS, R, ER_EPI_STORE>(rowp, yrow, live, x, K);
+    gemv_q4k_i8_core<LPR, NS, R, ER_EPI_STORE>(rowp, yrow, live, x, K, rowAt);
 }
 
 // Fused gate/up GeGLU (q4_k_gemv_dual_geglu_f32, Dequant_Q4_K_M.metal:925-1022):
@@ -271,6 +307,12 @@ ER_DEV void gemv_q4k_i8_geglu(const uint8_t *__restrict__ Wg, const uint8_t *__r
     const uint32_t g = lane / LPR;
     const size_t rowBytes = (size_t)(K >> 8) * 144u;
     const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)(R / 2);
+    const uint32_t waveS = __builtin_amdgcn_readfirstlane(wave);
+    auto rowAt = [=](uint32_t ln, int r) {
+        const uint32_t row = ((blockIdx.x * ER_GEMV_WAVES + waveS) * C::G + ln / LPR) * (uint32_t)(R / 2) +
+                             (uint32_t)(r % (R / 2));
+        return (r < R / 2 ? Wg : Wu) + (size_t)min(row, M - 1u) * rowBytes;
+    };
     const uint8_t *rowp[R];
     float *yrow[R];
     bool live[R];
@@ -282,7 +324,7 @@ ER_DEV void gemv_q4k_i8_geglu(const uint8_t *__restrict__ Wg, const uint8_t *__r
         yrow[r] = yrow[R / 2 + r] = y + row;
         live[r] = live[R / 2 + r] = row0 + (uint32_t)r < M;
     }
-    gemv_q4k_i8_core<LPR, NS, R, ER_EPI_GEGLU>(rowp, yrow, live, x, K);
+    gemv_q4k_i8_core<LPR, NS, R, ER_EPI_GEGLU>(rowp, yrow, live, x, K, rowAt);
 }
 
 // Q8_0 with K % 64 == 0: slot s = blocks 2s, 2s+1 = row bytes [68s, 68s+68)
@@ -333,6 +375,7 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
     const uint32_t S = K >> 6;
     const size_t rowBytes = (size_t)S * 68u;
     const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+    const uint32_t waveS = __builtin_amdgcn_readfirstlane(wave);
 
     float4 xr[C::XG][4];
     xl_load<C::XG, NT>(x, K, xr);
@@ -369,6 +412,23 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (nf_any_chunk(X.x16, K >> 4)) {
+        float sp[R], hits = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sp[r] = 0.0f;
+        const uint32_t ln = lane_id();
+        const uint32_t fr0 = ((blockIdx.x * ER_GEMV_WAVES + waveS) * C::G + ln / LPR) * (uint32_t)R;
+        nf_terms<R>([&](int r, uint32_t k) {
+                        return q8_0_weight_at(W + (size_t)min(fr0 + (uint32_t)r, M - 1u) * rowBytes, k);
+                    },
+                    [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, ln % LPR, LPR, sp, hits);
+        hits = group_sum<LPR>(hits);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = group_sum<LPR>(sp[r]);
+            acc[r] = hits > 0.0f ? v : acc[r];
+        }
+    }
     if (li == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -393,11 +453,12 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
 
 ER_DEV float silu(float g) { return g / (1.0f + expf(-g)); }
 
-template <int LPR, int NS, int R, int EPI>
+// rowAt(lane, r): as in gemv_q4k_i8_core.
+template <int LPR, int NS, int R, int EPI, class RowAt>
 ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const (&yrow)[R],
                                     const bool (&rowLive)[R], const bool (&rowHalf)[R],
                                     const float *const (&rowRes)[R], const float *__restrict__ x,
-                                    const float *__restrict__ normW, float eps, uint32_t K) {
+                                    const float *__restrict__ normW, float eps, uint32_t K, RowAt rowAt) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     __shared__ float red[ER_GEMV_WAVES];
     using C = I8Cfg<LPR, NS>;
@@ -467,6 +528,30 @@ ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (nf_any_chunk(X.x16, C16)) {
+        // the staged values: x, or x * rms * normW as the prologue formed them
+        // (rms recomputed from the same wave sums, so it is the same value)
+        float rms = 1.0f;
+        if (normW) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < ER_GEMV_WAVES; ++k) ss += red[k];
+            rms = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
+        }
+        float sp[R], hits = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sp[r] = 0.0f;
+        const uint32_t ln = lane_id();
+        nf_terms<R>([&](int r, uint32_t k) { return q8_0_weight_at(rowAt(ln, r), k); },
+                    [&](uint32_t k) { return normW ? x[k] * rms * normW[k] : x[k]; }, X.x16, C16, ln % LPR, LPR,
+                    sp, hits);
+        hits = group_sum<LPR>(hits);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = group_sum<LPR>(sp[r]);
+            acc[r] = hits > 0.0f ? v : acc[r];
+        }
+    }
     if (li != 0) return;
     if constexpr (EPI == ER_EPI_Q8_SILU) {
 #pragma unroll
@@ -508,6 +593,20 @@ ER_DEV void gemv_q8_0_i8_multi(const Q8Multi &mm, const float *__restrict__ x, u
     const size_t rowBytes = (size_t)(K >> 6) * 68u;
     const uint32_t Mt = mm.M[0] + mm.M[1] + mm.M[2];
     const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+    const uint32_t waveS = __builtin_amdgcn_readfirstlane(wave);
+    auto rowAt = [&](uint32_t ln, int r) {
+        uint32_t v = min(((blockIdx.x * ER_GEMV_WAVES + waveS) * C::G + ln / LPR) * (uint32_t)R + (uint32_t)r, Mt - 1u);
+        const uint8_t *base = mm.W[0];
+        if (v >= mm.M[0]) {
+            v -= mm.M[0];
+            base = mm.W[1];
+            if (v >= mm.M[1]) {
+                v -= mm.M[1];
+                base = mm.W[2];
+            }
+        }
+        return base + (size_t)v * rowBytes;
+    };
     const uint8_t *rowp[R];
     void *yrow[R];
     bool live[R], half[R];
@@ -532,7 +631,7 @@ ER_DEV void gemv_q8_0_i8_multi(const Q8Multi &mm, const float *__restrict__ x, u
         live[r] = row0 + (uint32_t)r < Mt;
     }
     gemv_q8_0_i8_fused_core<LPR, NS, R, ER_EPI_Q8_ROWS>(rowp, yrow, live, half, res, x + (size_t)t * K,
-                                                         mm.normW, mm.eps, K);
+                                                         mm.normW, mm.eps, K, rowAt);
 }
 
 // Gate/up pairs: y[t M + i] = silu(gate_i . n) * (up_i . n), n = RMSNorm(x_t)
@@ -548,6 +647,12 @@ ER_DEV void gemv_q8_0_i8_silu(const uint8_t *__restrict__ Wg, const uint8_t *__r
     const uint32_t t = blockIdx.y;
     const size_t rowBytes = (size_t)(K >> 6) * 68u;
     const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)(R / 2);
+    const uint32_t waveS = __builtin_amdgcn_readfirstlane(wave);
+    auto rowAt = [=](uint32_t ln, int r) {
+        const uint32_t row = ((blockIdx.x * ER_GEMV_WAVES + waveS) * C::G + ln / LPR) * (uint32_t)(R / 2) +
+                             (uint32_t)(r % (R / 2));
+        return (r < R / 2 ? Wg : Wu) + (size_t)min(row, M - 1u) * rowBytes;
+    };
     const uint8_t *rowp[R];
     void *yrow[R];
     bool live[R], half[R];
@@ -563,7 +668,7 @@ ER_DEV void gemv_q8_0_i8_silu(const uint8_t *__restrict__ Wg, const uint8_t *__r
         res[r] = res[R / 2 + r] = nullptr;
     }
     gemv_q8_0_i8_fused_core<LPR, NS, R, ER_EPI_Q8_SILU>(rowp, yrow, live, half, res, x + (size_t)t * K,
-                                                         normW, eps, K);
+                                                         normW, eps, K, rowAt);
 }
 
 // ---------------------------------------------------------------------------
@@ -706,6 +811,7 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
     const uint32_t S = K >> 6;
     const size_t rowBytes = (size_t)(K >> 8) * 210u;
     const uint32_t row0 = ((blockIdx.x * ER_GEMV_WAVES + wave) * C::G + g) * (uint32_t)R;
+    const uint32_t waveS = __builtin_amdgcn_readfirstlane(wave);
 
     float4 xr[C::XG][4];
     xl_load<C::XG, NT>(x, K, xr);
@@ -790,6 +896,23 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (nf_any_chunk(X.x16, K >> 4)) {
+        float sp[R], hits = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sp[r] = 0.0f;
+        const uint32_t ln = lane_id();
+        const uint32_t fr0 = ((blockIdx.x * ER_GEMV_WAVES + waveS) * C::G + ln / LPR) * (uint32_t)R;
+        nf_terms<R>([&](int r, uint32_t k) {
+                        return q6k_weight_at(W + (size_t)min(fr0 + (uint32_t)r, M - 1u) * rowBytes, k);
+                    },
+                    [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, ln % LPR, LPR, sp, hits);
+        hits = group_sum<LPR>(hits);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = group_sum<LPR>(sp[r]);
+            acc[r] = hits > 0.0f ? v : acc[r];
+        }
+    }
     if constexpr (TOP1) {
         top1_epilogue<ER_GEMV_WAVES * C::G * R>(acc, R, (wave * C::G + g) * R, li == 0, M, pv, pi);
     } else if (li == 0) {
@@ -848,6 +971,7 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // Per-format slot access: weights of one slot (Wt), the x side of one slot
 // (Xs), and the slot's contribution.
 struct CuQ4K {
+    static constexpr int FMT = ER_FMT_Q4_K;
     static constexpr int NLD = 3;    // load instructions per slot
     static constexpr int UNITS = 3;  // units in flight (ER_CU_UNITS)
     struct Wt {
@@ -881,6 +1005,7 @@ struct CuQ4K {
 };
 
 struct CuQ8 {
+    static constexpr int FMT = ER_FMT_Q8_0;
     static constexpr int NLD = 5;
     static constexpr int UNITS = 2;
     using Wt = Q8Slot;
@@ -902,6 +1027,7 @@ struct CuQ8 {
 // Q6_K, slot layout, loads and per-slot arithmetic of gemv_q6k_i8: one
 // 2-byte-aligned vector load per field (ld16_u2 / ld8_u2).
 struct CuQ6K {
+    static constexpr int FMT = ER_FMT_Q6_K;
     static constexpr int NLD = 5;
     static constexpr int UNITS = 3;
     struct Wt {
@@ -1085,7 +1211,7 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
             }
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's limb stores have landed
-        if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         if constexpr (!EARLY) prologue();
     } else {
         __builtin_amdgcn_sched_barrier(0);
@@ -1095,11 +1221,13 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     }
     __builtin_amdgcn_sched_barrier(0);
     // the staging waves always finish; the bound only keeps a wave from
-    // spinning forever should that ever fail
-    for (uint32_t n = 0; __hip_atomic_load(&staged, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < STG &&
-                         n < ER_CU_SPIN_LIMIT;
-         ++n)
+    // spinning forever should that ever fail, and a wave whose wait ran out
+    // (computing on x that may not be staged) reports NaN for its rows
+    uint32_t spins = 0;
+    for (; __hip_atomic_load(&staged, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < STG && spins < ER_CU_SPIN_LIMIT;
+         ++spins)
         __builtin_amdgcn_s_sleep(1);
+    const bool stale = spins >= ER_CU_SPIN_LIMIT;
     __builtin_amdgcn_sched_barrier(0);
 
     const XLimbs X = xl_view(lds, K);
@@ -1149,6 +1277,25 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) step(i0, u, true);
+    if (nf_any_chunk(X.x16, K >> 4)) {
+        // each lane redoes its own parked rows over every chunk; raw x is in LDS
+        float sp[NPARK], hits = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NPARK; ++q) sp[q] = 0.0f;
+        const uint32_t ln = lane_id();
+        const uint32_t fRow = wave * G + ln / LPR, fli = ln % LPR;
+        nf_terms<NPARK>(
+            [&](int q, uint32_t k) {
+                const uint32_t st = (uint32_t)q * LPR + fli;
+                const uint32_t row = min((st * gridDim.x + blockIdx.x) * STEP + fRow, M - 1u);
+                return weight_at<F::FMT>(W + (size_t)row * rowBytes, k);
+            },
+            [&](uint32_t k) { return ((const float *)xraw)[k]; }, X.x16, K >> 4, 0u, 1u, sp, hits);
+#pragma unroll
+        for (int q = 0; q < NPARK; ++q) res[q] = hits > 0.0f ? sp[q] : res[q];
+    }
+#pragma unroll
+    for (int q = 0; q < NPARK; ++q) res[q] = stale ? __builtin_nanf("") : res[q];
     if constexpr (TOP1) {
         __syncthreads();  // every wave is done with x: LDS now holds the row values
         float *tv = (float *)lds;  // local row i * STEP + laneRow of step i
@@ -1285,6 +1432,19 @@ ER_DEV void gemv_q4k(const uint8_t *__restrict__ W, const float *__restrict__ x,
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (nf_any_value(xv, K)) {
+        float sp[R], hits = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sp[r] = 0.0f;
+        nf_terms<R>([&](int r, uint32_t k) { return q4k_weight_at(rowp[r], k); }, [&](uint32_t k) { return xv[k]; },
+                    nullptr, K >> 4, li, LPR, sp, hits);
+        hits = group_sum<LPR>(hits);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = group_sum<LPR>(sp[r]);
+            acc[r] = hits > 0.0f ? v : acc[r];
+        }
+    }
     if (li == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -1374,6 +1534,19 @@ ER_DEV void gemv_q6k(const uint8_t *__restrict__ W, const float *__restrict__ x,
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (nf_any_value(xv, K)) {
+        float sp[R], hits = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sp[r] = 0.0f;
+        nf_terms<R>([&](int r, uint32_t k) { return q6k_weight_at(rowp[r], k); }, [&](uint32_t k) { return xv[k]; },
+                    nullptr, K >> 4, li, LPR, sp, hits);
+        hits = group_sum<LPR>(hits);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = group_sum<LPR>(sp[r]);
+            acc[r] = hits > 0.0f ? v : acc[r];
+        }
+    }
     if (li == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -1454,6 +1627,19 @@ ER_DEV void gemv_q8_0(const uint8_t *__restrict__ W, const float *__restrict__ x
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    if (nf_any_value(xv, K)) {
+        float sp[R], hits = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) sp[r] = 0.0f;
+        nf_terms<R>([&](int r, uint32_t k) { return q8_0_weight_at(rowp[r], k); }, [&](uint32_t k) { return xv[k]; },
+                    nullptr, K >> 4, li, LPR, sp, hits);
+        hits = group_sum<LPR>(hits);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = group_sum<LPR>(sp[r]);
+            acc[r] = hits > 0.0f ? v : acc[r];
+        }
+    }
     if (li == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)

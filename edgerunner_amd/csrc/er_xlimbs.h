@@ -68,15 +68,19 @@ ER_DEV void xl_load(const float *__restrict__ x, uint32_t K, float4 (&xr)[XG][4]
 }
 
 // Power-of-two group scale for a group maximum mx >= 0: the smallest 2^e with
-// mx / 2^e <= ER_XL_QMAX (0 when mx == 0); inv = 1 / scale exactly.
+// mx / 2^e <= ER_XL_QMAX (0 when mx == 0); inv = 1 / scale exactly.  A group
+// holding an infinity (mx = inf) gets scale 0 like an all-zero one: its limbs
+// carry nothing, and the kernels evaluate non-finite activations apart
+// (er_nonfinite.h).
 ER_DEV void xl_scale(float mx, float *sg, float *inv) {
     const float v = mx * (1.0f / ER_XL_QMAX);
     uint32_t b = __float_as_uint(v);
     b = (b + 0x007fffffu) & 0xff800000u;  // round up to a power of two (v >= 0)
     if (mx > 0.0f && b == 0u) b = 0x00800000u;  // keep the scale normal
-    *sg = mx > 0.0f ? __uint_as_float(b) : 0.0f;
+    const bool live = mx > 0.0f && mx < __builtin_inff();
+    *sg = live ? __uint_as_float(b) : 0.0f;
     // 1/2^e = 2^-e: exponent field 254 - e_field (exact for normal scales)
-    *inv = mx > 0.0f ? __uint_as_float((254u - (b >> 23)) << 23) : 0.0f;
+    *inv = live ? __uint_as_float((254u - (b >> 23)) << 23) : 0.0f;
 }
 
 // Converts one 16-value chunk (index tRaw, values in xr) into LDS.  The 4
