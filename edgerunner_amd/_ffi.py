@@ -135,6 +135,8 @@ SIGNATURES = {
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
     "er_hip_encode_q6k_weights_packed_top1": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q6k_weights_packed_top1_noalloc": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
     "er_hip_quantize_q8_0_rows": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, _u32, _u32, _u32, _u32]),
     "er_hip_q8_0_fused_qkv": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer,

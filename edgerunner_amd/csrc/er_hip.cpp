@@ -11,6 +11,7 @@
 #include "er_hip.h"
 #include "er_error.h"
 #include "er_gemv_cfg.h"
+#include "er_scratch.h"
 
 #include <hip/hip_runtime_api.h>
 
@@ -179,8 +180,15 @@ struct er_hip_ctx {
     int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1: non-pipelined GEMM, =2: 256-thread pipelined (comparisons)
     uint32_t gemm_tt = 0, gemm_sk = 0;  // ER_HIP_GEMM_TILE=tt:sk (benchmark sweeps only)
     int gemv_fp32 = 0;  // ER_HIP_GEMV_FP32=1 selects the fp32 GEMV family (benchmark comparison)
+    // device address of this context's copy of the code object's er_scratch
+    // array (er_scratch.hip), found once at creation; the allocation-free
+    // entry points pass it to kernels in place of caller scratch buffers
+    void *scratch = nullptr;
     er_device_info info{};
 };
+
+static_assert(ER_HIP_TOP1_NOALLOC_MAX_ROWS / 4u <= ER_SCRATCH_TOP1_PARTIALS,
+              "the scratch array holds a partial for every 4 rows of the largest allocation-free head");
 
 namespace {
 
@@ -502,23 +510,26 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
 // epilogue (the CU-resident kernel when the plain GEMV over this matrix takes
 // that family, else the lane-group one, so both compute the same row values;
 // one partial per workgroup, at most M/4 of them) and er_top1_reduce.
-er_status encode_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buffer x,
-                          er_buffer pv, er_buffer pi, er_buffer out, uint32_t M, uint32_t K) {
+er_status validate_q6k_top1(er_buffer W, er_buffer x, er_buffer out, uint32_t M, uint32_t K) {
     if (M % 4u != 0)
         return fail(ER_ERR_INVALID_MATRIX_SHAPE, "Q6_K top-1: M=%u must be a multiple of 4", M);
     er_status st = validate_gemv_shape(Fmt::Q6_K, W, x.length, (uint64_t)M * 4u, 1, M, K);
     if (st != ER_OK) return st;
-    const uint64_t partials = M / 4u;
-    if (pv.length < partials * 4u || pi.length < partials * 4u || out.length < 4u)
-        return fail(ER_ERR_ENCODING_FAILED,
-                    "Q6_K top-1: partial buffers %llu / %llu B and index buffer %llu B too small for M=%u",
-                    (unsigned long long)pv.length, (unsigned long long)pi.length,
-                    (unsigned long long)out.length, M);
-    st = check_ctx(ctx);
+    if (out.length < 4u)
+        return fail(ER_ERR_ENCODING_FAILED, "Q6_K top-1: index buffer %llu B too small",
+                    (unsigned long long)out.length);
+    return ER_OK;
+}
+
+// The launches of a validated top-1 call, with the partials at pv / pi
+// (room for M/4 entries each).
+er_status launch_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buffer x, void *pv, void *pi,
+                          er_buffer out, uint32_t M, uint32_t K) {
+    er_status st = check_ctx(ctx);
     if (st != ER_OK) return st;
-    if (!W.data || !x.data || !pv.data || !pi.data || !out.data)
+    if (!W.data || !x.data || !pv || !pi || !out.data)
         return fail(ER_ERR_INVALID_ARGUMENT, "Q6_K top-1: null buffer");
-    if (!aligned(W.data, 16) || !aligned(x.data, 16) || !aligned(pv.data, 4) || !aligned(pi.data, 4) ||
+    if (!aligned(W.data, 16) || !aligned(x.data, 16) || !aligned(pv, 4) || !aligned(pi, 4) ||
         !aligned(out.data, 4))
         return fail(ER_ERR_INVALID_ARGUMENT,
                     "Q6_K top-1: weight and input must be 16-byte, partial and index buffers 4-byte aligned");
@@ -534,7 +545,7 @@ er_status encode_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buf
         // row values of a workgroup reuse its x area of LDS
         count = (M + cp.rowsPerWg - 1u) / cp.rowsPerWg;
         const uint32_t ldsTop1 = std::max<uint32_t>(cu_lds_bytes(K), 4u * cp.rowsPerWg);
-        void *args[] = {&W.data, &x.data, &pv.data, &pi.data, &M, &K, (void *)&cp.rowsPerWg};
+        void *args[] = {&W.data, &x.data, &pv, &pi, &M, &K, (void *)&cp.rowsPerWg};
         st = launch_fn(ctx->fnQ6KTop1Cu[cp.ci][cp.slot], "er_gemv_q6k_top1_cu", dim3(count, 1, 1),
                        dim3(64u * ER_CU_WAVES, 1, 1), ldsTop1, stream, args);
         if (st != ER_OK) return st;
@@ -547,13 +558,43 @@ er_status encode_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buf
         const I8Cfg &c = kI8Cfg[ci];
         const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
         count = (M + rowsPerBlock - 1) / rowsPerBlock;
-        void *args[] = {&W.data, &x.data, &pv.data, &pi.data, &M, &K};
+        void *args[] = {&W.data, &x.data, &pv, &pi, &M, &K};
         st = launch_fn(ctx->fnQ6KTop1[ci], "er_gemv_q6k_top1", dim3(count, 1, 1), dim3(kGemvThreads, 1, 1),
                        lds, stream, args);
         if (st != ER_OK) return st;
     }
-    void *rargs[] = {&pv.data, &pi.data, &out.data, &count};
+    void *rargs[] = {&pv, &pi, &out.data, &count};
     return launch(ctx, K_TOP1_REDUCE, dim3(1, 1, 1), dim3(256, 1, 1), 0, stream, rargs);
+}
+
+er_status encode_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buffer x,
+                          er_buffer pv, er_buffer pi, er_buffer out, uint32_t M, uint32_t K) {
+    er_status st = validate_q6k_top1(W, x, out, M, K);
+    if (st != ER_OK) return st;
+    const uint64_t partials = M / 4u;
+    if (pv.length < partials * 4u || pi.length < partials * 4u)
+        return fail(ER_ERR_ENCODING_FAILED,
+                    "Q6_K top-1: partial buffers %llu / %llu B too small for M=%u",
+                    (unsigned long long)pv.length, (unsigned long long)pi.length, M);
+    return launch_q6k_top1(ctx, stream, W, x, pv.data, pi.data, out, M, K);
+}
+
+// The same top-1 with its partials in this context's scratch array: no
+// caller buffers, no allocation.  Heads of more than
+// ER_HIP_TOP1_NOALLOC_MAX_ROWS rows exceed the array (INVALID_MATRIX_SHAPE,
+// checked before anything touches the device).
+er_status encode_q6k_top1_noalloc(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buffer x, er_buffer out,
+                                  uint32_t M, uint32_t K) {
+    er_status st = validate_q6k_top1(W, x, out, M, K);
+    if (st != ER_OK) return st;
+    if (M > ER_HIP_TOP1_NOALLOC_MAX_ROWS)
+        return fail(ER_ERR_INVALID_MATRIX_SHAPE,
+                    "Q6_K top-1 without caller scratch: M=%u exceeds the %u rows its scratch array serves", M,
+                    (unsigned)ER_HIP_TOP1_NOALLOC_MAX_ROWS);
+    st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    uint8_t *base = (uint8_t *)ctx->scratch;
+    return launch_q6k_top1(ctx, stream, W, x, base, base + 4u * ER_SCRATCH_TOP1_PARTIALS, out, M, K);
 }
 
 // Q8_0 row quantizer (quantize_q8_0_rows, Dequant_Q8_0.metal:19-49, encoded
@@ -919,6 +960,19 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
         delete ctx;
         return fail(ER_ERR_LIBRARY_NOT_FOUND, "hipModuleLoadData(gfx950 code object, %zu bytes): %s",
                     (size_t)(er_kernels_blob_end - er_kernels_blob), hipGetErrorString(e));
+    }
+    {
+        // this device's copy of the scratch array, found once with the device current
+        hipDeviceptr_t sp = nullptr;
+        size_t sb = 0;
+        e = hipModuleGetGlobal(&sp, &sb, ctx->module, "er_scratch");
+        if (e != hipSuccess || sp == nullptr || sb < ER_SCRATCH_BYTES) {
+            (void)hipModuleUnload(ctx->module);
+            delete ctx;
+            return fail(ER_ERR_FUNCTION_NOT_FOUND, "hipModuleGetGlobal(er_scratch): %s (%zu bytes)",
+                        hipGetErrorString(e), sb);
+        }
+        ctx->scratch = (void *)sp;
     }
     for (int i = 0; i < K_COUNT; ++i) {
         e = hipModuleGetFunction(&ctx->fn[i], ctx->module, kKernelNames[i]);
@@ -1313,6 +1367,12 @@ er_status er_hip_encode_q6k_weights_packed_top1(er_hip_ctx *ctx, er_stream strea
                                                 er_buffer partial_indices, er_buffer output_index,
                                                 uint32_t M, uint32_t K) {
     return encode_q6k_top1(ctx, stream, weight, input, partial_values, partial_indices, output_index, M, K);
+}
+
+er_status er_hip_encode_q6k_weights_packed_top1_noalloc(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                                        er_buffer input, er_buffer output_index, uint32_t M,
+                                                        uint32_t K) {
+    return encode_q6k_top1_noalloc(ctx, stream, weight, input, output_index, M, K);
 }
 
 er_status er_hip_quantize_q8_0_rows(er_hip_ctx *ctx, er_stream stream, er_buffer source,

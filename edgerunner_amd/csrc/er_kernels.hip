@@ -5,3 +5,4 @@
 #include "er_gemv.hip"
 #include "er_gemm.hip"
 #include "er_quant.hip"
+#include "er_scratch.hip"

@@ -228,6 +228,22 @@ er_status er_hip_encode_q6k_weights_packed_top1(er_hip_ctx *ctx, er_stream strea
                                                 er_buffer partial_indices, er_buffer output_index,
                                                 uint32_t M, uint32_t K);
 
+/* ---- allocation-free greedy top-1 ----
+ * No counterpart in the reference.  For callers that cannot allocate or pass
+ * scratch memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc): er_hip_encode_q6k_weights_packed_top1 without the two partial
+ * buffers.  The partials go to a device array inside the library's code
+ * object (512 KiB, one per context, held until the context is destroyed),
+ * so the call allocates nothing.  Same rules, kernels and result as
+ * er_hip_encode_q6k_weights_packed_top1, plus M <= ER_HIP_TOP1_NOALLOC_MAX_ROWS
+ * (else INVALID_MATRIX_SHAPE).  Every call through one context shares that
+ * array: calls on one context that overlap in time (concurrent streams)
+ * race on it and must be ordered by the caller. */
+#define ER_HIP_TOP1_NOALLOC_MAX_ROWS 262144u
+er_status er_hip_encode_q6k_weights_packed_top1_noalloc(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                                        er_buffer input, er_buffer output_index, uint32_t M,
+                                                        uint32_t K);
+
 /* ---- Q8_0 row quantizer ----
  * Kernel quantize_q8_0_rows with ERQuantizeQ8RowsParams{rowCount,
  * sourceRowStride, destinationRowBase, blocksPerRow} (Dequant_Q8_0.metal:9-49),

@@ -105,3 +105,14 @@ def test_projection_rejects_unsupported_type():
     t.data_type = 12
     t.ndim = 3
     assert lib.er_hip_encode_projection(None, None, C.byref(t), _buf(1024), _buf(16), 1) == 4
+
+
+def test_top1_noalloc_validation_without_device():
+    lib = _ffi.load()
+    f = lib.er_hip_encode_q6k_weights_packed_top1_noalloc
+    K = 256
+    for M, want in ((1024, 8), (1022, 4), (262144, 8), (262148, 4)):
+        # valid shapes reach the null-context check; M % 4 != 0 and heads
+        # past ER_HIP_TOP1_NOALLOC_MAX_ROWS fail before it
+        assert f(None, None, _buf(M * 210), _buf(4 * K), _buf(4), M, K) == want, M
+    assert f(None, None, _buf(1024 * 210), _buf(4 * K), _buf(3), 1024, K) == 3
