@@ -1210,8 +1210,11 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
                 xl_store_chunk(lds, K, xr, t);  // stores only chunks t < K / 16
             }
         }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's limb stores have landed
-        if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        // publish this wave's limb stores: a release fence on LDS alone (it waits
+        // for the LDS stores, lgkmcnt(0), not for the weight loads in flight,
+        // which a release on every address space would drain first)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if constexpr (!EARLY) prologue();
     } else {
         __builtin_amdgcn_sched_barrier(0);
