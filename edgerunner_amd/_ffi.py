@@ -135,6 +135,28 @@ SIGNATURES = {
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
     "er_hip_encode_q6k_weights_packed_top1": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q4k_weights_packed": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q4k_weights_packed_four_rows": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q4k_weights_llama_style": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q4k_weights_two_rows": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q6k_weights_packed": (C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q4k_weights_llama_style_dual": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer, _u32, _u32]),
+    "er_hip_encode_q4k_weights_triple_packed": (
+        C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer, er_buffer,
+                  er_buffer, _u32, _u32, _u32, _u32]),
+    "er_hip_execute_q4k_weights": (
+        C.c_int, [_ctx_p, C.c_void_p, _u64, C.c_void_p, _u64, C.c_void_p, _u64, _u32, _u32]),
+    "er_hip_execute_q6k_weights": (
+        C.c_int, [_ctx_p, C.c_void_p, _u64, C.c_void_p, _u64, C.c_void_p, _u64, _u32, _u32]),
+    "er_hip_execute_q4k_weights_with_weight_buffer": (
+        C.c_int, [_ctx_p, er_buffer, C.c_void_p, _u64, C.c_void_p, _u64, _u32, _u32]),
+    "er_hip_execute_q6k_weights_with_weight_buffer": (
+        C.c_int, [_ctx_p, er_buffer, C.c_void_p, _u64, C.c_void_p, _u64, _u32, _u32]),
+    "er_hip_execute_batched_q4k_weights": (
+        C.c_int, [_ctx_p, C.c_void_p, _u64, C.c_void_p, _u64, C.c_void_p, _u64, _u32, _u32, _u32]),
     "er_hip_encode_q6k_weights_packed_top1_noalloc": (
         C.c_int, [_ctx_p, _stream, er_buffer, er_buffer, er_buffer, _u32, _u32]),
     "er_hip_quantize_q8_0_rows": (
@@ -179,6 +201,9 @@ SIGNATURES = {
     "er_hip_gguf_upload": (C.c_int, [_ctx_p, _stream, C.c_void_p, C.POINTER(er_buffer)]),
     "er_gguf_tensor_storage": (C.c_int, [C.c_void_p, C.c_uint64, er_buffer,
                                          C.POINTER(er_tensor_storage)]),
+    "er_hip_probe_stream_read": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, _u32, er_buffer]),
+    "er_hip_probe_empty": (C.c_int, [_ctx_p, _stream]),
+    "er_hip_probe_grid_barrier": (C.c_int, [_ctx_p, _stream, _u32, _u32, _u32, er_buffer, er_buffer]),
     "er_hip_encode_projection": (
         C.c_int, [_ctx_p, _stream, C.POINTER(er_tensor_storage), er_buffer, er_buffer, _u32]),
 }

@@ -9,6 +9,7 @@
 // (Sources/EdgeRunnerMetal/GEMVKernel.swift:1276-1300, 1415-1432) and the
 // Dequant*Kernel.dequantise checks (Sources/EdgeRunnerIO/DequantQ4KMKernel.swift:23-29).
 #include "er_hip.h"
+#include "er_hip_probe.h"
 #include "er_error.h"
 #include "er_gemv_cfg.h"
 #include "er_scratch.h"
@@ -78,7 +79,10 @@ using er_detail::fail;
     X(GEMMP_Q8_0_T128, "er_gemmp_q8_0_t128")                                           \
     X(GEMMP_Q8_0_T256, "er_gemmp_q8_0_t256")                                           \
     X(GEMMW_Q4K_T128, "er_gemmw_q4k_t128")                                             \
-    X(GEMMW_Q8_0_T128, "er_gemmw_q8_0_t128")
+    X(GEMMW_Q8_0_T128, "er_gemmw_q8_0_t128")                                           \
+    X(PROBE_STREAM_READ, "er_probe_stream_read")                                       \
+    X(PROBE_EMPTY, "er_probe_empty")                                                   \
+    X(PROBE_GRID_BARRIER, "er_probe_grid_barrier")
 
 enum KernelId {
 #define ER_ENUM(id, name) K_##id,
@@ -501,6 +505,80 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / lpr) * kQ6KRows;
     dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
     return launch(ctx, k, grid, dim3(kGemvThreads, 1, 1), lds, stream, args);
+}
+
+// GEMVKernel.execute* (GEMVKernel.swift:545-627, 1146-1162, 1363-1413): the
+// reference's validation, then device x / y, one encode on the device's null
+// stream, a wait and the copy-out.  Host-side allocation or copy failures are
+// encodingFailed, as the reference's failed makeBuffer.
+er_status execute_gemv(er_hip_ctx *ctx, Fmt f, er_buffer W, const float *x, uint64_t xCount, float *y,
+                       uint64_t yCount, uint32_t batch, bool batched, uint32_t M, uint32_t K) {
+    if (batched ? (batch == 0 || xCount != (uint64_t)batch * K) : xCount != K)
+        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s execute: x.count %llu does not match K=%u x batch %u",
+                    fmt_name(f), (unsigned long long)xCount, K, batch);
+    const uint64_t yNeed = (uint64_t)batch * M;
+    er_status st = validate_gemv_shape(f, W, xCount * 4u, yNeed * 4u, batch, M, K);
+    if (st != ER_OK) return st;
+    if (yCount < yNeed)
+        return fail(ER_ERR_ENCODING_FAILED, "%s execute: y holds %llu floats, %llu needed", fmt_name(f),
+                    (unsigned long long)yCount, (unsigned long long)yNeed);
+    st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!x || !y) return fail(ER_ERR_INVALID_ARGUMENT, "%s execute: null host array", fmt_name(f));
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    void *dx = nullptr, *dy = nullptr;
+    const size_t xb = (size_t)xCount * 4u, yb = std::max<size_t>(4u, (size_t)yNeed * 4u);
+    if (hipMalloc(&dx, std::max<size_t>(xb, 16u)) != hipSuccess || hipMalloc(&dy, yb) != hipSuccess) {
+        if (dx) (void)hipFree(dx);
+        return fail(ER_ERR_ENCODING_FAILED, "%s execute: device allocation of x / y failed", fmt_name(f));
+    }
+    hipError_t e = hipMemcpy(dx, x, xb, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        st = encode_gemv(ctx, nullptr, f, W, er_buffer{dx, xb}, er_buffer{dy, yb}, batch, M, K);
+        if (st == ER_OK) {
+            e = hipStreamSynchronize(nullptr);
+            if (e == hipSuccess) e = hipMemcpy(y, dy, (size_t)yNeed * 4u, hipMemcpyDeviceToHost);
+        }
+    }
+    (void)hipFree(dx);
+    (void)hipFree(dy);
+    if (st != ER_OK) return st;
+    if (e != hipSuccess) return fail(ER_ERR_DEVICE, "%s execute: %s", fmt_name(f), hipGetErrorString(e));
+    return ER_OK;
+}
+
+// The host-weight forms: the weights are validated as a buffer of raw_bytes,
+// then copied to device memory for the call.
+er_status execute_gemv_host(er_hip_ctx *ctx, Fmt f, const void *raw, uint64_t rawBytes, const float *x,
+                            uint64_t xCount, float *y, uint64_t yCount, uint32_t batch, bool batched, uint32_t M,
+                            uint32_t K) {
+    if (batched ? (batch == 0 || xCount != (uint64_t)batch * K) : xCount != K)
+        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s execute: x.count %llu does not match K=%u x batch %u",
+                    fmt_name(f), (unsigned long long)xCount, K, batch);
+    er_status st = validate_gemv_shape(f, er_buffer{nullptr, rawBytes}, xCount * 4u, (uint64_t)batch * M * 4u, batch,
+                                       M, K);
+    if (st != ER_OK) return st;
+    if (yCount < (uint64_t)batch * M)
+        return fail(ER_ERR_ENCODING_FAILED, "%s execute: y holds %llu floats, %llu needed", fmt_name(f),
+                    (unsigned long long)yCount, (unsigned long long)batch * M);
+    st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (!raw) return fail(ER_ERR_INVALID_ARGUMENT, "%s execute: null weights", fmt_name(f));
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    void *dw = nullptr;
+    if (hipMalloc(&dw, std::max<uint64_t>(rawBytes, 16u)) != hipSuccess)
+        return fail(ER_ERR_ENCODING_FAILED, "%s execute: device allocation of %llu weight bytes failed", fmt_name(f),
+                    (unsigned long long)rawBytes);
+    hipError_t e = hipMemcpy(dw, raw, (size_t)rawBytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(dw);
+        return fail(ER_ERR_DEVICE, "%s execute: weight upload: %s", fmt_name(f), hipGetErrorString(e));
+    }
+    st = execute_gemv(ctx, f, er_buffer{dw, rawBytes}, x, xCount, y, yCount, batch, batched, M, K);
+    (void)hipFree(dw);
+    return st;
 }
 
 // Greedy top-1 over a Q6_K head (GEMVKernel.encodeQ6KWeightsPackedTop1,
@@ -1337,6 +1415,73 @@ er_status er_hip_encode_q8_0_weights(er_hip_ctx *ctx, er_stream stream, er_buffe
     return encode_gemv(ctx, stream, Fmt::Q8_0, weight, input, output, 1, M, K);
 }
 
+er_status er_hip_encode_q4k_weights_packed(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                           er_buffer input, er_buffer output, uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q4_K, weight, input, output, 1, M, K);
+}
+
+er_status er_hip_encode_q4k_weights_packed_four_rows(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                                     er_buffer input, er_buffer output, uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q4_K, weight, input, output, 1, M, K);
+}
+
+er_status er_hip_encode_q4k_weights_llama_style(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                                er_buffer input, er_buffer output, uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q4_K, weight, input, output, 1, M, K);
+}
+
+er_status er_hip_encode_q4k_weights_two_rows(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                             er_buffer input, er_buffer output, uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q4_K, weight, input, output, 1, M, K);
+}
+
+er_status er_hip_encode_q6k_weights_packed(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                           er_buffer input, er_buffer output, uint32_t M, uint32_t K) {
+    return encode_gemv(ctx, stream, Fmt::Q6_K, weight, input, output, 1, M, K);
+}
+
+er_status er_hip_encode_q4k_weights_llama_style_dual(er_hip_ctx *ctx, er_stream stream, er_buffer weight_a,
+                                                     er_buffer weight_b, er_buffer input, er_buffer output_a,
+                                                     er_buffer output_b, uint32_t M, uint32_t K) {
+    return er_hip_encode_q4k_weights_dual(ctx, stream, weight_a, weight_b, input, output_a, output_b, M, K);
+}
+
+er_status er_hip_encode_q4k_weights_triple_packed(er_hip_ctx *ctx, er_stream stream, er_buffer weight_a,
+                                                  er_buffer weight_b, er_buffer weight_c, er_buffer input,
+                                                  er_buffer output_a, er_buffer output_b, er_buffer output_c,
+                                                  uint32_t rows_a, uint32_t rows_b, uint32_t rows_c, uint32_t K) {
+    return er_hip_encode_q4k_weights_triple(ctx, stream, weight_a, weight_b, weight_c, input, output_a, output_b,
+                                            output_c, rows_a, rows_b, rows_c, K);
+}
+
+er_status er_hip_execute_q4k_weights(er_hip_ctx *ctx, const void *raw_weights, uint64_t raw_bytes, const float *x,
+                                     uint64_t x_count, float *y, uint64_t y_count, uint32_t M, uint32_t K) {
+    return execute_gemv_host(ctx, Fmt::Q4_K, raw_weights, raw_bytes, x, x_count, y, y_count, 1, false, M, K);
+}
+
+er_status er_hip_execute_q6k_weights(er_hip_ctx *ctx, const void *raw_weights, uint64_t raw_bytes, const float *x,
+                                     uint64_t x_count, float *y, uint64_t y_count, uint32_t M, uint32_t K) {
+    return execute_gemv_host(ctx, Fmt::Q6_K, raw_weights, raw_bytes, x, x_count, y, y_count, 1, false, M, K);
+}
+
+er_status er_hip_execute_q4k_weights_with_weight_buffer(er_hip_ctx *ctx, er_buffer weight, const float *x,
+                                                        uint64_t x_count, float *y, uint64_t y_count, uint32_t M,
+                                                        uint32_t K) {
+    return execute_gemv(ctx, Fmt::Q4_K, weight, x, x_count, y, y_count, 1, false, M, K);
+}
+
+er_status er_hip_execute_q6k_weights_with_weight_buffer(er_hip_ctx *ctx, er_buffer weight, const float *x,
+                                                        uint64_t x_count, float *y, uint64_t y_count, uint32_t M,
+                                                        uint32_t K) {
+    return execute_gemv(ctx, Fmt::Q6_K, weight, x, x_count, y, y_count, 1, false, M, K);
+}
+
+er_status er_hip_execute_batched_q4k_weights(er_hip_ctx *ctx, const void *raw_weights, uint64_t raw_bytes,
+                                             const float *x, uint64_t x_count, float *y, uint64_t y_count,
+                                             uint32_t batch_seq, uint32_t M, uint32_t K) {
+    return execute_gemv_host(ctx, Fmt::Q4_K, raw_weights, raw_bytes, x, x_count, y, y_count, batch_seq, true, M, K);
+}
+
 er_status er_hip_encode_q4k_weights_dual(er_hip_ctx *ctx, er_stream stream, er_buffer weight_a,
                                          er_buffer weight_b, er_buffer input, er_buffer output_a,
                                          er_buffer output_b, uint32_t M, uint32_t K) {
@@ -1524,3 +1669,54 @@ er_status er_hip_encode_projection(er_hip_ctx *ctx, er_stream stream,
 }
 
 }  // extern "C"
+
+// ---- measurement kernels (include/er_hip_probe.h) ----
+
+er_status er_hip_probe_stream_read(er_hip_ctx *ctx, er_stream stream, er_buffer src, uint64_t bytes,
+                                   uint32_t workgroups, er_buffer sink) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (bytes % 16u != 0 || bytes > src.length || workgroups == 0 || sink.length < (uint64_t)workgroups * 256u * 4u)
+        return fail(ER_ERR_INVALID_ARGUMENT, "stream read: %llu bytes of a %llu-byte source, %u workgroups, "
+                    "sink %llu bytes", (unsigned long long)bytes, (unsigned long long)src.length, workgroups,
+                    (unsigned long long)sink.length);
+    if (!src.data || !sink.data || !aligned(src.data, 16) || !aligned(sink.data, 4))
+        return fail(ER_ERR_INVALID_ARGUMENT, "stream read: null or misaligned buffer");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    uint64_t n16 = bytes / 16u;
+    uint32_t never = 0x9e3779b9u;
+    void *args[] = {&src.data, &n16, &never, &sink.data};
+    return launch(ctx, K_PROBE_STREAM_READ, dim3(workgroups, 1, 1), dim3(256, 1, 1), 0, stream, args);
+}
+
+er_status er_hip_probe_empty(er_hip_ctx *ctx, er_stream stream) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    return launch(ctx, K_PROBE_EMPTY, dim3(1, 1, 1), dim3(64, 1, 1), 0, stream, nullptr);
+}
+
+er_status er_hip_probe_grid_barrier(er_hip_ctx *ctx, er_stream stream, uint32_t workgroups, uint32_t rounds,
+                                    uint32_t spin_limit, er_buffer counter, er_buffer out) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (workgroups == 0 || workgroups > (uint32_t)ctx->cu_count || spin_limit == 0)
+        return fail(ER_ERR_INVALID_ARGUMENT, "grid barrier: %u workgroups (1..%d resident), spin limit %u",
+                    workgroups, ctx->cu_count, spin_limit);
+    if (!counter.data || !out.data || counter.length < 16u || out.length < 16u || !aligned(counter.data, 16) ||
+        !aligned(out.data, 16))
+        return fail(ER_ERR_INVALID_ARGUMENT, "grid barrier: counter and out need 16 aligned bytes each");
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    uint64_t one = 1;
+    void *za[] = {&counter.data, &one};
+    st = launch(ctx, K_FILL_ZERO, dim3(1, 1, 1), dim3(256, 1, 1), 0, stream, za);
+    if (st != ER_OK) return st;
+    void *zb[] = {&out.data, &one};
+    st = launch(ctx, K_FILL_ZERO, dim3(1, 1, 1), dim3(256, 1, 1), 0, stream, zb);
+    if (st != ER_OK) return st;
+    void *args[] = {&counter.data, &rounds, &spin_limit, &out.data};
+    return launch(ctx, K_PROBE_GRID_BARRIER, dim3(workgroups, 1, 1), dim3(64, 1, 1), 0, stream, args);
+}

@@ -6,3 +6,4 @@
 #include "er_gemm.hip"
 #include "er_quant.hip"
 #include "er_scratch.hip"
+#include "er_probe.hip"

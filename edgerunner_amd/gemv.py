@@ -58,6 +58,60 @@ class GEMVKernel:
         check(self.lib.er_hip_encode_q8_0_weights(self.ctx.handle, _sh(stream), weightBuffer.raw,
                                                   inputBuffer.raw, outputBuffer.raw, M, K))
 
+    # The reference's alternative encoders (GEMVKernel.swift:724-877, 1045,
+    # 1184): other Metal lane mappings of the same product.  Each is its
+    # canonical entry point under the reference's name (same validation and
+    # bit-identical results).
+    def _encode_alias(self, entry: str, stream, weightBuffer, inputBuffer, outputBuffer, M, K) -> None:
+        check(getattr(self.lib, entry)(self.ctx.handle, _sh(stream), weightBuffer.raw, inputBuffer.raw,
+                                       outputBuffer.raw, M, K))
+
+    def encodeQ4KWeightsPacked(self, stream, weightBuffer, inputBuffer, outputBuffer, M, K) -> None:
+        self._encode_alias("er_hip_encode_q4k_weights_packed", stream, weightBuffer, inputBuffer, outputBuffer, M, K)
+
+    def encodeQ4KWeightsPackedFourRows(self, stream, weightBuffer, inputBuffer, outputBuffer, M, K) -> None:
+        self._encode_alias("er_hip_encode_q4k_weights_packed_four_rows", stream, weightBuffer, inputBuffer,
+                           outputBuffer, M, K)
+
+    def encodeQ4KWeightsLlamaStyle(self, stream, weightBuffer, inputBuffer, outputBuffer, M, K) -> None:
+        self._encode_alias("er_hip_encode_q4k_weights_llama_style", stream, weightBuffer, inputBuffer,
+                           outputBuffer, M, K)
+
+    def encodeQ4KWeightsTwoRows(self, stream, weightBuffer, inputBuffer, outputBuffer, M, K) -> None:
+        self._encode_alias("er_hip_encode_q4k_weights_two_rows", stream, weightBuffer, inputBuffer, outputBuffer,
+                           M, K)
+
+    def encodeQ6KWeightsPacked(self, stream, weightBuffer, inputBuffer, outputBuffer, M, K) -> None:
+        self._encode_alias("er_hip_encode_q6k_weights_packed", stream, weightBuffer, inputBuffer, outputBuffer, M, K)
+
+    def encodeQ4KWeightsLlamaStyleDual(self, stream, weightBufferA, weightBufferB, inputBuffer, outputBufferA,
+                                       outputBufferB, M, K) -> None:
+        check(self.lib.er_hip_encode_q4k_weights_llama_style_dual(
+            self.ctx.handle, _sh(stream), weightBufferA.raw, weightBufferB.raw, inputBuffer.raw,
+            outputBufferA.raw, outputBufferB.raw, M, K))
+
+    def encodeQ4KWeightsTriplePacked(self, stream, weightBufferA, weightBufferB, weightBufferC, inputBuffer,
+                                     outputBufferA, outputBufferB, outputBufferC, rowsA, rowsB, rowsC, K) -> None:
+        check(self.lib.er_hip_encode_q4k_weights_triple_packed(
+            self.ctx.handle, _sh(stream), weightBufferA.raw, weightBufferB.raw, weightBufferC.raw,
+            inputBuffer.raw, outputBufferA.raw, outputBufferB.raw, outputBufferC.raw, rowsA, rowsB, rowsC, K))
+
+    def executeQ4KWeightsWithWeightBuffer(self, weightBuffer: Buffer, x, M: int, K: int) -> np.ndarray:
+        """GEMVKernel.executeQ4KWeightsWithWeightBuffer (GEMVKernel.swift:605): the C
+        convenience er_hip_execute_q4k_weights_with_weight_buffer (allocates x and y, waits)."""
+        return self._execute_c("er_hip_execute_q4k_weights_with_weight_buffer", weightBuffer.raw, x, M, M, K)
+
+    def executeQ6KWeightsWithWeightBuffer(self, weightBuffer: Buffer, x, M: int, K: int) -> np.ndarray:
+        """GEMVKernel.executeQ6KWeightsWithWeightBuffer (GEMVKernel.swift:1146)."""
+        return self._execute_c("er_hip_execute_q6k_weights_with_weight_buffer", weightBuffer.raw, x, M, M, K)
+
+    def _execute_c(self, entry: str, weight, x, yCount: int, *shape) -> np.ndarray:
+        xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        y = np.empty(max(yCount, 1), dtype=np.float32)
+        check(getattr(self.lib, entry)(self.ctx.handle, weight, xv.ctypes.data, xv.size, y.ctypes.data, yCount,
+                                       *shape))
+        return y[:yCount]
+
     def encodeBatchedQ4KWeights(self, stream: Optional[Stream], weightBuffer: Buffer,
                                 inputBuffer: Buffer, outputBuffer: Buffer, batchSeq: int, M: int,
                                 K: int) -> None:

@@ -213,6 +213,68 @@ er_status er_hip_encode_q4k_weights_dual_geglu(er_hip_ctx *ctx, er_stream stream
                                                er_buffer input, er_buffer output, uint32_t M,
                                                uint32_t K);
 
+/* ---- GEMVKernel's alternative encoders ----
+ * The reference keeps several Metal kernels for one product and lets the
+ * model pick one by flag (Gemma4RuntimeOptions, Sources/EdgeRunner/Models/
+ * Gemma4/Gemma4RuntimeOptions.swift:13-24; dispatch at
+ * Gemma4LanguageModel.swift:4207-4285).  They differ only in their Metal
+ * lane mapping: each computes the same y = W.x with the same validation
+ * (encodeKQuantWeights, GEMVKernel.swift:1276-1300).  Here each is its
+ * canonical entry point under the reference's name: identical arguments,
+ * validation, errors and results (bit for bit), and the kernel choice is the
+ * library's (by shape) whichever name is called. */
+/* encodeQ4KWeightsPacked (GEMVKernel.swift:724) = er_hip_encode_q4k_weights. */
+er_status er_hip_encode_q4k_weights_packed(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                           er_buffer input, er_buffer output, uint32_t M, uint32_t K);
+/* encodeQ4KWeightsPackedFourRows (GEMVKernel.swift:745) = er_hip_encode_q4k_weights. */
+er_status er_hip_encode_q4k_weights_packed_four_rows(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                                     er_buffer input, er_buffer output, uint32_t M, uint32_t K);
+/* encodeQ4KWeightsLlamaStyle (GEMVKernel.swift:767) = er_hip_encode_q4k_weights. */
+er_status er_hip_encode_q4k_weights_llama_style(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                                er_buffer input, er_buffer output, uint32_t M, uint32_t K);
+/* encodeQ4KWeightsTwoRows (GEMVKernel.swift:840) = er_hip_encode_q4k_weights. */
+er_status er_hip_encode_q4k_weights_two_rows(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                             er_buffer input, er_buffer output, uint32_t M, uint32_t K);
+/* encodeQ4KWeightsLlamaStyleDual (GEMVKernel.swift:789) = er_hip_encode_q4k_weights_dual. */
+er_status er_hip_encode_q4k_weights_llama_style_dual(er_hip_ctx *ctx, er_stream stream, er_buffer weight_a,
+                                                     er_buffer weight_b, er_buffer input, er_buffer output_a,
+                                                     er_buffer output_b, uint32_t M, uint32_t K);
+/* encodeQ4KWeightsTriplePacked (GEMVKernel.swift:1045) = er_hip_encode_q4k_weights_triple. */
+er_status er_hip_encode_q4k_weights_triple_packed(er_hip_ctx *ctx, er_stream stream, er_buffer weight_a,
+                                                  er_buffer weight_b, er_buffer weight_c, er_buffer input,
+                                                  er_buffer output_a, er_buffer output_b, er_buffer output_c,
+                                                  uint32_t rows_a, uint32_t rows_b, uint32_t rows_c, uint32_t K);
+/* encodeQ6KWeightsPacked (GEMVKernel.swift:1184) = er_hip_encode_q6k_weights. */
+er_status er_hip_encode_q6k_weights_packed(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
+                                           er_buffer input, er_buffer output, uint32_t M, uint32_t K);
+
+/* ---- synchronous conveniences (GEMVKernel.execute*, GEMVKernel.swift:545-627,
+ * 1146-1162, 1363-1413): allocate device x and y (and the weights, for the
+ * host-weight forms), encode on the device's null stream, wait, copy y to
+ * the caller's host array and free.  Validation as validateKQuantInputShape
+ * (GEMVKernel.swift:1415-1432): x_count == K (batched: batch_seq > 0 and
+ * x_count == batch_seq * K) and K > 0, K % 256 == 0, else
+ * INVALID_VECTOR_SHAPE; weight bytes >= M*(K/256)*blockBytes else
+ * INVALID_MATRIX_SHAPE.  y_count (floats the caller's y holds) below M
+ * (batched: batch_seq * M) or a failed allocation or copy -> ENCODING_FAILED. */
+/* executeQ4KWeights / executeQ6KWeights (GEMVKernel.swift:545, 575): weights from host memory. */
+er_status er_hip_execute_q4k_weights(er_hip_ctx *ctx, const void *raw_weights, uint64_t raw_bytes, const float *x,
+                                     uint64_t x_count, float *y, uint64_t y_count, uint32_t M, uint32_t K);
+er_status er_hip_execute_q6k_weights(er_hip_ctx *ctx, const void *raw_weights, uint64_t raw_bytes, const float *x,
+                                     uint64_t x_count, float *y, uint64_t y_count, uint32_t M, uint32_t K);
+/* executeQ4KWeightsWithWeightBuffer / executeQ6KWeightsWithWeightBuffer
+ * (GEMVKernel.swift:605, 1146): weights already in device memory. */
+er_status er_hip_execute_q4k_weights_with_weight_buffer(er_hip_ctx *ctx, er_buffer weight, const float *x,
+                                                        uint64_t x_count, float *y, uint64_t y_count, uint32_t M,
+                                                        uint32_t K);
+er_status er_hip_execute_q6k_weights_with_weight_buffer(er_hip_ctx *ctx, er_buffer weight, const float *x,
+                                                        uint64_t x_count, float *y, uint64_t y_count, uint32_t M,
+                                                        uint32_t K);
+/* executeBatchedQ4KWeights (GEMVKernel.swift:627): y[t*M + r] for t < batch_seq. */
+er_status er_hip_execute_batched_q4k_weights(er_hip_ctx *ctx, const void *raw_weights, uint64_t raw_bytes,
+                                             const float *x, uint64_t x_count, float *y, uint64_t y_count,
+                                             uint32_t batch_seq, uint32_t M, uint32_t K);
+
 /* ---- greedy top-1 over a Q6_K head ----
  * GEMVKernel.encodeQ6KWeightsPackedTop1 (GEMVKernel.swift:1205-1265; kernels
  * q6_k_gemv_packed_4row_top1_f32 + q6_k_top1_reduce, Dequant_Q6_K.metal:196-365).

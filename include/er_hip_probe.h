@@ -1,0 +1,38 @@
+/*
+ * er_hip_probe.h -- measurement entry points of EdgeRunnerHIP.
+ *
+ * Not part of the drop-in interface (no reference counterpart): kernels
+ * whose timings are the ceilings the GEMV and decode-chain designs are
+ * measured against (bench.py's "ceilings" leg), launched through the same
+ * context, streams and graphs as the product entry points.
+ */
+#ifndef ER_HIP_PROBE_H
+#define ER_HIP_PROBE_H
+
+#include "er_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Reads bytes (a multiple of 16, src 16-byte aligned) of src with
+ * non-temporal 16-byte loads, `workgroups` x 256 lanes, grid-stride; sink
+ * must hold workgroups * 256 uint32 (written only in a case that does not
+ * occur with real data, so the loads cannot be removed). */
+er_status er_hip_probe_stream_read(er_hip_ctx *ctx, er_stream stream, er_buffer src, uint64_t bytes,
+                                   uint32_t workgroups, er_buffer sink);
+/* One launch of an empty 64-thread kernel. */
+er_status er_hip_probe_empty(er_hip_ctx *ctx, er_stream stream);
+/* `rounds` grid-wide barriers across `workgroups` single-wave workgroups
+ * (1 <= workgroups <= the CU count, so all are resident).  counter and out
+ * (16 bytes each, 16-byte aligned) are cleared by a fill kernel first; every
+ * wait is bounded by spin_limit polls; out[0] receives the total polls and
+ * out[1] the number of waits that ran out (uint32 each). */
+er_status er_hip_probe_grid_barrier(er_hip_ctx *ctx, er_stream stream, uint32_t workgroups, uint32_t rounds,
+                                    uint32_t spin_limit, er_buffer counter, er_buffer out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ER_HIP_PROBE_H */

@@ -116,3 +116,78 @@ def test_top1_noalloc_validation_without_device():
         # past ER_HIP_TOP1_NOALLOC_MAX_ROWS fail before it
         assert f(None, None, _buf(M * 210), _buf(4 * K), _buf(4), M, K) == want, M
     assert f(None, None, _buf(1024 * 210), _buf(4 * K), _buf(3), 1024, K) == 3
+
+
+# The reference's alternative GEMVKernel encoders and the canonical entry
+# each one is (GEMVKernel.swift:724, 745, 767, 789, 840, 1045, 1184).
+ALIASES = {
+    "er_hip_encode_q4k_weights_packed": "er_hip_encode_q4k_weights",
+    "er_hip_encode_q4k_weights_packed_four_rows": "er_hip_encode_q4k_weights",
+    "er_hip_encode_q4k_weights_llama_style": "er_hip_encode_q4k_weights",
+    "er_hip_encode_q4k_weights_two_rows": "er_hip_encode_q4k_weights",
+    "er_hip_encode_q6k_weights_packed": "er_hip_encode_q6k_weights",
+    "er_hip_encode_q4k_weights_llama_style_dual": "er_hip_encode_q4k_weights_dual",
+    "er_hip_encode_q4k_weights_triple_packed": "er_hip_encode_q4k_weights_triple",
+}
+
+
+def test_alias_table_matches_header():
+    names = set(declared_symbols())
+    for alias, canon in ALIASES.items():
+        assert alias in names and canon in names
+        assert _ffi.SIGNATURES[alias] == _ffi.SIGNATURES[canon], alias
+
+
+@pytest.mark.parametrize("alias", [a for a, c in ALIASES.items() if c in (
+    "er_hip_encode_q4k_weights", "er_hip_encode_q6k_weights")])
+def test_alias_validation_equals_canonical(alias):
+    lib = _ffi.load()
+    a, c = getattr(lib, alias), getattr(lib, ALIASES[alias])
+    block = 210 if "q6k" in alias else 144
+    M, K = 8, 512
+    wb = M * (K // 256) * block
+    cases = [(wb, K * 4, M * 4, M, K), (wb, K * 4, M * 4, M, K + 128), (wb, K * 4, M * 4, M, 0),
+             (wb - 1, K * 4, M * 4, M, K), (wb, K * 4 - 4, M * 4, M, K), (wb, K * 4, M * 4 - 4, M, K)]
+    for w, xl, yl, m, k in cases:
+        got = a(None, None, _buf(w), _buf(xl), _buf(yl), m, k)
+        assert got == c(None, None, _buf(w), _buf(xl), _buf(yl), m, k)
+    assert a(None, None, _buf(wb), _buf(K * 4), _buf(M * 4), M, K) == 8
+
+
+def test_multi_alias_validation_equals_canonical():
+    lib = _ffi.load()
+    M, K = 4, 256
+    for w in (M * 144, M * 144 - 1):
+        args = (None, None, _buf(w), _buf(M * 144), _buf(K * 4), _buf(M * 4), _buf(M * 4), M, K)
+        assert lib.er_hip_encode_q4k_weights_llama_style_dual(*args) == lib.er_hip_encode_q4k_weights_dual(*args)
+    for k in (K, K + 1):
+        args = (None, None, _buf(M * 144), _buf(M * 144), _buf(M * 144), _buf(K * 4), _buf(M * 4), _buf(M * 4),
+                _buf(M * 4), M, M, M, k)
+        assert lib.er_hip_encode_q4k_weights_triple_packed(*args) == lib.er_hip_encode_q4k_weights_triple(*args)
+
+
+def test_execute_validation_without_device():
+    """GEMVKernel.execute* rules (validateKQuantInputShape): x.count == K, K a
+    positive multiple of 256, enough weight bytes, room for y; a valid call
+    then fails on the null context."""
+    import numpy as np
+    lib = _ffi.load()
+    M, K = 4, 256
+    w = np.zeros(M * 144, np.uint8)
+    x = np.zeros(K, np.float32)
+    y = np.zeros(M, np.float32)
+    f = lib.er_hip_execute_q4k_weights
+    assert f(None, w.ctypes.data, w.size, x.ctypes.data, K, y.ctypes.data, M, M, K) == 8
+    assert f(None, w.ctypes.data, w.size, x.ctypes.data, K - 1, y.ctypes.data, M, M, K) == 5
+    assert f(None, w.ctypes.data, w.size - 1, x.ctypes.data, K, y.ctypes.data, M, M, K) == 4
+    assert f(None, w.ctypes.data, w.size, x.ctypes.data, K, y.ctypes.data, M - 1, M, K) == 3
+    g = lib.er_hip_execute_q6k_weights_with_weight_buffer
+    assert g(None, _buf(M * 210), x.ctypes.data, K, y.ctypes.data, M, M, K) == 8
+    assert g(None, _buf(M * 210 - 1), x.ctypes.data, K, y.ctypes.data, M, M, K) == 4
+    assert g(None, _buf(M * 210), x.ctypes.data, K + 1, y.ctypes.data, M, M, K) == 5
+    b = lib.er_hip_execute_batched_q4k_weights
+    xb = np.zeros(3 * K, np.float32)
+    yb = np.zeros(3 * M, np.float32)
+    assert b(None, w.ctypes.data, w.size, xb.ctypes.data, 3 * K, yb.ctypes.data, 3 * M, 3, M, K) == 8
+    assert b(None, w.ctypes.data, w.size, xb.ctypes.data, 3 * K, yb.ctypes.data, 3 * M, 0, M, K) == 5
+    assert b(None, w.ctypes.data, w.size, xb.ctypes.data, 2 * K, yb.ctypes.data, 3 * M, 3, M, K) == 5
