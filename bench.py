@@ -89,6 +89,11 @@ def algorithmic_bytes(fmt: str, M: int, K: int) -> int:
     return weight_bytes(fmt, M, K) + 4 * K + 4 * M
 
 
+def gemm_min_bytes(fmt: str, T: int, N: int, K: int) -> int:
+    """Least HBM traffic of one prefill GEMM: W once, X (bf16) once, Y (fp32) written once."""
+    return weight_bytes(fmt, N, K) + 2 * T * K + 4 * T * N
+
+
 def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
     """Times `steps` GEMV launches over rotating weight copies.  The launches
     are recorded once into a HIP graph and replayed, so the events bracket
@@ -314,7 +319,7 @@ def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warm
     tflops = flops / (us * 1e-6) / 1e12
     return {"fmt": fmt, "T": T, "N": N, "K": K, "us_per_call": us, "TFLOPs": tflops,
             "frac_of_mfma_bf16_peak": tflops / MFMA_BF16_PEAK_TFLOPS,
-            "min_bytes": W.nbytes + 2 * T * K + 4 * T * N, "y_finite": bool(np.all(np.isfinite(y)))}
+            "min_bytes": gemm_min_bytes(fmt, T, N, K), "y_finite": bool(np.all(np.isfinite(y)))}
 
 
 def bench_chain(ctx, steps: int, warmup: int) -> dict:
@@ -360,32 +365,231 @@ def bench_chain(ctx, steps: int, warmup: int) -> dict:
     return out
 
 
+def _graph_time_us(ctx, stream, enc, steps: int) -> float:
+    """Average GPU time per call of `steps` calls of enc(i) recorded into one
+    HIP graph (after untimed replays), bracketed by HIP events."""
+    from edgerunner_amd import Capture
+    with Capture(ctx, stream) as cap:
+        for i in range(steps):
+            enc(i)
+    g = cap.graph
+    for _ in range(UNTIMED_REPLAYS):
+        g.launch(stream)
+    stream.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record(stream)
+    g.launch(stream)
+    e1.record(stream)
+    stream.synchronize()
+    us = e0.elapsed_ms(e1) * 1000.0 / steps
+    g.destroy()
+    e0.destroy()
+    e1.destroy()
+    return us
+
+
+# (name, bytes): the weight bytes of the two headline GEMV matrices
+STREAM_WORKLOADS = [("stream_read_33MB", 33030144), ("stream_read_62MB", 62390272)]
+BARRIER_GRIDS = (64, 128, 256)
+
+
+def bench_ceilings(ctx, steps: int) -> dict:
+    """The ceilings the GEMV and chain designs are measured against:
+      - a plain non-temporal 16-byte-per-lane read of each headline matrix's
+        weight bytes, over rotating copies (>= 768 MB, so every launch misses
+        the Infinity Cache), graph-timed like the GEMVs, best of 3 grid sizes;
+      - an empty kernel: GPU time per node of a graph of `steps` launches;
+      - a grid-wide barrier (one agent-scope counter, bounded waits) across
+        64 / 128 / 256 resident workgroups: (time of 200 rounds - time of 0
+        rounds) / 200, each one launch bracketed by events."""
+    import ctypes as C
+    lib = ctx.lib
+    stream = ctx.stream()
+    out = {}
+    for name, nbytes in STREAM_WORKLOADS:
+        copies = max(2, -(-ROTATE_BYTES // nbytes))
+        bufs = [ctx.alloc(nbytes) for _ in range(copies)]
+        for b in bufs:
+            b.upload(np.full(nbytes // 4, 0x3f800000, np.uint32), stream=stream)
+        best = None
+        for wgs in (1024, 2048, 4096):
+            sink = ctx.alloc(wgs * 256 * 4)
+            enc = lambda i: _check(lib.er_hip_probe_stream_read(ctx.handle, stream.handle, bufs[i % copies].raw,
+                                                                 nbytes, wgs, sink.raw))  # noqa: E731
+            for i in range(5):
+                enc(i)
+            us = _graph_time_us(ctx, stream, enc, steps)
+            sink.free()
+            if best is None or us < best[0]:
+                best = (us, wgs)
+        for b in bufs:
+            b.free()
+        out[name] = {"bytes": nbytes, "copies": copies, "us_per_call": best[0], "workgroups": best[1],
+                     "GBps": nbytes / (best[0] * 1e-6) / 1e9,
+                     "frac_of_hbm_peak": nbytes / (best[0] * 1e-6) / 1e9 / HBM_PEAK_GBS}
+        log(f"{name}: {best[0]:.2f} us, {out[name]['GBps']:.0f} GB/s ({best[1]} workgroups)")
+    us = _graph_time_us(ctx, stream, lambda i: _check(lib.er_hip_probe_empty(ctx.handle, stream.handle)), steps)
+    out["empty_kernel_in_graph"] = {"us_per_launch": us, "launches": steps}
+    log(f"empty kernel in a graph: {us:.2f} us per launch")
+    counter, res = ctx.alloc(16), ctx.alloc(16)
+    e0, e1 = ctx.event(), ctx.event()
+    rounds = 200
+    for wgs in BARRIER_GRIDS:
+        if wgs > ctx.compute_units:
+            continue
+        t = {}
+        for r in (0, rounds, 0, rounds):
+            e0.record(stream)
+            _check(lib.er_hip_probe_grid_barrier(ctx.handle, stream.handle, wgs, r, 1 << 20, counter.raw, res.raw))
+            e1.record(stream)
+            stream.synchronize()
+            t[r] = min(t.get(r, 1e30), e0.elapsed_ms(e1) * 1000.0)
+        polls, timeouts = (int(v) for v in res.download(np.uint32, 2))
+        per = (t[rounds] - t[0]) / rounds
+        out[f"grid_barrier_{wgs}"] = {"workgroups": wgs, "rounds": rounds, "us_per_barrier": per,
+                                      "timeouts": timeouts, "polls": polls}
+        log(f"grid barrier, {wgs} workgroups: {per:.2f} us per barrier ({timeouts} timed-out waits)")
+    e0.destroy()
+    e1.destroy()
+    counter.free()
+    res.free()
+    stream.destroy()
+    return out
+
+
+def bench_chain_breakdown(ctx, steps: int) -> dict:
+    """Where the decode chain's time goes: each distinct projection of a layer
+    (and the head), and the fused triple / dual launches, timed alone like a
+    GEMV workload (graph of `steps` launches over >= 768 MB of rotating weight
+    copies, so each launch reads HBM as it does inside the 398 MB step).  The
+    sums per step (x 28 layers + head) are set beside the measured chain."""
+    import edgerunner_amd.synth as synth
+    from edgerunner_amd import GEMVKernel
+    from edgerunner_amd.chain import ChainSpec
+
+    spec = ChainSpec()
+    gemv = GEMVKernel(ctx)
+    stream = ctx.stream()
+    out = {}
+
+    def rotating(fmt, M, K, t):
+        W = synth.weights(fmt, synth.seed(5, 200 + t), M, K, **DSCALE[fmt])
+        copies = max(2, -(-ROTATE_BYTES // W.nbytes))
+        return [ctx.upload(W, stream) for _ in range(copies)], W.nbytes
+
+    xs = {n: ctx.upload(synth.normal_f32(synth.seed(5, 300 + i), d), stream)
+          for i, (n, d) in enumerate((("h", spec.hidden), ("a", spec.q_dim), ("f", spec.ffn)))}
+    shapes = {}
+    for name, fmt, M, K, src in spec.layer_projections() + [("head", spec.head_fmt, spec.vocab, spec.hidden, "h")]:
+        shapes[name] = (fmt, M, K, src)
+    for t, (name, (fmt, M, K, src)) in enumerate(shapes.items()):
+        ws, wbytes = rotating(fmt, M, K, t)
+        yb = ctx.alloc(4 * M)
+        enc = getattr(gemv, ENCODE[fmt])
+        f = lambda i: enc(stream, ws[i % len(ws)], xs[src], yb, M, K)  # noqa: E731
+        for i in range(3):
+            f(i)
+        us = _graph_time_us(ctx, stream, f, steps)
+        out[name] = {"fmt": fmt, "M": M, "K": K, "weight_bytes": wbytes, "us_per_call": us,
+                     "GBps": wbytes / (us * 1e-6) / 1e9}
+        for b in ws:
+            b.free()
+        yb.free()
+        log(f"chain part {name} {fmt} {M}x{K}: {us:.2f} us ({out[name]['GBps']:.0f} GB/s)")
+    # fused launches: q/k/v triple and gate/up dual over rotating layer copies
+    tri = [rotating("q4_k", m, spec.hidden, 20 + j) for j, m in enumerate((spec.q_dim, spec.kv_dim, spec.kv_dim))]
+    ys = [ctx.alloc(4 * m) for m in (spec.q_dim, spec.kv_dim, spec.kv_dim)]
+    n = min(len(w[0]) for w in tri)
+    f = lambda i: gemv.encodeQ4KWeightsTriple(stream, tri[0][0][i % n], tri[1][0][i % n], tri[2][0][i % n],  # noqa
+                                              xs["h"], ys[0], ys[1], ys[2], spec.q_dim, spec.kv_dim, spec.kv_dim,
+                                              spec.hidden)
+    us = _graph_time_us(ctx, stream, f, steps)
+    out["qkv_triple"] = {"us_per_call": us, "weight_bytes": sum(w[1] for w in tri)}
+    for w in tri:
+        for b in w[0]:
+            b.free()
+    for b in ys:
+        b.free()
+    log(f"chain part qkv triple: {us:.2f} us")
+    du = [rotating("q4_k", spec.ffn, spec.hidden, 30 + j) for j in range(2)]
+    ys = [ctx.alloc(4 * spec.ffn) for _ in range(2)]
+    n = min(len(w[0]) for w in du)
+    f = lambda i: gemv.encodeQ4KWeightsDual(stream, du[0][0][i % n], du[1][0][i % n], xs["h"], ys[0], ys[1],  # noqa
+                                            spec.ffn, spec.hidden)
+    us = _graph_time_us(ctx, stream, f, steps)
+    out["gate_up_dual"] = {"us_per_call": us, "weight_bytes": sum(w[1] for w in du)}
+    for w in du:
+        for b in w[0]:
+            b.free()
+    for b in ys:
+        b.free()
+    log(f"chain part gate/up dual: {us:.2f} us")
+    L = spec.layers
+    per = sum(out[k]["us_per_call"] for k in ("q", "k", "v", "o", "gate", "up", "down"))
+    fused = sum(out[k]["us_per_call"] for k in ("qkv_triple", "o", "gate_up_dual", "down"))
+    out["sum_per_projection_us"] = L * per + out["head"]["us_per_call"]
+    out["sum_fused_us"] = L * fused + out["head"]["us_per_call"]
+    for b in xs.values():
+        b.free()
+    stream.destroy()
+    return out
+
+
+def _check(status: int) -> None:
+    from edgerunner_amd.runtime import check
+    check(status)
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(fmt: str, M: int, K: int, cfg: int, budget_s: float) -> dict:
     """Times the CPU oracle (oracle/er_oracle.c, the reference's Swift CPU
-    loop restated in C) on the same synthetic workload, all rows of the matrix,
-    repeated until `budget_s` seconds have passed."""
+    loop restated in C) on the same synthetic workload, all rows of the
+    matrix per call: single-threaded for a third of `budget_s`, then with the
+    rows split over every host thread this process may use for the rest.
+    The GPU boxes give one GPU's process a 16-thread CPU share
+    (OMP_NUM_THREADS=16, whatever nproc shows), so "all cores" is that share;
+    nproc, the affinity mask and the CPU model are reported beside it."""
     import edgerunner_amd.synth as synth
     from oracle import ref
 
     W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
     x = synth.normal_f32(synth.seed(cfg, 1), K)
-    threads = min(16, os.cpu_count() or 1, ref.max_threads())
-    ref.gemv(fmt, W, x, M, K, threads=threads)  # warm
-    calls = 0
-    t0 = time.perf_counter()
-    while True:
-        ref.gemv(fmt, W, x, M, K, threads=threads)
-        calls += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    per_call = el / calls
     nbytes = algorithmic_bytes(fmt, M, K)
+    nproc = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or affinity
+    threads = max(1, min(share, affinity, ref.max_threads()))
+
+    def timed(nthreads: int, seconds: float):
+        ref.gemv(fmt, W, x, M, K, threads=nthreads)  # warm
+        calls, t0 = 0, time.perf_counter()
+        while True:
+            ref.gemv(fmt, W, x, M, K, threads=nthreads)
+            calls += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                return calls, el
+
+    c1, e1 = timed(1, budget_s / 3.0)
+    cn, en = timed(threads, budget_s * 2.0 / 3.0)
+    per1, pern = e1 / c1, en / cn
     return {
-        "value": nbytes / per_call / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": f"{calls} full {fmt.upper()} GEMV calls {M}x{K} in {el:.1f} s "
-                  f"({per_call * 1e3:.2f} ms/call, OpenMP rows split over {threads} threads)",
-        "us_per_call": per_call * 1e6,
+        "value": nbytes / pern / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        "value_1thread": nbytes / per1 / 1e9,
+        "nproc": nproc, "affinity_cpus": affinity, "cpu_model": _cpu_model(),
+        "sample": f"full {fmt.upper()} GEMV calls {M}x{K}: {c1} single-threaded in {e1:.1f} s "
+                  f"({per1 * 1e3:.1f} ms/call), {cn} with rows split over {threads} OpenMP threads "
+                  f"(the process's CPU share; nproc {nproc}) in {en:.1f} s ({pern * 1e3:.2f} ms/call)",
+        "us_per_call": pern * 1e6,
     }
 
 
@@ -407,12 +611,14 @@ def load_traffic(name: str):
 COPY_CAL_BYTES = 64 << 20
 
 
-def probe(ctx, todo, steps: int, gemm_todo=()) -> None:
+def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None) -> None:
     """Counter-collection driver (run under `rocprofv3 --pmc ...`): three
     device-to-device copies of COPY_CAL_BYTES (the calibration kernel of known
-    traffic), then `steps` launches of each GEMV workload over rotating
-    weights, then `steps` eager launches of each GEMM workload in
-    `gemm_todo`."""
+    traffic), then for each GEMV workload (rotating weights) and each GEMM
+    workload in `gemm_todo`: one empty kernel (er_probe_empty) that marks
+    where the workload's dispatches begin, then its `steps` calls.  The workload names
+    and step counts go to `order_file` (one `name steps` line each), which
+    summarize() reads to label the dispatch groups."""
     import edgerunner_amd.synth as synth
     from edgerunner_amd import GEMVKernel
 
@@ -421,8 +627,10 @@ def probe(ctx, todo, steps: int, gemm_todo=()) -> None:
     for _ in range(3):
         dst.copy_from(src, stream=stream)
     stream.synchronize()
-    src.free()
-    dst.free()
+    order = []
+
+    def separator():
+        _check(ctx.lib.er_hip_probe_empty(ctx.handle, stream.handle))
     gemv = GEMVKernel(ctx)
     for name, fmt, M, K, cfg in todo:
         W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
@@ -431,9 +639,12 @@ def probe(ctx, todo, steps: int, gemm_todo=()) -> None:
         wbufs = [ctx.upload(W, stream) for _ in range(copies)]
         xb, yb = ctx.upload(x, stream), ctx.alloc(4 * M)
         enc = getattr(gemv, ENCODE[fmt])
+        stream.synchronize()
+        separator()
         for i in range(steps):
             enc(stream, wbufs[i % copies], xb, yb, M, K)
         stream.synchronize()
+        order.append((name, steps))
         log(f"probe {name}: {steps} launches")
         for b in wbufs:
             b.free()
@@ -445,15 +656,25 @@ def probe(ctx, todo, steps: int, gemm_todo=()) -> None:
     for name, fmt, T, N, K, cfg in gemm_todo:
         W = synth.weights(fmt, synth.seed(cfg, 0), N, K, **DSCALE[fmt])
         X = synth.normal_bf16(synth.seed(cfg, 1), T * K)
-        wb, xb, yb = ctx.upload(W, stream), ctx.upload(X, stream), ctx.alloc(4 * T * N)
+        copies = max(2, -(-ROTATE_BYTES // W.nbytes))
+        wbufs = [ctx.upload(W, stream) for _ in range(copies)]
+        xb, yb = ctx.upload(X, stream), ctx.alloc(4 * T * N)
         enc = gemm.encodeQ4K if fmt == "q4_k" else gemm.encodeQ8_0
-        for _ in range(steps):
-            enc(stream, wb, xb, yb, T, N, K)
         stream.synchronize()
-        log(f"probe {name}: {steps} launches")
-        for b in (wb, xb, yb):
+        separator()
+        for i in range(steps):
+            enc(stream, wbufs[i % copies], xb, yb, T, N, K)
+        stream.synchronize()
+        order.append((name, steps))
+        log(f"probe {name}: {steps} calls")
+        for b in wbufs + [xb, yb]:
             b.free()
+    for b in (src, dst):
+        b.free()
     stream.destroy()
+    if order_file:
+        Path(order_file).parent.mkdir(parents=True, exist_ok=True)
+        Path(order_file).write_text("".join(f"{n} {k}\n" for n, k in order))
 
 
 def _read_csv(path: Path):
@@ -485,6 +706,25 @@ def summarize(root: Path) -> str:
             key = (r["Kernel_Name"], r.get("Grid_Size_X", r.get("Grid_Size", "")),
                    r.get("Grid_Size_Y", ""))
             by[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        # consecutive launches of one (kernel, grid) in dispatch order: the
+        # workloads of a leg one after another (shapes that share a grid, such
+        # as the two stream reads, stay apart here)
+        runs = []
+        for r in sorted(_read_csv(traces[0]), key=lambda r: int(r["Start_Timestamp"])):
+            key = (r["Kernel_Name"], r.get("Grid_Size_X", r.get("Grid_Size", "")))
+            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            if runs and runs[-1][0] == key:
+                runs[-1][1].append(d)
+            else:
+                runs.append((key, [d]))
+        out.append("## Runs of consecutive launches (kernel trace, dispatch order, runs of 20 or more)\n")
+        out.append("| # | kernel | grid x | launches | avg us | median us | min us |")
+        out.append("|---|---|---|---|---|---|---|")
+        for i, ((k, gx), v) in enumerate(r for r in runs if len(r[1]) >= 20):
+            v = sorted(v)
+            out.append(f"| {i} | {k} | {gx} | {len(v)} | {sum(v) / len(v):.2f} | {v[len(v) // 2]:.2f} | "
+                       f"{v[0]:.2f} |")
+        out.append("")
         out.append("## Per-launch-shape durations (kernel trace)\n")
         out.append("| kernel | grid x | grid y | launches | avg us | median us |")
         out.append("|---|---|---|---|---|---|")
@@ -494,6 +734,9 @@ def summarize(root: Path) -> str:
                        f"{v[len(v) // 2]:.2f} |")
         out.append("")
     per_workload = {}
+    order_path = root / "probe_order.txt"
+    order = ([(l.split()[0], int(l.split()[1])) for l in order_path.read_text().splitlines() if l.strip()]
+             if order_path.exists() else [(w[0], None) for w in GEMV_WORKLOADS])
     for counter, sub in (("FETCH_SIZE", "fetch"), ("WRITE_SIZE", "write")):
         files = sorted(root.glob(f"{sub}/**/*counter_collection.csv"))
         if not files:
@@ -505,45 +748,44 @@ def summarize(root: Path) -> str:
         big = [v for v in copies if copies and v >= 0.5 * max(copies)]
         measured = sum(big) / len(big) if big else float("nan")
         factor = (COPY_CAL_BYTES / 1024) / measured if big else float("nan")
-        # GEMV dispatches in probe order: consecutive runs of one (kernel, grid)
-        runs = []
+        # dispatch groups: the kernels after each er_probe_empty marker
+        # (copy kernels, which uploads use too, belong to no group)
+        groups = []
         for r in rows:
-            if "copyBuffer" in r["Kernel_Name"]:
-                continue
-            key = (r["Kernel_Name"], r["Grid_Size"])
-            if not runs or runs[-1][0] != key:
-                runs.append((key, []))
-            runs[-1][1].append(float(r["Counter_Value"]))
-        out.append(f"## {counter} per dispatch, rocprofv3 --pmc {counter}\n")
+            if r["Kernel_Name"].startswith("er_probe_empty"):
+                groups.append([])
+            elif "copyBuffer" not in r["Kernel_Name"] and groups:
+                groups[-1].append(r)
+        out.append(f"## {counter} per call, rocprofv3 --pmc {counter}\n")
         out.append(f"Calibration: a {COPY_CAL_BYTES >> 20} MiB device-to-device copy (reads and "
                    f"writes {COPY_CAL_BYTES >> 10} KiB) counts {measured:.0f} KiB per dispatch on "
                    f"this counter; scale factor {factor:.4f}.\n")
-        out.append("| workload | kernel | grid | dispatches | KiB/dispatch | calibrated bytes |")
-        out.append("|---|---|---|---|---|---|")
-        for i, ((k, g), vs) in enumerate(runs):
-            name = GEMV_WORKLOADS[i][0] if i < len(GEMV_WORKLOADS) else f"run{i}"
-            avg = sum(vs) / len(vs)
-            cb = avg * 1024 * factor
+        out.append("| workload | kernels | dispatches | KiB per call | calibrated bytes per call |")
+        out.append("|---|---|---|---|---|")
+        for i, grp in enumerate(groups):
+            name, steps = order[i] if i < len(order) else (f"group{i}", None)
+            calls = steps or len(grp)
+            kib = sum(float(r["Counter_Value"]) for r in grp) / calls
+            cb = kib * 1024 * factor
             per_workload.setdefault(name, {})[counter] = cb
-            out.append(f"| {name} | {k} | {g} | {len(vs)} | {avg:.1f} | {cb:.0f} |")
+            kernels = ", ".join(sorted({r["Kernel_Name"] for r in grp}))
+            out.append(f"| {name} | {kernels} | {len(grp)} | {kib:.1f} | {cb:.0f} |")
         out.append("")
     if per_workload:
-        out.append("## HBM traffic per launch vs algorithmic bytes\n")
+        out.append("## HBM traffic per call vs algorithmic bytes\n")
         out.append("```")
         out.append("# workload fetch_bytes write_bytes  (calibrated FETCH_SIZE, WRITE_SIZE)")
-        for name, fmt, M, K, cfg in GEMV_WORKLOADS:
-            if name in per_workload:
-                v = per_workload[name]
-                out.append(f"{name} {v.get('FETCH_SIZE', 0):.0f} {v.get('WRITE_SIZE', 0):.0f}")
+        for name, v in per_workload.items():
+            out.append(f"{name} {v.get('FETCH_SIZE', 0):.0f} {v.get('WRITE_SIZE', 0):.0f}")
         out.append("```\n")
         out.append("| workload | algorithmic bytes | measured bytes | ratio |")
         out.append("|---|---|---|---|")
-        for name, fmt, M, K, cfg in GEMV_WORKLOADS:
-            if name in per_workload:
-                v = per_workload[name]
+        alg = {w[0]: algorithmic_bytes(w[1], w[2], w[3]) for w in GEMV_WORKLOADS}
+        alg.update({w[0]: gemm_min_bytes(w[1], w[2], w[3], w[4]) for w in GEMM_WORKLOADS})
+        for name, v in per_workload.items():
+            if name in alg:
                 tot = v.get("FETCH_SIZE", 0) + v.get("WRITE_SIZE", 0)
-                alg = algorithmic_bytes(fmt, M, K)
-                out.append(f"| {name} | {alg} | {tot:.0f} | {tot / alg:.3f} |")
+                out.append(f"| {name} | {alg[name]} | {tot:.0f} | {tot / alg[name]:.3f} |")
         out.append("")
     return "\n".join(out)
 
@@ -568,6 +810,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--probe", action="store_true",
                     help="counter-collection driver for rocprofv3 --pmc (no JSON line)")
+    ap.add_argument("--probe-order", metavar="FILE",
+                    help="with --probe: write the workload order for --summarize")
     ap.add_argument("--summarize", metavar="DIR",
                     help="print a markdown summary of a rocprofv3 output tree and exit")
     args = ap.parse_args()
@@ -597,12 +841,13 @@ def main() -> int:
     if args.probe:
         gemm_todo = [w for w in GEMM_WORKLOADS if args.workloads not in ("all", "headline")
                      and w[0] in args.workloads.split(",")]
-        probe(ctx, todo, args.steps, gemm_todo)
+        probe(ctx, todo, args.steps, gemm_todo, args.probe_order)
         return 0
     results = {}
     for name, fmt, M, K, cfg in todo:
         log(f"{name}: running")
         r = bench_gemv(ctx, fmt, M, K, cfg, args.steps, args.warmup)
+        r["traffic_bytes"] = load_traffic(name)
         results[name] = r
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
             f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s); eager {r['us_per_call_eager']:.2f} us")
@@ -630,6 +875,7 @@ def main() -> int:
             continue
         log(f"{name}: running")
         r = bench_gemm(ctx, fmt, T, N, K, cfg, max(20, args.steps // 4), min(args.warmup, 5))
+        r["traffic_bytes"] = load_traffic(name)
         results[name] = r
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['TFLOPs']:.1f} TFLOP/s "
             f"({100 * r['frac_of_mfma_bf16_peak']:.1f}% of bf16 dense peak)")
@@ -651,12 +897,21 @@ def main() -> int:
                 f"{v['GBps']:.0f} GB/s ({100 * v['frac_of_hbm_peak']:.1f}% of 8 TB/s); "
                 f"eager {v['us_per_step_eager']:.1f} us")
 
+    if args.workloads in ("all", "chain") or "chain_breakdown" in args.workloads.split(","):
+        log("chain_breakdown: running")
+        results["chain_breakdown"] = bench_chain_breakdown(ctx, max(20, args.steps // 4))
+
+    if args.workloads == "all" or "ceilings" in args.workloads.split(","):
+        log("ceilings: running")
+        results["ceilings"] = bench_ceilings(ctx, args.steps)
+
     h = results[head[0]]
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline: running")
         cpu = cpu_baseline(head[1], head[2], head[3], head[4], args.cpu_seconds)
-        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads, {cpu['value_1thread']:.2f} GB/s "
+            f"single-threaded ({cpu['cpu_model']}, nproc {cpu['nproc']})")
 
     traffic = load_traffic(head[0])
     out = {
