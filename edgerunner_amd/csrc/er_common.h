@@ -27,6 +27,9 @@ ER_DEV float f16_to_f32(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
+// s_waitcnt immediate for vmcnt(n), n < 64, with the other counters unconstrained.
+constexpr uint16_t vmcnt_imm(int n) { return (uint16_t)((n & 15) | ((n >> 4) << 14) | 0x0070 | 0x0f00); }
+
 // Lane index within the wave, computed afresh from the exec-mask counters
 // (no register has to stay live to provide it).
 ER_DEV uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }

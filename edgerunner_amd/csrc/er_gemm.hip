@@ -571,3 +571,344 @@ ER_GEMMP_ENTRY(q4k, true, 128)
 ER_GEMMP_ENTRY(q4k, true, 256)
 ER_GEMMP_ENTRY(q8_0, false, 128)
 ER_GEMMP_ENTRY(q8_0, false, 256)
+
+// ---------------------------------------------------------------------------
+// Loader-specialised variant (512 threads, 256 weight rows x 128 tokens per
+// workgroup, K % 256 == 0).  Waves 4-5 copy the X tile and waves 6-7 the raw
+// weight bytes of each 64-wide chunk into LDS rings with global_load_lds, each
+// pair with its own vmcnt queue, so an X copy never waits behind a weight
+// fetch from HBM (a wave's loads complete in issue order).  Waves 0-3 never
+// touch global memory until the epilogue: wave w dequantises the raw bytes of
+// its 64 rows [64w, 64w + 64) straight into MFMA operand registers and
+// multiplies them against all 128 tokens (2 x 4 blocks of 32x32
+// accumulators), so only X passes through LDS as bf16.
+//
+// Per chunk c, one barrier for all 8 waves (barrier c):
+//   - before it, the X pair waits until chunk c is in LDS, the weight pair
+//     until chunk c + 1 is (its dequantisation runs during the MFMAs of c);
+//     the compute waves' LDS reads of the iteration before are complete;
+//   - after it, the X pair copies chunk c + DX into the stage of chunk c - 1
+//     and the weight pair chunk c + DW into the stage of chunk c - 1 (read
+//     by the dequantisation during iteration c - 2).
+// Copies past the last chunk re-copy the last chunk into a free stage, so each
+// loader's wait is the same every iteration.
+//
+// LDS: X stages of 128 token rows x 144 bytes (128 of data + 16 of padding,
+// so the 16-byte A-fragment reads of 32 consecutive rows fall on distinct
+// banks); weight stages of 256 rows x WROWB bytes:
+//   Q4_K: 48 = super-block header (16) + the chunk's 32 qs bytes;
+//   Q8_0: 80 = the 16-byte-aligned window [68c & ~15, +80) of the row's bytes,
+//         which holds the chunk's two 34-byte blocks at offset 4 (c % 4).
+//
+// Inside a chunk the k order of each MFMA step s is the one the raw bytes give
+// lane half h (gemml_acol): Q4_K low nibbles of qs bytes [16h, 16h + 16) for
+// s < 2, their high nibbles for s >= 2; Q8_0 block h; the A fragments read X
+// at the same k, so every product pairs the right operands.
+// ---------------------------------------------------------------------------
+#define ER_GEMML_TN 256
+#define ER_GEMML_TT 128
+#define ER_GEMML_XROWB 144
+#define ER_GEMML_XSTAGE (ER_GEMML_TT * ER_GEMML_XROWB)  // 18432
+
+template <bool Q4K>
+struct GemmL {
+    static constexpr uint32_t WROWB = Q4K ? 48u : 80u;
+    static constexpr uint32_t WSTAGE = ER_GEMML_TN * WROWB;   // 12288 / 20480
+    static constexpr int NX = 4;                              // X stages
+    static constexpr int NW = Q4K ? 6 : 4;                    // weight stages
+    static constexpr int DX = NX - 1, DW = NW;                // copy-ahead distances (chunks)
+    static constexpr int LX = ER_GEMML_XSTAGE / 1024 / 2;     // 9 copies per X wave per chunk
+    static constexpr int LW = (int)(WSTAGE / 1024u / 2u);     // 6 / 10 per weight wave per chunk
+    static constexpr uint32_t LDS = NX * ER_GEMML_XSTAGE + NW * WSTAGE;  // 147456 / 155648
+};
+
+ER_DEV uint32_t gemml_acol(bool q4k, uint32_t s, uint32_t h) {
+    // bf16 column of the chunk that step s / lane half h reads
+    return q4k ? 32u * (s >> 1) + 16u * h + 8u * (s & 1u) : 32u * h + 8u * s;
+}
+
+// Scales of one lane's weights for a chunk: Q4_K (s0, m0) for the low
+// nibbles (sub-block 2p of pair p = chunk % 4) and (s1, m1) for the high
+// nibbles (sub-block 2p + 1); Q8_0 s0 = d of block 2 chunk + h.
+struct DqScale {
+    float s0, m0, s1, m1;
+};
+
+template <bool Q4K>
+ER_DEV DqScale dq_scale(const WRaw &r, uint32_t chunk, uint32_t h) {
+    DqScale q;
+    if (Q4K) {
+        const float d = f16_to_f32(r.a.x & 0xffffu), dmin = f16_to_f32(r.a.x >> 16);
+        uint32_t sc2, m2;
+        q4k_scales_pair(r.a.y, r.a.z, r.a.w, chunk & 3u, &sc2, &m2);
+        q.s0 = d * ub0(sc2);
+        q.m0 = dmin * ub0(m2);
+        q.s1 = d * ub1(sc2);
+        q.m1 = dmin * ub1(m2);
+    } else {
+        q.s0 = f16_to_f32(h ? (r.a.x >> 16) : (r.a.x & 0xffffu));
+        q.m0 = -128.0f * q.s0;  // exact: a power-of-two multiple of d
+        q.s1 = q.m1 = 0.0f;
+    }
+    return q;
+}
+
+// The four packed bf16 pairs of MFMA step s (0..3) that dequant_w puts at
+// out[4s .. 4s + 3], with the same operations, so a chunk can be
+// dequantised one step at a time between the matrix instructions.
+template <bool Q4K>
+ER_DEV void dq_step(const WRaw &r, const DqScale &q, uint32_t h, int s, uint32_t *out) {
+    if (Q4K) {
+        const uint32_t qw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+        const uint32_t M0F = vreg_const(0x0f0f0f0fu);
+        const bool hi = s >= 2;
+        const float sc = hi ? q.s1 : q.s0, mn = hi ? q.m1 : q.m0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t w = qw[2 * (s & 1) + j];
+            const uint32_t v = hi ? ((w >> 4) & M0F) : (w & M0F);
+            out[2 * j + 0] = pack_bf16x2(__builtin_fmaf(sc, ub0(v), -mn), __builtin_fmaf(sc, ub1(v), -mn));
+            out[2 * j + 1] = pack_bf16x2(__builtin_fmaf(sc, ub2(v), -mn), __builtin_fmaf(sc, ub3(v), -mn));
+        }
+    } else {
+        const uint32_t v[9] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c};
+        // byte b as u = b + 128 (flipping the sign bit), then d * u - 128 d:
+        // for finite d, d * u and 128 d are exact and so is their difference d * b, which
+        // equals the d * b of dequant_w
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int k = 2 * s + j;
+            const uint32_t w = (h ? v[k + 1] : alignbyte(v[k + 1], v[k], 2)) ^ 0x80808080u;
+            out[2 * j + 0] = pack_bf16x2(__builtin_fmaf(q.s0, ub0(w), q.m0), __builtin_fmaf(q.s0, ub1(w), q.m0));
+            out[2 * j + 1] = pack_bf16x2(__builtin_fmaf(q.s0, ub2(w), q.m0), __builtin_fmaf(q.s0, ub3(w), q.m0));
+        }
+    }
+}
+
+template <int N>
+ER_DEV void gemml_vmwait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(N) & 0xc07f);
+}
+
+// s_barrier with only a compiler ordering fence around it: a release fence
+// would also wait for the loader's global_load_lds copies in flight (they
+// write LDS) and so drain the prefetch.
+ER_DEV void gemml_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool Q4K>
+ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
+                    uint32_t T, uint32_t N, uint32_t K) {
+    using G = GemmL<Q4K>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t glds[];
+    uint8_t *xs = glds;                             // NX X stages
+    uint8_t *wsm = glds + G::NX * ER_GEMML_XSTAGE;  // NW weight stages
+    const uint32_t nT = (T + ER_GEMML_TT - 1) / ER_GEMML_TT, nN = (N + ER_GEMML_TN - 1) / ER_GEMML_TN;
+    const uint32_t total = nT * nN, per = (total + 7u) / 8u;
+    const uint32_t L = blockIdx.x;
+    // the items of one XCD (L % 8) are consecutive, token tile fastest, so the
+    // workgroups reading one weight tile share that XCD's L2
+    const uint32_t item = (L % 8u) * per + L / 8u;
+    if (item >= total) return;
+    const uint32_t tt = item % nT, nt = item / nT;
+    const uint32_t n0 = nt * ER_GEMML_TN, t0 = tt * ER_GEMML_TT;
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t NC = K / 64u;
+    const uint32_t rowBytes = Q4K ? (K >> 8) * 144u : (K >> 6) * 68u;
+
+    if (wave >= 6) {
+        // weight copies: unit u (of the stage's 2 LW units of 1 KB) puts 16
+        // bytes at stage byte 1024 u + 16 lane = row r, byte b of the row
+        const uint32_t ub = (wave - 6u) * G::LW;
+        uint32_t wa[G::LW], wq = 0;  // wq bit q: unit q's piece is qs bytes (Q4_K)
+#pragma unroll
+        for (int q = 0; q < G::LW; ++q) {
+            const uint32_t o = 1024u * (ub + q) + 16u * lane, r = o / G::WROWB, b = o % G::WROWB;
+            wa[q] = min(n0 + r, N - 1u) * rowBytes + b;
+            wq |= (b >= 16u ? 1u : 0u) << q;
+        }
+        auto issue = [&](uint32_t chunk, uint32_t slot) {
+            chunk = min(chunk, NC - 1u);
+            uint8_t *st = wsm + slot * G::WSTAGE + 1024u * ub;
+            // Q4_K piece b: header (b < 16) or qs bytes [32p + b - 16, +16) of pair p;
+            // Q8_0: the aligned window of the chunk
+            const uint32_t cq = Q4K ? (chunk >> 2) * 144u : (68u * chunk) & ~15u;
+            const uint32_t cp = Q4K ? 32u * (chunk & 3u) : 0u;
+#pragma unroll
+            for (int q = 0; q < G::LW; ++q) {
+                const uint32_t off = wa[q] + cq + (Q4K && ((wq >> q) & 1u) ? cp : 0u);
+                __builtin_amdgcn_global_load_lds((const void *)(W + off), (void *)(st + 1024u * q), 16, 0, 0);
+            }
+        };
+#pragma unroll
+        for (int j = 0; j < G::DW; ++j) issue((uint32_t)j, (uint32_t)j);
+        gemml_vmwait<(G::DW - 2) * G::LW>();  // chunks 0 and 1 are in
+        gemml_barrier();
+        for (uint32_t c = 0; c < NC; ++c) {
+            gemml_vmwait<(G::DW - 3) * G::LW>();  // chunks <= c + 2 are in
+            gemml_barrier();
+            issue(c + G::DW, (c + G::DW) % G::NW);
+        }
+        gemml_vmwait<0>();
+        return;
+    }
+    if (wave >= 4) {
+        // X copies: unit u (of the stage's 2 LX units) puts 16 bytes at stage
+        // byte 1024 u + 16 lane = token row r, byte column b; the padding bytes
+        // (b >= 128) take a copy of the row's first 16 bytes
+        const uint32_t ub = (wave - 4u) * G::LX;
+        uint32_t xo[G::LX];
+#pragma unroll
+        for (int q = 0; q < G::LX; ++q) {
+            const uint32_t o = 1024u * (ub + q) + 16u * lane, r = o / ER_GEMML_XROWB, b = o % ER_GEMML_XROWB;
+            xo[q] = min(t0 + r, T - 1u) * K * 2u + (b < 128u ? b : 0u);
+        }
+        auto issue = [&](uint32_t chunk, uint32_t slot) {
+            chunk = min(chunk, NC - 1u);
+            uint8_t *st = xs + slot * ER_GEMML_XSTAGE + 1024u * ub;
+#pragma unroll
+            for (int q = 0; q < G::LX; ++q)
+                __builtin_amdgcn_global_load_lds((const void *)((const uint8_t *)X + xo[q] + 128u * chunk),
+                                                 (void *)(st + 1024u * q), 16, 0, 0);
+        };
+#pragma unroll
+        for (int j = 0; j < G::DX; ++j) issue((uint32_t)j, (uint32_t)j);
+        gemml_vmwait<(G::DX - 1) * G::LX>();  // chunk 0 is in
+        gemml_barrier();
+        for (uint32_t c = 0; c < NC; ++c) {
+            gemml_vmwait<(G::DX - 2) * G::LX>();  // chunks <= c + 1 are in
+            gemml_barrier();
+            issue(c + G::DX, (c + G::DX) % G::NX);
+        }
+        gemml_vmwait<0>();
+        return;
+    }
+
+    // compute waves
+    const uint32_t h = lane >> 5, l32 = lane & 31u;
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[f][i][r] = 0.0f;
+    // raw bytes of row 64 wave + 32 f + l32 for `chunk` from its stage
+    auto rawW = [&](uint32_t chunk, int f, WRaw &r) {
+        const uint8_t *row = wsm + (chunk % G::NW) * G::WSTAGE + (64u * wave + 32u * (uint32_t)f + l32) * G::WROWB;
+        if (Q4K) {
+            r.a = *(const u32x4 *)row;
+            r.b = *(const u32x4 *)(row + 16u + 16u * h);
+            r.c = 0;
+        } else {
+            // blocks 2 chunk + h start at window byte 4 (chunk % 4) + 34 h; the
+            // 4-byte-aligned 36-byte window dequant_w expects starts at 4 (chunk % 4) + 32 h
+            const uint32_t *p = (const uint32_t *)(row + 4u * (chunk & 3u) + 32u * h);
+            r.a = u32x4{p[0], p[1], p[2], p[3]};
+            r.b = u32x4{p[4], p[5], p[6], p[7]};
+            r.c = p[8];
+        }
+    };
+    auto readA = [&](uint32_t chunk, int s, bf16x8 (&a)[4]) {
+        const uint8_t *xst = xs + (chunk % G::NX) * ER_GEMML_XSTAGE;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            a[i] = *(const bf16x8 *)(xst + (32u * i + l32) * ER_GEMML_XROWB + 2u * gemml_acol(Q4K, s, h));
+    };
+    // Software pipeline, per chunk c and MFMA step s (one scheduling region
+    // each): the LDS reads of the next step's X fragments (after step 3: the
+    // next chunk's step 0 and the raw weights of chunk c + 2), then the
+    // step's 8 MFMAs interleaved with the dequantisation of step s of chunk
+    // c + 1.  B operands: wd[c % 2]; raw weights of chunk c + 1: rw[c % 2].
+    uint32_t wd[2][2][16];
+    WRaw rw[2][2];
+    bf16x8 a[2][4];
+    DqScale sc[2];
+    gemml_barrier();  // X chunk 0 and weight chunks 0, 1 are in
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+        WRaw r0;
+        rawW(0u, f, r0);
+        const DqScale q0 = dq_scale<Q4K>(r0, 0u, h);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) dq_step<Q4K>(r0, q0, h, s, &wd[0][f][4 * s]);
+        rawW(1u, f, rw[0][f]);
+    }
+    readA(0u, 0, a[0]);
+    for (uint32_t c = 0; c < NC; c += 2u) {
+#pragma unroll
+        for (int P = 0; P < 2; ++P) {
+            const uint32_t cc = c + (uint32_t)P;
+            // NC is even (K % 256 == 0), so cc < NC on both halves
+            gemml_barrier();  // X chunk cc + 1 and weight chunk cc + 2 are in
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if (s < 3) {
+                    readA(cc, s + 1, a[(s + 1) & 1]);
+                } else {
+                    readA(cc + 1u, 0, a[0]);
+#pragma unroll
+                    for (int f = 0; f < 2; ++f) rawW(cc + 2u, f, rw[P ^ 1][f]);
+                }
+                if (s == 0) {
+#pragma unroll
+                    for (int f = 0; f < 2; ++f) sc[f] = dq_scale<Q4K>(rw[P][f], cc + 1u, h);
+                }
+#pragma unroll
+                for (int f = 0; f < 2; ++f) dq_step<Q4K>(rw[P][f], sc[f], h, s, &wd[P ^ 1][f][4 * s]);
+#pragma unroll
+                for (int f = 0; f < 2; ++f) {
+                    const bf16x8 b = __builtin_bit_cast(
+                        bf16x8, u32x4{wd[P][f][4 * s], wd[P][f][4 * s + 1], wd[P][f][4 * s + 2], wd[P][f][4 * s + 3]});
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[f][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s & 1][i], b, acc[f][i], 0, 0, 0);
+                }
+                // reads first, then matrix instructions each followed by a share
+                // of the dequantisation
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+                for (int m = 0; m < 8; ++m) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (s == 0) __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
+                    else __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+    // Branch-free epilogue: an element outside Y (last tiles) is the exact
+    // duplicate of the clamped element, because its X row and weight row were
+    // copied clamped the same way, so a plain store of it writes the value
+    // already there.  Offsets are 32-bit byte offsets from Y (host:
+    // T * N * 4 < 2^32).
+    uint32_t tl = t0 + 4u * h;
+    asm volatile("" : "+v"(tl));
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+        const uint32_t nc = min(n0 + 64u * wave + 32u * (uint32_t)f + l32, N - 1u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t t = min(tl + 32u * (uint32_t)i + 8u * (uint32_t)(r >> 2) + (uint32_t)(r & 3), T - 1u);
+                *(float *)((uint8_t *)Y + (t * N + nc) * 4u) = acc[f][i][r];
+            }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(512, 1)
+    er_gemml_q4k(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y, uint32_t T,
+                 uint32_t N, uint32_t K) {
+    gemm_ls<true>(W, X, Y, T, N, K);
+}
+extern "C" __global__ void __launch_bounds__(512, 1)
+    er_gemml_q8_0(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y, uint32_t T,
+                  uint32_t N, uint32_t K) {
+    gemm_ls<false>(W, X, Y, T, N, K);
+}

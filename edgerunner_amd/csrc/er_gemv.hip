@@ -1098,8 +1098,6 @@ struct CuQ6K {
 // LDS bytes of the family: limbs, then K fp32 values of raw x.
 ER_DEV uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 
-// s_waitcnt immediate for vmcnt(n), n < 64, with the other counters unconstrained.
-constexpr uint16_t vmcnt_imm(int n) { return (uint16_t)((n & 15) | ((n >> 4) << 14) | 0x0070 | 0x0f00); }
 
 // D: units (slot, row step) of weight loads in flight per wave.
 // JC > 0: exactly JC row steps per wave, fully unrolled (rowsPerWg = STEP * JC).

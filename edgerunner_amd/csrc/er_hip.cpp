@@ -80,6 +80,8 @@ using er_detail::fail;
     X(GEMMP_Q8_0_T256, "er_gemmp_q8_0_t256")                                           \
     X(GEMMW_Q4K_T128, "er_gemmw_q4k_t128")                                             \
     X(GEMMW_Q8_0_T128, "er_gemmw_q8_0_t128")                                           \
+    X(GEMML_Q4K, "er_gemml_q4k")                                                       \
+    X(GEMML_Q8_0, "er_gemml_q8_0")                                                     \
     X(PROBE_STREAM_READ, "er_probe_stream_read")                                       \
     X(PROBE_EMPTY, "er_probe_empty")                                                   \
     X(PROBE_GRID_BARRIER, "er_probe_grid_barrier")
@@ -181,7 +183,8 @@ struct er_hip_ctx {
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
     int multi_override = -1;  // ER_HIP_GEMV_MULTI_CONFIG=lpr:ns:r for the multi-matrix kernels (tests, sweeps)
     int cu_mode = -1;      // ER_HIP_GEMV_CU: 0 never, 1 whenever it applies, unset: by shape
-    int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1: non-pipelined GEMM, =2: 256-thread pipelined (comparisons)
+    int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1: non-pipelined GEMM, =2: 256-thread pipelined,
+                           // =3: warp-specialised, =4: loader-specialised wherever it applies (comparisons, tests)
     uint32_t gemm_tt = 0, gemm_sk = 0;  // ER_HIP_GEMM_TILE=tt:sk (benchmark sweeps only)
     int gemv_fp32 = 0;  // ER_HIP_GEMV_FP32=1 selects the fp32 GEMV family (benchmark comparison)
     // device address of this context's copy of the code object's er_scratch
@@ -739,6 +742,23 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
                     fmt_name(f), (unsigned long long)need, (unsigned long long)T * K * 2u);
     st = bind_device(ctx);
     if (st != ER_OK) return st;
+    {
+        // loader-specialised kernel: 256 weight rows x 128 tokens per
+        // workgroup, no K split, so it runs where those tiles alone give
+        // (nearly) every CU a workgroup
+        const uint64_t tiles = (uint64_t)((T + 127u) / 128u) * ((N + 255u) / 256u);
+        const bool fits = K % 256u == 0 && (uint64_t)T * N * 4u < (1ull << 32) && tiles <= 8ull * 65535u;
+        const bool wide = 4u * tiles >= 3u * (uint64_t)ctx->cu_count;
+        if (fits && ((ctx->gemm_variant == 0 && wide) || ctx->gemm_variant == 4)) {
+            void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K};
+            const uint32_t lds = f == Fmt::Q4_K ? 147456u : 155648u;  // GemmL<Q4K>::LDS
+            if (lds > ctx->info.lds_per_workgroup)
+                return fail(ER_ERR_ENCODING_FAILED, "GEMM: %u B of LDS per workgroup needed, %u available", lds,
+                            (unsigned)ctx->info.lds_per_workgroup);
+            return launch(ctx, f == Fmt::Q4_K ? K_GEMML_Q4K : K_GEMML_Q8_0,
+                          dim3((uint32_t)(8u * ((tiles + 7u) / 8u)), 1, 1), dim3(512, 1, 1), lds, stream, args);
+        }
+    }
     // Tile height TT (tokens) and K split SK: 128-token tiles (64 for short
     // inputs), then split K until the grid gives every CU a workgroup
     // (measured on MI355X: 512x14336x4096 is fastest unsplit, 512x4096x4096
