@@ -7,10 +7,13 @@ no CPU fallback for any entry point.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
-LIB_PATH = PKG / "libedgerunner_hip.so"
+# ER_HIP_LIB selects another build of the same library (the sanitizer build
+# of the host-side tests); by default the in-tree library.
+LIB_PATH = Path(os.environ["ER_HIP_LIB"]) if os.environ.get("ER_HIP_LIB") else PKG / "libedgerunner_hip.so"
 
 ER_OK = 0
 STATUS_NAMES = {

@@ -50,20 +50,23 @@ def build_code_object(extra: list[str] | None = None) -> Path:
     return CODE_OBJECT
 
 
+def _blob_source(code_object: Path) -> str:
+    """Assembly that embeds the code object as er_kernels_blob[_end]."""
+    return ("    .section .rodata\n"
+            "    .balign 4096\n"
+            "    .globl er_kernels_blob\n"
+            "er_kernels_blob:\n"
+            f"    .incbin \"{code_object}\"\n"
+            "    .globl er_kernels_blob_end\n"
+            "er_kernels_blob_end:\n"
+            "    .byte 0\n"
+            "    .section .note.GNU-stack,\"\",@progbits\n")
+
+
 def build_host_library(code_object: Path = CODE_OBJECT, out: Path = LIB) -> Path:
     BUILD.mkdir(exist_ok=True)
     blob = BUILD / "er_blob.S"
-    blob.write_text(
-        "    .section .rodata\n"
-        "    .balign 4096\n"
-        "    .globl er_kernels_blob\n"
-        "er_kernels_blob:\n"
-        f"    .incbin \"{code_object}\"\n"
-        "    .globl er_kernels_blob_end\n"
-        "er_kernels_blob_end:\n"
-        "    .byte 0\n"
-        "    .section .note.GNU-stack,\"\",@progbits\n"
-    )
+    blob.write_text(_blob_source(code_object))
     blob_o = BUILD / "er_blob.o"
     host_o = BUILD / "er_hip.o"
     _run(["gcc", "-c", str(blob), "-o", str(blob_o)])
@@ -78,6 +81,39 @@ def build_host_library(code_object: Path = CODE_OBJECT, out: Path = LIB) -> Path
           "-Wl,--version-script=" + str(CSRC / "er_hip.map")])
     os.replace(tmp, out)
     return out
+
+
+# Host-side sanitizer flags (g++/gcc only; no device code is built with them).
+SAN_FLAGS = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer",
+             "-g", "-O1"]
+
+
+def build_sanitized(out_dir: Path) -> tuple[Path, Path]:
+    """AddressSanitizer + UndefinedBehaviorSanitizer builds of the host code:
+    the C-ABI library (er_hip.cpp, er_gguf.cpp, with the gfx950 code object
+    embedded unchanged) and the CPU oracle.  For CPU runs of the host-side
+    tests (argument validation, GGUF parsing); the GPU kernels are never
+    built with a sanitizer.  Returns (library, oracle library)."""
+    out_dir.mkdir(parents=True, exist_ok=True)
+    if not CODE_OBJECT.exists():
+        build_code_object()
+    blob = out_dir / "er_blob.S"
+    blob.write_text(_blob_source(CODE_OBJECT))
+    blob_o = out_dir / "er_blob.o"
+    _run(["gcc", "-c", str(blob), "-o", str(blob_o)])
+    objs = []
+    for src in (CSRC / "er_hip.cpp", CSRC / "er_gguf.cpp"):
+        obj = out_dir / (src.stem + ".o")
+        _run(["g++", *SAN_FLAGS, "-fPIC", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I", str(ROCM / "include"),
+              "-I", str(ROOT / "include"), "-I", str(CSRC), "-c", str(src), "-o", str(obj)])
+        objs.append(str(obj))
+    lib = out_dir / "libedgerunner_hip.so"
+    _run(["g++", *SAN_FLAGS, "-shared", "-o", str(lib), *objs, str(blob_o), "-pthread", "-L", str(ROCM / "lib"),
+          "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}", "-Wl,--version-script=" + str(CSRC / "er_hip.map")])
+    oracle = out_dir / "liber_oracle.so"
+    _run(["gcc", *SAN_FLAGS, "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-fopenmp", "-std=c11", "-shared",
+          "-o", str(oracle), str(ROOT / "oracle" / "er_oracle.c"), "-lm"])
+    return lib, oracle
 
 
 def build_synth() -> Path:

@@ -6,13 +6,15 @@ cpu_baseline leg of bench.py.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB = HERE / "liber_oracle.so"
+# ER_ORACLE_LIB selects another build of the oracle (the sanitizer build)
+LIB = Path(os.environ["ER_ORACLE_LIB"]) if os.environ.get("ER_ORACLE_LIB") else HERE / "liber_oracle.so"
 _lib = None
 
 u8p = C.POINTER(C.c_uint8)
