@@ -611,12 +611,13 @@ def load_traffic(name: str):
 COPY_CAL_BYTES = 64 << 20
 
 
-def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None) -> None:
+def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None, chain_steps: int = 0) -> None:
     """Counter-collection driver (run under `rocprofv3 --pmc ...`): three
     device-to-device copies of COPY_CAL_BYTES (the calibration kernel of known
     traffic), then for each GEMV workload (rotating weights) and each GEMM
     workload in `gemm_todo`: one empty kernel (er_probe_empty) that marks
-    where the workload's dispatches begin, then its `steps` calls.  The workload names
+    where the workload's dispatches begin, then its `steps` calls; with
+    chain_steps, the same for that many eager steps of the fused decode chain.  The workload names
     and step counts go to `order_file` (one `name steps` line each), which
     summarize() reads to label the dispatch groups."""
     import edgerunner_amd.synth as synth
@@ -669,6 +670,20 @@ def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None) -> None:
         log(f"probe {name}: {steps} calls")
         for b in wbufs + [xb, yb]:
             b.free()
+    if chain_steps:
+        # the decode chain's fused encodes, eagerly on the stream (no graph
+        # capture): per-kernel durations of the chain under --kernel-trace
+        from edgerunner_amd.chain import ChainSpec, DecodeChain, make_inputs, make_weights
+        spec = ChainSpec()
+        ch = DecodeChain(ctx, spec, make_weights(spec), make_inputs(spec), stream)
+        stream.synchronize()
+        separator()
+        for _ in range(chain_steps):
+            ch.encode(stream, True)
+        stream.synchronize()
+        order.append(("decode_chain_fused_eager", chain_steps))  # per call = per decode step
+        log(f"probe decode_chain_fused_eager: {chain_steps} steps, {spec.launches(True)} launches each")
+        ch.free()
     for b in (src, dst):
         b.free()
     stream.destroy()
@@ -782,6 +797,8 @@ def summarize(root: Path) -> str:
         out.append("|---|---|---|---|")
         alg = {w[0]: algorithmic_bytes(w[1], w[2], w[3]) for w in GEMV_WORKLOADS}
         alg.update({w[0]: gemm_min_bytes(w[1], w[2], w[3], w[4]) for w in GEMM_WORKLOADS})
+        from edgerunner_amd.chain import ChainSpec
+        alg["decode_chain_fused_eager"] = ChainSpec().weight_bytes()
         for name, v in per_workload.items():
             if name in alg:
                 tot = v.get("FETCH_SIZE", 0) + v.get("WRITE_SIZE", 0)
@@ -841,7 +858,8 @@ def main() -> int:
     if args.probe:
         gemm_todo = [w for w in GEMM_WORKLOADS if args.workloads not in ("all", "headline")
                      and w[0] in args.workloads.split(",")]
-        probe(ctx, todo, args.steps, gemm_todo, args.probe_order)
+        chain_steps = 3 if "decode_chain" in args.workloads.split(",") else 0
+        probe(ctx, todo, args.steps, gemm_todo, args.probe_order, chain_steps)
         return 0
     results = {}
     for name, fmt, M, K, cfg in todo:
