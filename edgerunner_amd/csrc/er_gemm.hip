@@ -573,29 +573,35 @@ ER_GEMMP_ENTRY(q8_0, false, 128)
 ER_GEMMP_ENTRY(q8_0, false, 256)
 
 // ---------------------------------------------------------------------------
-// Loader-specialised variant (512 threads, 256 weight rows x 128 tokens per
+// Loader-specialised variant (512 threads, 128 R weight rows x 128 tokens per
 // workgroup, K % 256 == 0).  Waves 4-5 copy the X tile and waves 6-7 the raw
 // weight bytes of each 64-wide chunk into LDS rings with global_load_lds, each
 // pair with its own vmcnt queue, so an X copy never waits behind a weight
 // fetch from HBM (a wave's loads complete in issue order).  Waves 0-3 never
 // touch global memory until the epilogue: wave w dequantises the raw bytes of
-// its 64 rows [64w, 64w + 64) straight into MFMA operand registers and
-// multiplies them against all 128 tokens (2 x 4 blocks of 32x32
-// accumulators), so only X passes through LDS as bf16.
+// its 32 R rows straight into MFMA operand registers and multiplies them
+// against all 128 tokens (R x 4 blocks of 32x32 accumulators), so only X
+// passes through LDS as bf16.
+//
+// Compute waves, per chunk c and MFMA step s (one scheduling region each):
+// the LDS reads of the next step's X fragments are issued first (after step
+// 3: the next chunk's step 0 and the raw weights of chunk c + 2), then the
+// step's matrix instructions, each followed by a share of the dequantisation
+// of step s of chunk c + 1, so the LDS latency and the conversion both run
+// under the matrix instructions.
 //
 // Per chunk c, one barrier for all 8 waves (barrier c):
-//   - before it, the X pair waits until chunk c is in LDS, the weight pair
-//     until chunk c + 1 is (its dequantisation runs during the MFMAs of c);
-//     the compute waves' LDS reads of the iteration before are complete;
+//   - before it, the X pair waits until chunk c + 1 is in LDS and the weight
+//     pair until chunk c + 2 is (both are read ahead during chunk c);
 //   - after it, the X pair copies chunk c + DX into the stage of chunk c - 1
-//     and the weight pair chunk c + DW into the stage of chunk c - 1 (read
-//     by the dequantisation during iteration c - 2).
+//     (DX = NX - 1) and the weight pair chunk c + DW into the stage of chunk c
+//     (DW = NW; those raw bytes were read during chunk c - 2).
 // Copies past the last chunk re-copy the last chunk into a free stage, so each
 // loader's wait is the same every iteration.
 //
 // LDS: X stages of 128 token rows x 144 bytes (128 of data + 16 of padding,
 // so the 16-byte A-fragment reads of 32 consecutive rows fall on distinct
-// banks); weight stages of 256 rows x WROWB bytes:
+// banks); weight stages of 128 R rows x WROWB bytes:
 //   Q4_K: 48 = super-block header (16) + the chunk's 32 qs bytes;
 //   Q8_0: 80 = the 16-byte-aligned window [68c & ~15, +80) of the row's bytes,
 //         which holds the chunk's two 34-byte blocks at offset 4 (c % 4).
@@ -605,21 +611,26 @@ ER_GEMMP_ENTRY(q8_0, false, 256)
 // s < 2, their high nibbles for s >= 2; Q8_0 block h; the A fragments read X
 // at the same k, so every product pairs the right operands.
 // ---------------------------------------------------------------------------
-#define ER_GEMML_TN 256
 #define ER_GEMML_TT 128
 #define ER_GEMML_XROWB 144
 #define ER_GEMML_XSTAGE (ER_GEMML_TT * ER_GEMML_XROWB)  // 18432
 
-template <bool Q4K>
+// R: 32-row blocks per compute wave; the workgroup tile is TN = 128 R weight
+// rows (R = 2: 256 rows, for grids that fill the chip with 256-row tiles;
+// R = 1: 128 rows, twice the workgroups for narrower matrices).
+template <bool Q4K, int R>
 struct GemmL {
+    static constexpr uint32_t TN = 128u * R;
     static constexpr uint32_t WROWB = Q4K ? 48u : 80u;
-    static constexpr uint32_t WSTAGE = ER_GEMML_TN * WROWB;   // 12288 / 20480
+    static constexpr uint32_t WSTAGE = TN * WROWB;            // R = 2: 12288 / 20480, R = 1: 6144 / 10240
     static constexpr int NX = 4;                              // X stages
-    static constexpr int NW = Q4K ? 6 : 4;                    // weight stages
+    static constexpr int NW = R == 2 ? (Q4K ? 6 : 4) : (Q4K ? 8 : 6);  // weight stages
     static constexpr int DX = NX - 1, DW = NW;                // copy-ahead distances (chunks)
     static constexpr int LX = ER_GEMML_XSTAGE / 1024 / 2;     // 9 copies per X wave per chunk
-    static constexpr int LW = (int)(WSTAGE / 1024u / 2u);     // 6 / 10 per weight wave per chunk
-    static constexpr uint32_t LDS = NX * ER_GEMML_XSTAGE + NW * WSTAGE;  // 147456 / 155648
+    static constexpr int LW = (int)(WSTAGE / 1024u / 2u);     // copies per weight wave per chunk
+    static constexpr uint32_t LDS = NX * ER_GEMML_XSTAGE + NW * WSTAGE;
+    static_assert(WSTAGE % 2048u == 0, "weight stages split into 1 KB copies over two waves");
+    static_assert((DW - 2) * LW < 64 && (DX - 1) * LX < 64, "waits fit the load counter");
 };
 
 ER_DEV uint32_t gemml_acol(bool q4k, uint32_t s, uint32_t h) {
@@ -701,14 +712,14 @@ ER_DEV void gemml_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool Q4K>
+template <bool Q4K, int R>
 ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
                     uint32_t T, uint32_t N, uint32_t K) {
-    using G = GemmL<Q4K>;
+    using G = GemmL<Q4K, R>;
     extern __shared__ __attribute__((aligned(16))) uint8_t glds[];
     uint8_t *xs = glds;                             // NX X stages
     uint8_t *wsm = glds + G::NX * ER_GEMML_XSTAGE;  // NW weight stages
-    const uint32_t nT = (T + ER_GEMML_TT - 1) / ER_GEMML_TT, nN = (N + ER_GEMML_TN - 1) / ER_GEMML_TN;
+    const uint32_t nT = (T + ER_GEMML_TT - 1) / ER_GEMML_TT, nN = (N + G::TN - 1) / G::TN;
     const uint32_t total = nT * nN, per = (total + 7u) / 8u;
     const uint32_t L = blockIdx.x;
     // the items of one XCD (L % 8) are consecutive, token tile fastest, so the
@@ -716,7 +727,7 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
     const uint32_t item = (L % 8u) * per + L / 8u;
     if (item >= total) return;
     const uint32_t tt = item % nT, nt = item / nT;
-    const uint32_t n0 = nt * ER_GEMML_TN, t0 = tt * ER_GEMML_TT;
+    const uint32_t n0 = nt * G::TN, t0 = tt * ER_GEMML_TT;
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t NC = K / 64u;
     const uint32_t rowBytes = Q4K ? (K >> 8) * 144u : (K >> 6) * 68u;
@@ -791,16 +802,17 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
 
     // compute waves
     const uint32_t h = lane >> 5, l32 = lane & 31u;
-    f32x16 acc[2][4];
+    f32x16 acc[R][4];
 #pragma unroll
-    for (int f = 0; f < 2; ++f)
+    for (int f = 0; f < R; ++f)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[f][i][r] = 0.0f;
-    // raw bytes of row 64 wave + 32 f + l32 for `chunk` from its stage
+    // raw bytes of row 32 R wave + 32 f + l32 for `chunk` from its stage
     auto rawW = [&](uint32_t chunk, int f, WRaw &r) {
-        const uint8_t *row = wsm + (chunk % G::NW) * G::WSTAGE + (64u * wave + 32u * (uint32_t)f + l32) * G::WROWB;
+        const uint8_t *row =
+            wsm + (chunk % G::NW) * G::WSTAGE + (32u * R * wave + 32u * (uint32_t)f + l32) * G::WROWB;
         if (Q4K) {
             r.a = *(const u32x4 *)row;
             r.b = *(const u32x4 *)(row + 16u + 16u * h);
@@ -825,13 +837,13 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
     // next chunk's step 0 and the raw weights of chunk c + 2), then the
     // step's 8 MFMAs interleaved with the dequantisation of step s of chunk
     // c + 1.  B operands: wd[c % 2]; raw weights of chunk c + 1: rw[c % 2].
-    uint32_t wd[2][2][16];
-    WRaw rw[2][2];
+    uint32_t wd[2][R][16];
+    WRaw rw[2][R];
     bf16x8 a[2][4];
-    DqScale sc[2];
+    DqScale sc[R];
     gemml_barrier();  // X chunk 0 and weight chunks 0, 1 are in
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
+    for (int f = 0; f < R; ++f) {
         WRaw r0;
         rawW(0u, f, r0);
         const DqScale q0 = dq_scale<Q4K>(r0, 0u, h);
@@ -853,16 +865,16 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
                 } else {
                     readA(cc + 1u, 0, a[0]);
 #pragma unroll
-                    for (int f = 0; f < 2; ++f) rawW(cc + 2u, f, rw[P ^ 1][f]);
+                    for (int f = 0; f < R; ++f) rawW(cc + 2u, f, rw[P ^ 1][f]);
                 }
                 if (s == 0) {
 #pragma unroll
-                    for (int f = 0; f < 2; ++f) sc[f] = dq_scale<Q4K>(rw[P][f], cc + 1u, h);
+                    for (int f = 0; f < R; ++f) sc[f] = dq_scale<Q4K>(rw[P][f], cc + 1u, h);
                 }
 #pragma unroll
-                for (int f = 0; f < 2; ++f) dq_step<Q4K>(rw[P][f], sc[f], h, s, &wd[P ^ 1][f][4 * s]);
+                for (int f = 0; f < R; ++f) dq_step<Q4K>(rw[P][f], sc[f], h, s, &wd[P ^ 1][f][4 * s]);
 #pragma unroll
-                for (int f = 0; f < 2; ++f) {
+                for (int f = 0; f < R; ++f) {
                     const bf16x8 b = __builtin_bit_cast(
                         bf16x8, u32x4{wd[P][f][4 * s], wd[P][f][4 * s + 1], wd[P][f][4 * s + 2], wd[P][f][4 * s + 3]});
 #pragma unroll
@@ -873,7 +885,7 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
                 // of the dequantisation
                 __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-                for (int m = 0; m < 8; ++m) {
+                for (int m = 0; m < 4 * R; ++m) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     if (s == 0) __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
                     else __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
@@ -890,8 +902,8 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
     uint32_t tl = t0 + 4u * h;
     asm volatile("" : "+v"(tl));
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-        const uint32_t nc = min(n0 + 64u * wave + 32u * (uint32_t)f + l32, N - 1u);
+    for (int f = 0; f < R; ++f) {
+        const uint32_t nc = min(n0 + 32u * R * wave + 32u * (uint32_t)f + l32, N - 1u);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -902,13 +914,14 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
     }
 }
 
-extern "C" __global__ void __launch_bounds__(512, 1)
-    er_gemml_q4k(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y, uint32_t T,
-                 uint32_t N, uint32_t K) {
-    gemm_ls<true>(W, X, Y, T, N, K);
-}
-extern "C" __global__ void __launch_bounds__(512, 1)
-    er_gemml_q8_0(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y, uint32_t T,
-                  uint32_t N, uint32_t K) {
-    gemm_ls<false>(W, X, Y, T, N, K);
-}
+#define ER_GEMML_ENTRY(name, q4k, r)                                                                         \
+    extern "C" __global__ void __launch_bounds__(512, 1)                                                     \
+        name(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y, uint32_t T, \
+             uint32_t N, uint32_t K) {                                                                       \
+        gemm_ls<q4k, r>(W, X, Y, T, N, K);                                                                   \
+    }
+
+ER_GEMML_ENTRY(er_gemml_q4k, true, 2)
+ER_GEMML_ENTRY(er_gemml_q8_0, false, 2)
+ER_GEMML_ENTRY(er_gemml_q4k_r1, true, 1)
+ER_GEMML_ENTRY(er_gemml_q8_0_r1, false, 1)

@@ -82,6 +82,8 @@ using er_detail::fail;
     X(GEMMW_Q8_0_T128, "er_gemmw_q8_0_t128")                                           \
     X(GEMML_Q4K, "er_gemml_q4k")                                                       \
     X(GEMML_Q8_0, "er_gemml_q8_0")                                                     \
+    X(GEMML_Q4K_R1, "er_gemml_q4k_r1")                                                 \
+    X(GEMML_Q8_0_R1, "er_gemml_q8_0_r1")                                               \
     X(PROBE_STREAM_READ, "er_probe_stream_read")                                       \
     X(PROBE_EMPTY, "er_probe_empty")                                                   \
     X(PROBE_GRID_BARRIER, "er_probe_grid_barrier")
@@ -184,7 +186,8 @@ struct er_hip_ctx {
     int multi_override = -1;  // ER_HIP_GEMV_MULTI_CONFIG=lpr:ns:r for the multi-matrix kernels (tests, sweeps)
     int cu_mode = -1;      // ER_HIP_GEMV_CU: 0 never, 1 whenever it applies, unset: by shape
     int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1: non-pipelined GEMM, =2: 256-thread pipelined,
-                           // =3: warp-specialised, =4: loader-specialised wherever it applies (comparisons, tests)
+                           // =3: warp-specialised, =4 / =5: loader-specialised with 256 / 128-row tiles
+                           // wherever it applies (comparisons, tests)
     uint32_t gemm_tt = 0, gemm_sk = 0;  // ER_HIP_GEMM_TILE=tt:sk (benchmark sweeps only)
     int gemv_fp32 = 0;  // ER_HIP_GEMV_FP32=1 selects the fp32 GEMV family (benchmark comparison)
     // device address of this context's copy of the code object's er_scratch
@@ -743,20 +746,32 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     {
-        // loader-specialised kernel: 256 weight rows x 128 tokens per
+        // loader-specialised kernel: 256 (or 128) weight rows x 128 tokens per
         // workgroup, no K split, so it runs where those tiles alone give
-        // (nearly) every CU a workgroup
-        const uint64_t tiles = (uint64_t)((T + 127u) / 128u) * ((N + 255u) / 256u);
-        const bool fits = K % 256u == 0 && (uint64_t)T * N * 4u < (1ull << 32) && tiles <= 8ull * 65535u;
-        const bool wide = 4u * tiles >= 3u * (uint64_t)ctx->cu_count;
-        if (fits && ((ctx->gemm_variant == 0 && wide) || ctx->gemm_variant == 4)) {
+        // (nearly) every CU a workgroup (256-row tiles), or at least half of
+        // them (128-row tiles)
+        const uint64_t nT = (T + 127u) / 128u;
+        const uint64_t tiles2 = nT * ((N + 255u) / 256u), tiles1 = nT * ((N + 127u) / 128u);
+        const uint64_t cu = (uint64_t)ctx->cu_count;
+        const bool fits = K % 256u == 0 && (uint64_t)T * N * 4u < (1ull << 32) && tiles1 <= 8ull * 65535u;
+        int r = 0;
+        if (fits && ctx->gemm_variant == 0) r = 4u * tiles2 >= 3u * cu ? 2 : 2u * tiles1 >= cu ? 1 : 0;
+        if (fits && ctx->gemm_variant == 4) r = 2;
+        if (fits && ctx->gemm_variant == 5) r = 1;
+        if (r) {
             void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K};
-            const uint32_t lds = f == Fmt::Q4_K ? 147456u : 155648u;  // GemmL<Q4K>::LDS
+            // GemmL<Q4K, R>::LDS: 4 X stages of 18432 bytes + the weight stages
+            const uint32_t wst = (r == 2 ? 256u : 128u) * (f == Fmt::Q4_K ? 48u : 80u);
+            const uint32_t nw = r == 2 ? (f == Fmt::Q4_K ? 6u : 4u) : (f == Fmt::Q4_K ? 8u : 6u);
+            const uint32_t lds = 4u * 18432u + nw * wst;
             if (lds > ctx->info.lds_per_workgroup)
                 return fail(ER_ERR_ENCODING_FAILED, "GEMM: %u B of LDS per workgroup needed, %u available", lds,
                             (unsigned)ctx->info.lds_per_workgroup);
-            return launch(ctx, f == Fmt::Q4_K ? K_GEMML_Q4K : K_GEMML_Q8_0,
-                          dim3((uint32_t)(8u * ((tiles + 7u) / 8u)), 1, 1), dim3(512, 1, 1), lds, stream, args);
+            const uint64_t tiles = r == 2 ? tiles2 : tiles1;
+            const KernelId k = f == Fmt::Q4_K ? (r == 2 ? K_GEMML_Q4K : K_GEMML_Q4K_R1)
+                                              : (r == 2 ? K_GEMML_Q8_0 : K_GEMML_Q8_0_R1);
+            return launch(ctx, k, dim3((uint32_t)(8u * ((tiles + 7u) / 8u)), 1, 1), dim3(512, 1, 1), lds, stream,
+                          args);
         }
     }
     // Tile height TT (tokens) and K split SK: 128-token tiles (64 for short

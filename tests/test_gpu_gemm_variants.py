@@ -1,8 +1,9 @@
 """Every prefill GEMM kernel through contexts that force it: the
 warp-specialised kernel at each K split (ER_HIP_GEMM_TILE=128:sk, 1 to 8 ways,
 split-K summing with fp32 atomics into a zero-filled Y), the loader-specialised
-kernel on shapes whose tiles alone would not select it (ER_HIP_GEMM_VARIANT=4:
-partial token and weight-row tiles, one token tile of 33 rows), and the
+kernel with 256- and 128-row tiles on shapes whose tiles alone would not select
+it (ER_HIP_GEMM_VARIANT=4 / 5: partial token and weight-row tiles, one token
+tile of 33 rows), and the
 earlier kernels kept for comparison (=1 single-stage, =2 pipelined, =3
 warp-specialised).  Same bars as test_gpu_gemm.py: <= 1e-5 relative L2
 against the float64 product with the bf16-rounded dequantised weights (the
@@ -37,7 +38,7 @@ def _gemm(**env):
 
 
 CONFIGS = [{"ER_HIP_GEMM_TILE": f"128:{sk}"} for sk in (1, 2, 3, 4, 8)] + \
-          [{"ER_HIP_GEMM_VARIANT": v} for v in ("1", "2", "3", "4")]
+          [{"ER_HIP_GEMM_VARIANT": v} for v in ("1", "2", "3", "4", "5")]
 
 
 @pytest.mark.parametrize("env", CONFIGS, ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()))
