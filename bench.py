@@ -401,7 +401,10 @@ def bench_ceilings(ctx, steps: int) -> dict:
       - an empty kernel: GPU time per node of a graph of `steps` launches;
       - a grid-wide barrier (one agent-scope counter, bounded waits) across
         64 / 128 / 256 resident workgroups: (time of 200 rounds - time of 0
-        rounds) / 200, each one launch bracketed by events."""
+        rounds) / 200, each one launch bracketed by events;
+      - per-CU rates behind the prefill GEMM: LDS reads (A-fragment layout)
+        with 4 / 8 / 16 waves per CU, and bf16 MFMA / fp32 FMA overlap within
+        one wave and across two waves of a SIMD (best of 3 launches each)."""
     import ctypes as C
     lib = ctx.lib
     stream = ctx.stream()
@@ -449,6 +452,30 @@ def bench_ceilings(ctx, steps: int) -> dict:
         out[f"grid_barrier_{wgs}"] = {"workgroups": wgs, "rounds": rounds, "us_per_barrier": per,
                                       "timeouts": timeouts, "polls": polls}
         log(f"grid barrier, {wgs} workgroups: {per:.2f} us per barrier ({timeouts} timed-out waits)")
+    # per-CU rates of the prefill GEMM design: LDS reads in the A-fragment
+    # layout with 4 / 8 / 16 waves per CU, and matrix-core / vector-ALU overlap
+    sink = ctx.alloc(ctx.compute_units * 1024 * 4)
+
+    def timed(launch) -> float:
+        best = 1e30
+        for _ in range(3):
+            e0.record(stream)
+            launch()
+            e1.record(stream)
+            stream.synchronize()
+            best = min(best, e0.elapsed_ms(e1) * 1000.0)
+        return best
+    iters = 20000
+    for waves in (4, 8, 16):
+        us = timed(lambda: _check(lib.er_hip_probe_lds_read(ctx.handle, stream.handle, waves, iters, sink.raw)))
+        per_cu = iters * 8 * 1024 * waves / (us * 1000.0)
+        out[f"lds_read_{waves}_waves"] = {"us": us, "bytes_per_ns_per_cu": per_cu, "iters": iters}
+        log(f"LDS reads, {waves} waves per CU: {per_cu:.0f} B/ns per CU")
+    for mode, tag in enumerate(("mfma_alone", "fma_alone", "mfma_and_fma_two_waves", "mfma_and_fma_one_wave")):
+        us = timed(lambda: _check(lib.er_hip_probe_mfma_valu(ctx.handle, stream.handle, mode, iters, sink.raw)))
+        out[f"overlap_{tag}"] = {"us": us, "ns_per_iteration": us * 1000.0 / iters, "iters": iters}
+        log(f"overlap {tag}: {us * 1000.0 / iters:.1f} ns per iteration (8 MFMA and/or 64 FMA per wave)")
+    sink.free()
     e0.destroy()
     e1.destroy()
     counter.free()

@@ -207,6 +207,8 @@ SIGNATURES = {
     "er_hip_probe_stream_read": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, _u32, er_buffer]),
     "er_hip_probe_empty": (C.c_int, [_ctx_p, _stream]),
     "er_hip_probe_grid_barrier": (C.c_int, [_ctx_p, _stream, _u32, _u32, _u32, er_buffer, er_buffer]),
+    "er_hip_probe_lds_read": (C.c_int, [_ctx_p, _stream, _u32, _u32, er_buffer]),
+    "er_hip_probe_mfma_valu": (C.c_int, [_ctx_p, _stream, _u32, _u32, er_buffer]),
     "er_hip_encode_projection": (
         C.c_int, [_ctx_p, _stream, C.POINTER(er_tensor_storage), er_buffer, er_buffer, _u32]),
 }

@@ -86,7 +86,9 @@ using er_detail::fail;
     X(GEMML_Q8_0_R1, "er_gemml_q8_0_r1")                                               \
     X(PROBE_STREAM_READ, "er_probe_stream_read")                                       \
     X(PROBE_EMPTY, "er_probe_empty")                                                   \
-    X(PROBE_GRID_BARRIER, "er_probe_grid_barrier")
+    X(PROBE_GRID_BARRIER, "er_probe_grid_barrier")                                     \
+    X(PROBE_LDS_READ, "er_probe_lds_read")                                             \
+    X(PROBE_MFMA_VALU, "er_probe_mfma_valu")
 
 enum KernelId {
 #define ER_ENUM(id, name) K_##id,
@@ -1706,6 +1708,39 @@ er_status er_hip_encode_projection(er_hip_ctx *ctx, er_stream stream,
 }  // extern "C"
 
 // ---- measurement kernels (include/er_hip_probe.h) ----
+
+// One workgroup per CU for the per-CU rate probes: 96 KB of LDS each, so no
+// second workgroup fits beside it.
+constexpr uint32_t kProbeCuLds = 96u * 1024u;
+
+er_status er_hip_probe_lds_read(er_hip_ctx *ctx, er_stream stream, uint32_t waves, uint32_t iters, er_buffer sink) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if ((waves != 4 && waves != 8 && waves != 16) || !sink.data || !aligned(sink.data, 4) ||
+        sink.length < (uint64_t)ctx->cu_count * 1024u * 4u)
+        return fail(ER_ERR_INVALID_ARGUMENT, "lds read probe: waves %u (4, 8 or 16), sink %llu bytes", waves,
+                    (unsigned long long)sink.length);
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    uint32_t never = 0x9e3779b9u;
+    void *args[] = {&iters, &never, (void *)&sink.data};
+    return launch(ctx, K_PROBE_LDS_READ, dim3((uint32_t)ctx->cu_count, 1, 1), dim3(64u * waves, 1, 1), kProbeCuLds,
+                  stream, args);
+}
+
+er_status er_hip_probe_mfma_valu(er_hip_ctx *ctx, er_stream stream, uint32_t mode, uint32_t iters, er_buffer sink) {
+    er_status st = check_ctx(ctx);
+    if (st != ER_OK) return st;
+    if (mode > 3u || !sink.data || !aligned(sink.data, 4) || sink.length < (uint64_t)ctx->cu_count * 512u * 4u)
+        return fail(ER_ERR_INVALID_ARGUMENT, "mfma/valu probe: mode %u (0..3), sink %llu bytes", mode,
+                    (unsigned long long)sink.length);
+    st = bind_device(ctx);
+    if (st != ER_OK) return st;
+    uint32_t never = 0x9e3779b9u;
+    void *args[] = {&mode, &iters, &never, (void *)&sink.data};
+    return launch(ctx, K_PROBE_MFMA_VALU, dim3((uint32_t)ctx->cu_count, 1, 1), dim3(512, 1, 1), kProbeCuLds, stream,
+                  args);
+}
 
 er_status er_hip_probe_stream_read(er_hip_ctx *ctx, er_stream stream, er_buffer src, uint64_t bytes,
                                    uint32_t workgroups, er_buffer sink) {

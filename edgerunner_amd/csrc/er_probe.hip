@@ -56,3 +56,89 @@ extern "C" __global__ void __launch_bounds__(64)
     __hip_atomic_fetch_add(out, polls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_fetch_add(out + 1, timeouts, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// ---------------------------------------------------------------------------
+// Per-CU rates the prefill GEMM design rests on.  Both run one workgroup per
+// CU (the host asks for 96 KB of LDS, so no second workgroup fits beside it)
+// and keep their results alive through a store that real data never takes.
+// ---------------------------------------------------------------------------
+typedef __bf16 pb_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float pb_f32x16 __attribute__((ext_vector_type(16)));
+
+// LDS read rate: every wave issues, per iteration, 8 independent 16-byte-per-
+// lane reads laid out like the GEMM's A fragments (lane l: row l % 32 of a
+// 144-byte pitch, column 16 (l / 32)), and XORs them into its result.
+extern "C" __global__ void __launch_bounds__(1024)
+    er_probe_lds_read(uint32_t iters, uint32_t never, uint32_t *__restrict__ sink) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t plds[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    for (uint32_t i = tid; i < 16384u; i += blockDim.x) ((uint32_t *)plds)[i] = i * 2654435761u;
+    __syncthreads();
+    u32x4 x = {0u, 0u, 0u, 0u};
+    const uint32_t base = (lane & 31u) * 144u + 16u * (lane >> 5);
+    uint32_t off = (wave * 1024u) & 32767u;
+    for (uint32_t it = 0; it < iters; ++it) {
+#pragma unroll
+        for (uint32_t u = 0; u < 8u; ++u) x ^= *(const u32x4 *)(plds + ((base + ((off + 4608u * u) & 16383u)) & ~15u));
+        off += 64u;
+        asm volatile("" : "+v"(off));
+    }
+    const uint32_t v = x.x ^ x.y ^ x.z ^ x.w;
+    if (v == never) sink[blockIdx.x * blockDim.x + tid] = v;
+}
+
+// Matrix-core / vector-ALU overlap, 8 waves (2 per SIMD: waves w and w + 4).
+// Per iteration a wave of role MFMA issues 8 v_mfma_f32_32x32x16_bf16 on
+// independent accumulators, a wave of role VALU 64 independent fp32 FMAs, and
+// a wave of role BOTH the two interleaved (one matrix instruction, then 8
+// FMAs).  mode: 0 waves 0-3 MFMA, 4-7 idle; 1 waves 0-3 VALU; 2 waves 0-3
+// MFMA and 4-7 VALU (the two on each SIMD from different waves); 3 waves 0-3
+// BOTH (from one wave).
+extern "C" __global__ void __launch_bounds__(512)
+    er_probe_mfma_valu(uint32_t mode, uint32_t iters, uint32_t never, uint32_t *__restrict__ sink) {
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t role = wave < 4u ? (mode == 1u ? 2u : mode == 3u ? 3u : 1u) : (mode == 2u ? 2u : 0u);
+    pb_f32x16 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[j][q] = 0.0f;
+    pb_bf16x8 a, b;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        a[q] = (__bf16)(float)(tid + q);
+        b[q] = (__bf16)(float)(3 * q);
+    }
+    float y[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) y[k] = (float)(tid + k);
+    const float m = 1.0001f, c = 0.5f;
+    if (role == 1u) {
+        for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+    } else if (role == 2u) {
+        for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) y[k] = __builtin_fmaf(y[k], m, c);
+    } else if (role == 3u) {
+        for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) y[k] = __builtin_fmaf(y[k], m, c);
+            }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += y[k];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) s += acc[j][q];
+    const uint32_t v = __builtin_bit_cast(uint32_t, s);
+    if (v == never) sink[blockIdx.x * 512u + tid] = v;
+}

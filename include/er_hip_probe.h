@@ -31,6 +31,16 @@ er_status er_hip_probe_empty(er_hip_ctx *ctx, er_stream stream);
 er_status er_hip_probe_grid_barrier(er_hip_ctx *ctx, er_stream stream, uint32_t workgroups, uint32_t rounds,
                                     uint32_t spin_limit, er_buffer counter, er_buffer out);
 
+/* LDS read rate: one workgroup of `waves` (4, 8 or 16) waves per CU, each
+ * wave `iters` x 8 independent 16-byte-per-lane LDS reads in the prefill
+ * GEMM's A-fragment layout; sink holds CU count * 1024 uint32. */
+er_status er_hip_probe_lds_read(er_hip_ctx *ctx, er_stream stream, uint32_t waves, uint32_t iters, er_buffer sink);
+/* Matrix-core / vector-ALU overlap: one 8-wave workgroup per CU, `iters`
+ * iterations of 8 bf16 MFMAs and/or 64 fp32 FMAs per wave; mode 0 MFMA
+ * alone, 1 FMAs alone, 2 both from different waves of each SIMD, 3 both
+ * interleaved in one wave; sink holds CU count * 512 uint32. */
+er_status er_hip_probe_mfma_valu(er_hip_ctx *ctx, er_stream stream, uint32_t mode, uint32_t iters, er_buffer sink);
+
 #ifdef __cplusplus
 }
 #endif
