@@ -83,6 +83,27 @@ def test_baseline_shapes_sampled(gemm, fmt, N):
     check(gemm, fmt, T, N, K, seed=1, rows=rows)
 
 
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+@pytest.mark.parametrize("N", [4096, 14336])
+def test_baseline_shapes_every_row(gemm, fmt, N):
+    """BASELINE config 4 at full size, every one of the 512 token rows: against
+    the float64 product of X and the bf16-rounded dequantised weights (the
+    kernel's own arithmetic, <= 1e-5 relative L2 over all of Y and per row
+    <= 1e-4) and against the oracle's per-token GEMV (<= 1e-2 relative L2)."""
+    T, K = 512, 4096
+    W, X = case(fmt, T, N, K, 2)
+    Y = gemm.execute(fmt, W, X, T, N, K)
+    Xf = bf16_to_f32(X).reshape(T, K)
+    exact = Xf.astype(np.float64) @ bf16_round(rn.weights_f32(fmt, W, N, K)).astype(np.float64).T
+    assert rel_l2(Y, exact) < 1e-5
+    per_row = np.linalg.norm(Y - exact, axis=1) / np.maximum(np.linalg.norm(exact, axis=1), 1e-30)
+    assert per_row.max() < 1e-4, int(per_row.argmax())
+    oracle = ref.gemm(fmt, W, X, T, N, K, threads=ref.max_threads()).reshape(T, N)
+    err = rel_l2(Y, oracle)
+    print(f"{fmt} 512x{N}x4096 all rows: rel_l2 vs oracle {err:.2e}")
+    assert err < 1e-2
+
+
 def test_one_hot_tokens_extract_weight_rows(gemm):
     """X = identity rows: Y[t] is column t of the dequantised (bf16-rounded) W."""
     T, N, K = 256, 64, 256
