@@ -104,6 +104,18 @@ def test_baseline_shapes_every_row(gemm, fmt, N):
     assert err < 1e-2
 
 
+@pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
+def test_unsplit_gemm_is_deterministic(gemm, fmt):
+    """Shapes that run without a K split (no fp32 atomics) give bit-identical Y
+    on every call; split-K shapes add their partial tiles with atomics in an
+    order that varies, so only those may differ in the last bits."""
+    T, N, K = 512, 14336, 1024
+    W, X = case(fmt, T, N, K, 3)
+    first = gemm.execute(fmt, W, X, T, N, K)
+    for _ in range(3):
+        assert np.array_equal(gemm.execute(fmt, W, X, T, N, K).view(np.uint32), first.view(np.uint32))
+
+
 def test_one_hot_tokens_extract_weight_rows(gemm):
     """X = identity rows: Y[t] is column t of the dequantised (bf16-rounded) W."""
     T, N, K = 256, 64, 256
