@@ -950,7 +950,10 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // Row assignment: step i of lane group (wave, g) in workgroup b is row
 // (i * gridDim.x + b) * STEP + wave * G + g, G = 64 / LPR rows per wave step,
 // STEP = ER_CU_WAVES * G rows per workgroup step: the workgroups' steps
-// interleave over the matrix.
+// interleave over the matrix.  Q8_0 (F::SPREAD) puts the waves of a workgroup
+// a grid apart instead: row ((i * ER_CU_WAVES + wave) * gridDim.x + b) * G + g
+// (the same rows overall; 2% faster for Q8_0 at 14336 x 4096, no gain for
+// Q4_K or Q6_K).
 // Per-row arithmetic (slot order, lane reduction) is that of the family-1
 // kernel with the same LPR and NS.
 
@@ -972,6 +975,7 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // (Xs), and the slot's contribution.
 struct CuQ4K {
     static constexpr int FMT = ER_FMT_Q4_K;
+    static constexpr bool SPREAD = false;  // row assignment (family comment)
     static constexpr int NLD = 3;    // load instructions per slot
     static constexpr int UNITS = 3;  // units in flight (ER_CU_UNITS)
     struct Wt {
@@ -1006,6 +1010,7 @@ struct CuQ4K {
 
 struct CuQ8 {
     static constexpr int FMT = ER_FMT_Q8_0;
+    static constexpr bool SPREAD = true;
     static constexpr int NLD = 5;
     static constexpr int UNITS = 2;
     using Wt = Q8Slot;
@@ -1028,6 +1033,7 @@ struct CuQ8 {
 // 2-byte-aligned vector load per field (ld16_u2 / ld8_u2).
 struct CuQ6K {
     static constexpr int FMT = ER_FMT_Q6_K;
+    static constexpr bool SPREAD = false;
     static constexpr int NLD = 5;
     static constexpr int UNITS = 3;
     struct Wt {
@@ -1130,6 +1136,7 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     constexpr uint32_t STG = (NS == 1 || NS >= 5) ? ER_CU_WAVES : 4u;
     constexpr bool EARLY = STG == ER_CU_WAVES;
     static_assert(D0 * F::NLD < 64, "the early weight loads fit the load counter");
+    static_assert(!(TOP1 && F::SPREAD), "the top-1 epilogue maps local rows with the neighbouring-row assignment");
     x += (size_t)blockIdx.y * K;
     y += (size_t)blockIdx.y * M;
     // wave index as a scalar: the staging branch and the step count are wave-uniform
@@ -1144,7 +1151,12 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     const uint32_t J = rowsPerWg / STEP;  // steps per workgroup (rows past M are skipped)
     const uint32_t JR = JC > 0 ? (uint32_t)JC : max((J + UNR - 1u) / UNR * UNR, (uint32_t)UNR);
     const uint32_t laneRow = wave * G + g;  // row within a step
-    auto rowOf = [&](uint32_t i) { return (i * gridDim.x + blockIdx.x) * STEP + laneRow; };
+    // row of lane group (w, gg)'s step i
+    auto rowAt = [&](uint32_t i, uint32_t w, uint32_t gg) {
+        return F::SPREAD ? ((i * ER_CU_WAVES + w) * gridDim.x + blockIdx.x) * G + gg
+                         : (i * gridDim.x + blockIdx.x) * STEP + w * G + gg;
+    };
+    auto rowOf = [&](uint32_t i) { return rowAt(i, wave, g); };
     const size_t rowBytes = F::row_bytes(K);
     uint32_t *xraw = lds + xl_lds_bytes(K) / 4u;  // 16-byte aligned for K % 256 == 0
 
@@ -1284,11 +1296,11 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
 #pragma unroll
         for (int q = 0; q < NPARK; ++q) sp[q] = 0.0f;
         const uint32_t ln = lane_id();
-        const uint32_t fRow = wave * G + ln / LPR, fli = ln % LPR;
+        const uint32_t fg = ln / LPR, fli = ln % LPR;
         nf_terms<NPARK>(
             [&](int q, uint32_t k) {
                 const uint32_t st = (uint32_t)q * LPR + fli;
-                const uint32_t row = min((st * gridDim.x + blockIdx.x) * STEP + fRow, M - 1u);
+                const uint32_t row = min(rowAt(st, wave, fg), M - 1u);
                 return weight_at<F::FMT>(W + (size_t)row * rowBytes, k);
             },
             [&](uint32_t k) { return ((const float *)xraw)[k]; }, X.x16, K >> 4, 0u, 1u, sp, hits);
