@@ -763,9 +763,11 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
         if (r) {
             void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K};
             // GemmL<Q4K, R>::LDS: 4 X stages of 18432 bytes + the weight stages
-            const uint32_t wst = (r == 2 ? 256u : 128u) * (f == Fmt::Q4_K ? 48u : 80u);
+            // (+ 4 Q4_K header slots of 16 bytes per row)
+            const uint32_t tn = r == 2 ? 256u : 128u;
+            const uint32_t wst = tn * (f == Fmt::Q4_K ? 32u : 80u);
             const uint32_t nw = r == 2 ? (f == Fmt::Q4_K ? 6u : 4u) : (f == Fmt::Q4_K ? 8u : 6u);
-            const uint32_t lds = 4u * 18432u + nw * wst;
+            const uint32_t lds = 4u * 18432u + nw * wst + (f == Fmt::Q4_K ? 4u * tn * 16u : 0u);
             if (lds > ctx->info.lds_per_workgroup)
                 return fail(ER_ERR_ENCODING_FAILED, "GEMM: %u B of LDS per workgroup needed, %u available", lds,
                             (unsigned)ctx->info.lds_per_workgroup);
