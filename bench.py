@@ -74,6 +74,8 @@ GEMM_WORKLOADS = [
     ("q8_0_gemm_512x14336x4096", "q8_0", 512, 14336, 4096, 4),
 ]
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+PEAK_SCLK_MHZ = 2400.0  # the engine clock the MFMA peak is quoted at
+CLOCK_LAUNCHES = 5      # back-to-back stamped GEMM launches per workload; the last one is read
 
 
 def log(msg: str) -> None:
@@ -307,6 +309,7 @@ def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warm
     stream.synchronize()
     us = e0.elapsed_ms(e1) * 1000.0 / steps
     y = yb.download(np.float32, count=min(T * N, 1 << 20), stream=stream)
+    clock = gemm_clock(ctx, stream, fmt, wbufs, xb, yb, T, N, K)
     graph.destroy()
     for b in wbufs:
         b.free()
@@ -317,9 +320,42 @@ def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warm
     stream.destroy()
     flops = 2.0 * T * N * K
     tflops = flops / (us * 1e-6) / 1e12
-    return {"fmt": fmt, "T": T, "N": N, "K": K, "us_per_call": us, "TFLOPs": tflops,
-            "frac_of_mfma_bf16_peak": tflops / MFMA_BF16_PEAK_TFLOPS,
-            "min_bytes": gemm_min_bytes(fmt, T, N, K), "y_finite": bool(np.all(np.isfinite(y)))}
+    out = {"fmt": fmt, "T": T, "N": N, "K": K, "us_per_call": us, "TFLOPs": tflops,
+           "frac_of_mfma_bf16_peak": tflops / MFMA_BF16_PEAK_TFLOPS,
+           "min_bytes": gemm_min_bytes(fmt, T, N, K), "y_finite": bool(np.all(np.isfinite(y)))}
+    if clock:
+        out.update(clock)
+        out["frac_of_mfma_bf16_peak_at_clock"] = tflops / (MFMA_BF16_PEAK_TFLOPS * clock["sclk_mhz"] / PEAK_SCLK_MHZ)
+    return out
+
+
+def gemm_clock(ctx, stream, fmt: str, wbufs, xb, yb, T: int, N: int, K: int) -> dict:
+    """The shader clock the GEMM's workgroups run at: CLOCK_LAUNCHES
+    back-to-back launches through er_hip_probe_gemm_clock (the same kernel
+    and result as the product call, plus per-workgroup stamps of the 100 MHz
+    real-time and the shader-clock counters); the last launch's workgroups
+    give d(shader clock) / d(real time).  Empty where the loader-specialised
+    kernel does not take the shape."""
+    import ctypes as C
+    from edgerunner_amd import _ffi
+    lib = _ffi.load()
+    nT = -(-T // 128)
+    stamps = ctx.alloc(32 * nT * -(-N // 128))  # enough for either tile height
+    items = C.c_uint32(0)
+    typ = 12 if fmt == "q4_k" else 8  # ER_TYPE_Q4_K / ER_TYPE_Q8_0
+    try:
+        for i in range(CLOCK_LAUNCHES):
+            st = lib.er_hip_probe_gemm_clock(ctx.handle, stream.handle, typ, wbufs[i % len(wbufs)].raw, xb.raw, yb.raw,
+                                             T, N, K, stamps.raw, C.byref(items))
+            if st != 0:
+                return {}
+        stream.synchronize()
+        s = stamps.download(np.uint64, count=4 * items.value, stream=stream).reshape(-1, 4).astype(np.float64)
+    finally:
+        stamps.free()
+    mhz = (s[:, 3] - s[:, 2]) / (s[:, 1] - s[:, 0]) * 100.0
+    return {"sclk_mhz": float(np.median(mhz)), "sclk_mhz_min": float(mhz.min()), "sclk_mhz_max": float(mhz.max()),
+            "workgroup_us_median": float(np.median(s[:, 1] - s[:, 0]) / 100.0), "clock_workgroups": int(items.value)}
 
 
 def bench_chain(ctx, steps: int, warmup: int) -> dict:
@@ -922,8 +958,10 @@ def main() -> int:
         r = bench_gemm(ctx, fmt, T, N, K, cfg, max(20, args.steps // 4), min(args.warmup, 5))
         r["traffic_bytes"] = load_traffic(name)
         results[name] = r
+        clk = (f"; workgroups ran at {r['sclk_mhz']:.0f} MHz (min {r['sclk_mhz_min']:.0f}), "
+               f"{100 * r['frac_of_mfma_bf16_peak_at_clock']:.1f}% of the peak at that clock") if "sclk_mhz" in r else ""
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['TFLOPs']:.1f} TFLOP/s "
-            f"({100 * r['frac_of_mfma_bf16_peak']:.1f}% of bf16 dense peak)")
+            f"({100 * r['frac_of_mfma_bf16_peak']:.1f}% of bf16 dense peak){clk}")
 
     if args.workloads == "all" or "gguf_upload" in args.workloads:
         log("gguf_upload_1gib: running")

@@ -209,6 +209,8 @@ SIGNATURES = {
     "er_hip_probe_grid_barrier": (C.c_int, [_ctx_p, _stream, _u32, _u32, _u32, er_buffer, er_buffer]),
     "er_hip_probe_lds_read": (C.c_int, [_ctx_p, _stream, _u32, _u32, er_buffer]),
     "er_hip_probe_mfma_valu": (C.c_int, [_ctx_p, _stream, _u32, _u32, er_buffer]),
+    "er_hip_probe_gemm_clock": (C.c_int, [_ctx_p, _stream, C.c_int, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32,
+                                          er_buffer, C.POINTER(C.c_uint32)]),
     "er_hip_encode_projection": (
         C.c_int, [_ctx_p, _stream, C.POINTER(er_tensor_storage), er_buffer, er_buffer, _u32]),
 }

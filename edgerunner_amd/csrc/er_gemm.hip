@@ -726,10 +726,19 @@ ER_DEV void gemml_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// stamps (null in the product path): thread 0 of each work item's
+// workgroup writes stamps[4 item ..] = the 100 MHz real-time counter and the
+// shader-clock counter at its start and after its epilogue, so the clock the
+// workgroup ran at is d(shader clock) / d(real time) x 100 MHz.
 template <bool Q4K, int R>
 ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
-                    uint32_t T, uint32_t N, uint32_t K) {
+                    uint32_t T, uint32_t N, uint32_t K, uint64_t *__restrict__ stamps) {
     using G = GemmL<Q4K, R>;
+    uint64_t rt0 = 0, ct0 = 0;
+    if (stamps) {
+        rt0 = __builtin_amdgcn_s_memrealtime();
+        ct0 = __builtin_amdgcn_s_memtime();
+    }
     extern __shared__ __attribute__((aligned(16))) uint8_t glds[];
     uint8_t *xs = glds;                             // NX X stages
     uint8_t *wsm = glds + G::NX * ER_GEMML_XSTAGE;  // NW weight stages
@@ -956,13 +965,20 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
                 *(float *)((uint8_t *)Y + (t * N + nc) * 4u) = acc[f][i][r];
             }
     }
+    if (stamps && threadIdx.x == 0) {
+        const uint64_t rt1 = __builtin_amdgcn_s_memrealtime(), ct1 = __builtin_amdgcn_s_memtime();
+        stamps[4u * item + 0u] = rt0;
+        stamps[4u * item + 1u] = rt1;
+        stamps[4u * item + 2u] = ct0;
+        stamps[4u * item + 3u] = ct1;
+    }
 }
 
 #define ER_GEMML_ENTRY(name, q4k, r)                                                                         \
     extern "C" __global__ void __launch_bounds__(512, 1)                                                     \
         name(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y, uint32_t T, \
-             uint32_t N, uint32_t K) {                                                                       \
-        gemm_ls<q4k, r>(W, X, Y, T, N, K);                                                                   \
+             uint32_t N, uint32_t K, uint64_t *__restrict__ stamps) {                                        \
+        gemm_ls<q4k, r>(W, X, Y, T, N, K, stamps);                                                           \
     }
 
 ER_GEMML_ENTRY(er_gemml_q4k, true, 2)

@@ -720,8 +720,50 @@ er_status encode_quantize_q8_0(er_hip_ctx *ctx, er_stream stream, er_buffer src,
 
 // Prefill GEMM: validation mirrors the GEMV rules (K multiple of the block,
 // buffer lengths), then a grid of ceil(N/128) x ceil(T/TT) workgroups.
+// Loader-specialised kernel: 256 (or 128) weight rows x 128 tokens per
+// workgroup, no K split, so it runs where those tiles alone give (nearly)
+// every CU a workgroup (256-row tiles), or at least half of them (128-row
+// tiles).  r = 0: another kernel takes the shape.
+struct GemmLPlan {
+    int r = 0;           // 32-row blocks per compute wave (tile of 128 r rows)
+    uint64_t tiles = 0;  // work items = workgroups doing work
+};
+GemmLPlan plan_gemml(const er_hip_ctx *ctx, uint32_t T, uint32_t N, uint32_t K) {
+    GemmLPlan p;
+    const uint64_t nT = (T + 127u) / 128u;
+    const uint64_t tiles2 = nT * ((N + 255u) / 256u), tiles1 = nT * ((N + 127u) / 128u);
+    const uint64_t cu = (uint64_t)ctx->cu_count;
+    const bool fits = K % 256u == 0 && (uint64_t)T * N * 4u < (1ull << 32) && tiles1 <= 8ull * 65535u;
+    if (fits && ctx->gemm_variant == 0) p.r = 4u * tiles2 >= 3u * cu ? 2 : 2u * tiles1 >= cu ? 1 : 0;
+    if (fits && ctx->gemm_variant == 4) p.r = 2;
+    if (fits && ctx->gemm_variant == 5) p.r = 1;
+    p.tiles = p.r == 2 ? tiles2 : p.r == 1 ? tiles1 : 0;
+    return p;
+}
+
+// stamps: null, or 32 bytes per work item (the kernel's clock stamps)
+er_status launch_gemml(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_buffer x, er_buffer y, uint32_t T,
+                       uint32_t N, uint32_t K, const GemmLPlan &p, uint64_t *stamps) {
+    void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K, &stamps};
+    // GemmL<Q4K, R>::LDS: 4 X stages of 18432 bytes + the weight stages
+    // (+ 4 Q4_K header slots of 16 bytes per row)
+    const uint32_t tn = p.r == 2 ? 256u : 128u;
+    const uint32_t wst = tn * (f == Fmt::Q4_K ? 32u : 80u);
+    const uint32_t nw = p.r == 2 ? (f == Fmt::Q4_K ? 6u : 4u) : (f == Fmt::Q4_K ? 8u : 6u);
+    const uint32_t lds = 4u * 18432u + nw * wst + (f == Fmt::Q4_K ? 4u * tn * 16u : 0u);
+    if (lds > ctx->info.lds_per_workgroup)
+        return fail(ER_ERR_ENCODING_FAILED, "GEMM: %u B of LDS per workgroup needed, %u available", lds,
+                    (unsigned)ctx->info.lds_per_workgroup);
+    const KernelId k = f == Fmt::Q4_K ? (p.r == 2 ? K_GEMML_Q4K : K_GEMML_Q4K_R1)
+                                      : (p.r == 2 ? K_GEMML_Q8_0 : K_GEMML_Q8_0_R1);
+    return launch(ctx, k, dim3((uint32_t)(8u * ((p.tiles + 7u) / 8u)), 1, 1), dim3(512, 1, 1), lds, stream, args);
+}
+
+// stamps (the clock probe only): the loader-specialised kernel must take the
+// shape, and stamps receives its per-work-item clock stamps
 er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_buffer x,
-                      er_buffer y, uint32_t T, uint32_t N, uint32_t K) {
+                      er_buffer y, uint32_t T, uint32_t N, uint32_t K, const er_buffer *stamps = nullptr,
+                      uint32_t *stampItems = nullptr) {
     const uint32_t kmul = f == Fmt::Q4_K ? 256u : 64u;
     if (K == 0 || K % kmul != 0)
         return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s GEMM: K=%u must be a positive multiple of %u",
@@ -747,37 +789,17 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
                     fmt_name(f), (unsigned long long)need, (unsigned long long)T * K * 2u);
     st = bind_device(ctx);
     if (st != ER_OK) return st;
-    {
-        // loader-specialised kernel: 256 (or 128) weight rows x 128 tokens per
-        // workgroup, no K split, so it runs where those tiles alone give
-        // (nearly) every CU a workgroup (256-row tiles), or at least half of
-        // them (128-row tiles)
-        const uint64_t nT = (T + 127u) / 128u;
-        const uint64_t tiles2 = nT * ((N + 255u) / 256u), tiles1 = nT * ((N + 127u) / 128u);
-        const uint64_t cu = (uint64_t)ctx->cu_count;
-        const bool fits = K % 256u == 0 && (uint64_t)T * N * 4u < (1ull << 32) && tiles1 <= 8ull * 65535u;
-        int r = 0;
-        if (fits && ctx->gemm_variant == 0) r = 4u * tiles2 >= 3u * cu ? 2 : 2u * tiles1 >= cu ? 1 : 0;
-        if (fits && ctx->gemm_variant == 4) r = 2;
-        if (fits && ctx->gemm_variant == 5) r = 1;
-        if (r) {
-            void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K};
-            // GemmL<Q4K, R>::LDS: 4 X stages of 18432 bytes + the weight stages
-            // (+ 4 Q4_K header slots of 16 bytes per row)
-            const uint32_t tn = r == 2 ? 256u : 128u;
-            const uint32_t wst = tn * (f == Fmt::Q4_K ? 32u : 80u);
-            const uint32_t nw = r == 2 ? (f == Fmt::Q4_K ? 6u : 4u) : (f == Fmt::Q4_K ? 8u : 6u);
-            const uint32_t lds = 4u * 18432u + nw * wst + (f == Fmt::Q4_K ? 4u * tn * 16u : 0u);
-            if (lds > ctx->info.lds_per_workgroup)
-                return fail(ER_ERR_ENCODING_FAILED, "GEMM: %u B of LDS per workgroup needed, %u available", lds,
-                            (unsigned)ctx->info.lds_per_workgroup);
-            const uint64_t tiles = r == 2 ? tiles2 : tiles1;
-            const KernelId k = f == Fmt::Q4_K ? (r == 2 ? K_GEMML_Q4K : K_GEMML_Q4K_R1)
-                                              : (r == 2 ? K_GEMML_Q8_0 : K_GEMML_Q8_0_R1);
-            return launch(ctx, k, dim3((uint32_t)(8u * ((tiles + 7u) / 8u)), 1, 1), dim3(512, 1, 1), lds, stream,
-                          args);
-        }
+    const GemmLPlan lp = plan_gemml(ctx, T, N, K);
+    if (stamps) {
+        if (!lp.r)
+            return fail(ER_ERR_INVALID_ARGUMENT, "GEMM clock probe: the loader-specialised kernel does not take "
+                        "T=%u N=%u K=%u", T, N, K);
+        if (!stamps->data || !aligned(stamps->data, 8) || stamps->length < 32u * lp.tiles)
+            return fail(ER_ERR_INVALID_ARGUMENT, "GEMM clock probe: stamps need %llu bytes (8-byte aligned), %llu given",
+                        (unsigned long long)(32u * lp.tiles), (unsigned long long)stamps->length);
+        if (stampItems) *stampItems = (uint32_t)lp.tiles;
     }
+    if (lp.r) return launch_gemml(ctx, stream, f, W, x, y, T, N, K, lp, stamps ? (uint64_t *)stamps->data : nullptr);
     // Tile height TT (tokens) and K split SK: 128-token tiles (64 for short
     // inputs), then split K until the grid gives every CU a workgroup
     // (measured on MI355X: 512x14336x4096 is fastest unsplit, 512x4096x4096
@@ -1760,6 +1782,17 @@ er_status er_hip_probe_stream_read(er_hip_ctx *ctx, er_stream stream, er_buffer 
     uint32_t never = 0x9e3779b9u;
     void *args[] = {&src.data, &n16, &never, &sink.data};
     return launch(ctx, K_PROBE_STREAM_READ, dim3(workgroups, 1, 1), dim3(256, 1, 1), 0, stream, args);
+}
+
+er_status er_hip_probe_gemm_clock(er_hip_ctx *ctx, er_stream stream, er_tensor_type type, er_buffer weight,
+                                  er_buffer x_bf16, er_buffer y, uint32_t tokens, uint32_t N, uint32_t K,
+                                  er_buffer stamps, uint32_t *items) {
+    if (type != ER_TYPE_Q4_K && type != ER_TYPE_Q8_0)
+        return fail(ER_ERR_INVALID_ARGUMENT, "GEMM clock probe: type %d is not Q4_K or Q8_0", (int)type);
+    if (!items) return fail(ER_ERR_INVALID_ARGUMENT, "GEMM clock probe: null items");
+    *items = 0;
+    return encode_gemm(ctx, stream, type == ER_TYPE_Q4_K ? Fmt::Q4_K : Fmt::Q8_0, weight, x_bf16, y, tokens, N, K,
+                       &stamps, items);
 }
 
 er_status er_hip_probe_empty(er_hip_ctx *ctx, er_stream stream) {

@@ -21,6 +21,17 @@ extern "C" {
  * occur with real data, so the loads cannot be removed). */
 er_status er_hip_probe_stream_read(er_hip_ctx *ctx, er_stream stream, er_buffer src, uint64_t bytes,
                                    uint32_t workgroups, er_buffer sink);
+/* The prefill GEMM (er_hip_gemm_q4_k / _q8_0 for type ER_TYPE_Q4_K /
+ * ER_TYPE_Q8_0, same arguments and result) where its loader-specialised
+ * kernel takes the shape (ER_ERR_INVALID_ARGUMENT otherwise), with clock
+ * stamps: *items receives the number of work items and stamps (8-byte
+ * aligned, at least 32 bytes per item) four uint64 per item: the 100 MHz
+ * real-time counter and the shader-clock counter at the start of its
+ * workgroup and after its epilogue.  The clock a workgroup ran at is
+ * (s[3] - s[2]) / (s[1] - s[0]) x 100 MHz. */
+er_status er_hip_probe_gemm_clock(er_hip_ctx *ctx, er_stream stream, er_tensor_type type, er_buffer weight,
+                                  er_buffer x_bf16, er_buffer y, uint32_t tokens, uint32_t N, uint32_t K,
+                                  er_buffer stamps, uint32_t *items);
 /* One launch of an empty 64-thread kernel. */
 er_status er_hip_probe_empty(er_hip_ctx *ctx, er_stream stream);
 /* `rounds` grid-wide barriers across `workgroups` single-wave workgroups

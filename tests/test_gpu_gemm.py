@@ -141,3 +141,46 @@ def test_validation(ctx, gemm):
         gemm.encodeQ4K(None, wb, xb, yb, T, N, K)
     with pytest.raises(InvalidVectorShape):
         gemm.encodeQ8_0(None, wb, xb, ctx.alloc(T * N * 4), T, N, 96)
+
+
+@pytest.mark.parametrize("fmt,T,N,items", [("q4_k", 512, 4096, 128), ("q8_0", 512, 14336, 224)])
+def test_clock_probe(ctx, gemm, fmt, T, N, items):
+    """er_hip_probe_gemm_clock runs the product kernel: Y is bit-identical to
+    the plain call, one stamp set per work item (128-row tiles at N = 4096,
+    256-row tiles at 14336), each with both counters advancing and a clock
+    between 100 MHz and 3.5 GHz."""
+    import ctypes as C
+    from edgerunner_amd import _ffi
+    K = 1024
+    W, X = case(fmt, T, N, K, 5)
+    want = gemm.execute(fmt, W, X, T, N, K)
+    lib = _ffi.load()
+    typ = 12 if fmt == "q4_k" else 8
+    wb, xb, yb = ctx.upload(W), ctx.upload(X), ctx.alloc(4 * T * N)
+    stamps = ctx.alloc(32 * items)
+    n = C.c_uint32(0)
+    try:
+        assert lib.er_hip_probe_gemm_clock(ctx.handle, None, typ, wb.raw, xb.raw, yb.raw, T, N, K, stamps.raw,
+                                           C.byref(n)) == 0
+        ctx.synchronize()
+        assert n.value == items
+        assert np.array_equal(yb.download(np.float32).view(np.uint32), want.reshape(-1).view(np.uint32))
+        s = stamps.download(np.uint64).reshape(-1, 4)
+        assert np.all(s[:, 1] > s[:, 0]) and np.all(s[:, 3] > s[:, 2])
+        mhz = (s[:, 3] - s[:, 2]).astype(np.float64) / (s[:, 1] - s[:, 0]).astype(np.float64) * 100.0
+        print(f"{fmt} {T}x{N}x{K}: workgroups at {np.median(mhz):.0f} MHz (min {mhz.min():.0f})")
+        assert np.all((mhz > 100.0) & (mhz < 3500.0))
+        # too few stamps, a shape the kernel does not take, a format without it
+        small = ctx.alloc(32 * items - 8)
+        try:
+            assert lib.er_hip_probe_gemm_clock(ctx.handle, None, typ, wb.raw, xb.raw, yb.raw, T, N, K, small.raw,
+                                               C.byref(n)) != 0
+        finally:
+            small.free()
+        assert lib.er_hip_probe_gemm_clock(ctx.handle, None, typ, wb.raw, xb.raw, yb.raw, 33, 64, K, stamps.raw,
+                                           C.byref(n)) != 0
+        assert lib.er_hip_probe_gemm_clock(ctx.handle, None, 14, wb.raw, xb.raw, yb.raw, T, N, K, stamps.raw,
+                                           C.byref(n)) != 0
+    finally:
+        for b in (wb, xb, yb, stamps):
+            b.free()
