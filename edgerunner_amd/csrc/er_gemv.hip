@@ -951,9 +951,10 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // (i * gridDim.x + b) * STEP + wave * G + g, G = 64 / LPR rows per wave step,
 // STEP = ER_CU_WAVES * G rows per workgroup step: the workgroups' steps
 // interleave over the matrix.  Q8_0 (F::SPREAD) puts the waves of a workgroup
-// a grid apart instead: row ((i * ER_CU_WAVES + wave) * gridDim.x + b) * G + g
-// (the same rows overall; 2% faster for Q8_0 at 14336 x 4096, no gain for
-// Q4_K or Q6_K).
+// a grid apart instead: row ((i * ER_CU_WAVES + wave) * gridDim.x + b') * G + g
+// with b' a permutation of the workgroup index that gives neighbouring rows to
+// workgroups on one XCD (the same rows overall; 2% faster for Q8_0 at
+// 14336 x 4096, no gain for Q4_K or Q6_K).
 // Per-row arithmetic (slot order, lane reduction) is that of the family-1
 // kernel with the same LPR and NS.
 
@@ -1151,9 +1152,13 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     const uint32_t J = rowsPerWg / STEP;  // steps per workgroup (rows past M are skipped)
     const uint32_t JR = JC > 0 ? (uint32_t)JC : max((J + UNR - 1u) / UNR * UNR, (uint32_t)UNR);
     const uint32_t laneRow = wave * G + g;  // row within a step
-    // row of lane group (w, gg)'s step i
+    // row of lane group (w, gg)'s step i.  With the spread assignment,
+    // neighbouring rows of a step go to workgroups dispatched to the same XCD
+    // (workgroup b runs on XCD b % 8; bx below orders them XCD by XCD when the
+    // grid is a multiple of 8), so y is written back in whole L2 lines.
+    const uint32_t bx = gridDim.x % 8u == 0 ? (blockIdx.x % 8u) * (gridDim.x / 8u) + blockIdx.x / 8u : blockIdx.x;
     auto rowAt = [&](uint32_t i, uint32_t w, uint32_t gg) {
-        return F::SPREAD ? ((i * ER_CU_WAVES + w) * gridDim.x + blockIdx.x) * G + gg
+        return F::SPREAD ? ((i * ER_CU_WAVES + w) * gridDim.x + bx) * G + gg
                          : (i * gridDim.x + blockIdx.x) * STEP + w * G + gg;
     };
     auto rowOf = [&](uint32_t i) { return rowAt(i, wave, g); };
