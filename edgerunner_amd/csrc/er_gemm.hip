@@ -809,10 +809,15 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
 #pragma unroll
             for (uint32_t hq = 0; hq < 4u; ++hq) issueHeader(0u, 0u, hq);  // super-block 0's header
         }
+        // chunks 0..2 first, the rest of the copy-ahead after the first
+        // barrier, so the launch's first requests are the ones the compute
+        // waves wait for
 #pragma unroll
-        for (int j = 0; j < G::DW; ++j) issue((uint32_t)j, (uint32_t)j);
-        gemml_vmwait<(G::DW - 2) * G::LW>();  // header 0 and chunks 0 and 1 are in
+        for (int j = 0; j < 3; ++j) issue((uint32_t)j, (uint32_t)j);
+        gemml_vmwait<G::LW>();  // header 0 and chunks 0 and 1 are in
         gemml_barrier();
+#pragma unroll
+        for (int j = 3; j < G::DW; ++j) issue((uint32_t)j, (uint32_t)j);
         for (uint32_t c = 0; c < NC; ++c) {
             gemml_vmwait<(G::DW - 3) * G::LW>();  // chunks <= c + 2 are in
             gemml_barrier();
