@@ -718,8 +718,6 @@ er_status encode_quantize_q8_0(er_hip_ctx *ctx, er_stream stream, er_buffer src,
                   stream, args);
 }
 
-// Prefill GEMM: validation mirrors the GEMV rules (K multiple of the block,
-// buffer lengths), then a grid of ceil(N/128) x ceil(T/TT) workgroups.
 // Loader-specialised kernel: 256 (or 128) weight rows x 128 tokens per
 // workgroup, no K split, so it runs where those tiles alone give (nearly)
 // every CU a workgroup (256-row tiles), or at least half of them (128-row
@@ -759,6 +757,9 @@ er_status launch_gemml(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er
     return launch(ctx, k, dim3((uint32_t)(8u * ((p.tiles + 7u) / 8u)), 1, 1), dim3(512, 1, 1), lds, stream, args);
 }
 
+// Prefill GEMM: validation mirrors the GEMV rules (K multiple of the block,
+// buffer lengths), then the loader-specialised kernel where it takes the
+// shape, else a grid of ceil(N/128) x ceil(T/TT) workgroups of the others.
 // stamps (the clock probe only): the loader-specialised kernel must take the
 // shape, and stamps receives its per-work-item clock stamps
 er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_buffer x,
