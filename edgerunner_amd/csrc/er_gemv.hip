@@ -1385,27 +1385,33 @@ ER_DEV float dot4u(uint32_t u, const float *x, float acc) {
 // i = s%8, i.e. pair p = i/2 and positions l in [16(i&1), 16(i&1)+16) of
 // sub-blocks 2p (low nibbles) and 2p+1 (high nibbles).
 // ---------------------------------------------------------------------------
-template <int LPR, int R, bool XG>
+// EPI = ER_EPI_GEGLU: the dual gate/up GeGLU for rows longer than the
+// integer-dot kernels cover: a lane group's rows [0, R/2) are gate rows of W,
+// [R/2, R) the matching up rows of Wu, and the gate row's output is
+// gelu_tanh(gate) * up.
+template <int LPR, int R, bool XG, int EPI = ER_EPI_STORE>
 ER_DEV void gemv_q4k(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                     float *__restrict__ y, uint32_t M, uint32_t K) {
+                     float *__restrict__ y, uint32_t M, uint32_t K,
+                     const uint8_t *__restrict__ Wu = nullptr) {
     extern __shared__ float xs_dyn[];
     x += (size_t)blockIdx.y * K;
     y += (size_t)blockIdx.y * M;
     const float *xv = stage_x<XG>(x, xs_dyn, K);
 
     constexpr int G = 64 / LPR;
+    constexpr int OR = EPI == ER_EPI_GEGLU ? R / 2 : R;  // output rows per lane group
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t g = lane / LPR, li = lane % LPR;
     const uint32_t nb = K >> 8, S = nb << 3;
     const size_t rowBytes = (size_t)nb * 144u;
     const uint32_t row0 =
-        ((blockIdx.x * (ER_GEMV_THREADS / 64) + wave) * G + g) * (uint32_t)R;
+        ((blockIdx.x * (ER_GEMV_THREADS / 64) + wave) * G + g) * (uint32_t)OR;
 
     const uint8_t *rowp[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t row = min(row0 + (uint32_t)r, M - 1u);
-        rowp[r] = W + (size_t)row * rowBytes;
+        const uint32_t row = min(row0 + (uint32_t)(r % OR), M - 1u);
+        rowp[r] = (EPI == ER_EPI_GEGLU && r >= OR ? Wu : W) + (size_t)row * rowBytes;
     }
     float acc[R];
 #pragma unroll
@@ -1464,9 +1470,15 @@ ER_DEV void gemv_q4k(const uint8_t *__restrict__ W, const float *__restrict__ x,
         }
     }
     if (li == 0) {
+        if constexpr (EPI == ER_EPI_GEGLU) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+            for (int r = 0; r < OR; ++r)
+                if (row0 + (uint32_t)r < M) y[row0 + r] = gelu_tanh(acc[r]) * acc[OR + r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
+        }
     }
 }
 
@@ -1476,9 +1488,12 @@ ER_DEV void gemv_q4k(const uint8_t *__restrict__ W, const float *__restrict__ x,
 // high nibbles), [64h+32+16c, +16) (q2, q4), qh bytes [128+32h+16c, +16),
 // scales sc[8h+c+{0,2,4,6}].  Blocks are 2-byte aligned: ld16_a2/ld8_a2.
 // ---------------------------------------------------------------------------
-template <int LPR, int R, bool XG>
+// TOP1: the greedy top-1 partial epilogue in place of the store (one
+// partial per workgroup; row values as the plain kernel computes them).
+template <int LPR, int R, bool XG, bool TOP1 = false>
 ER_DEV void gemv_q6k(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                     float *__restrict__ y, uint32_t M, uint32_t K) {
+                     float *__restrict__ y, uint32_t M, uint32_t K,
+                     float *__restrict__ pv = nullptr, uint32_t *__restrict__ pi = nullptr) {
     extern __shared__ float xs_dyn[];
     x += (size_t)blockIdx.y * K;
     y += (size_t)blockIdx.y * M;
@@ -1565,7 +1580,9 @@ ER_DEV void gemv_q6k(const uint8_t *__restrict__ W, const float *__restrict__ x,
             acc[r] = hits > 0.0f ? v : acc[r];
         }
     }
-    if (li == 0) {
+    if constexpr (TOP1) {
+        top1_epilogue<ER_GEMV_WAVES * G * R>(acc, R, (wave * G + g) * R, li == 0, M, pv, pi);
+    } else if (li == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
             if (row0 + (uint32_t)r < M) y[row0 + r] = acc[r];
@@ -1708,6 +1725,120 @@ ER_DEV void gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict
     }
 }
 
+// Fused Q8_0 projections for any K % 32 == 0: rows only 2-byte aligned (odd
+// K/32) or longer than the integer-dot kernels cover.  The arithmetic of
+// gemv_q8_0_any over the concatenated rows of mm (EPI = ER_EPI_Q8_ROWS:
+// + residual, fp32 or fp16 store) or over gate/up pairs (ER_EPI_Q8_SILU:
+// W[0] gate, W[1] up, M[0] rows, silu(gate) * up into y[0]); R row
+// computations per wave.  RMSNorm, when mm.normW is set: the workgroup sums
+// x^2 over the token's row and every x value enters as x * rms * normW, the
+// expression the integer-dot prologue stages.
+template <int R, int EPI>
+ER_DEV void gemv_q8_0_any_fused(const Q8Multi &mm, const float *__restrict__ x, uint32_t K) {
+    __shared__ float red[ER_GEMV_WAVES];
+    constexpr int OR = EPI == ER_EPI_Q8_SILU ? R / 2 : R;  // output rows per wave
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.y;
+    const uint32_t nb = K >> 5;
+    const size_t rowBytes = (size_t)nb * 34u;
+    const uint32_t Mt = EPI == ER_EPI_Q8_SILU ? mm.M[0] : mm.M[0] + mm.M[1] + mm.M[2];
+    const uint32_t row0 = (blockIdx.x * ER_GEMV_WAVES + wave) * (uint32_t)OR;
+    x += (size_t)t * K;
+    const float *__restrict__ nw = mm.normW;
+    float rms = 1.0f;
+    if (nw) {
+        float ss = 0.0f;
+        for (uint32_t k = threadIdx.x; k < K; k += ER_GEMV_THREADS) ss = __builtin_fmaf(x[k], x[k], ss);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < ER_GEMV_WAVES; ++k) ss += red[k];
+        rms = 1.0f / __builtin_sqrtf(ss / (float)K + mm.eps);
+    }
+    const uint8_t *rowp[R];
+    void *yrow[OR];
+    bool live[OR], half[OR];
+    const float *res[OR];
+#pragma unroll
+    for (int r = 0; r < OR; ++r) {
+        uint32_t v = min(row0 + (uint32_t)r, Mt - 1u);
+        int m = 0;
+        if (EPI == ER_EPI_Q8_ROWS && v >= mm.M[0]) {
+            v -= mm.M[0];
+            m = 1;
+            if (v >= mm.M[1]) {
+                v -= mm.M[1];
+                m = 2;
+            }
+        }
+        const size_t out = (size_t)t * mm.M[m] + v;
+        rowp[r] = mm.W[m] + (size_t)v * rowBytes;
+        if (EPI == ER_EPI_Q8_SILU) rowp[OR + r] = mm.W[1] + (size_t)v * rowBytes;
+        half[r] = EPI == ER_EPI_Q8_ROWS && ((mm.halfMask >> m) & 1u);
+        yrow[r] = (uint8_t *)mm.y[m] + out * (half[r] ? 2u : 4u);
+        res[r] = EPI == ER_EPI_Q8_ROWS && mm.res[m] ? mm.res[m] + out : nullptr;
+        live[r] = row0 + (uint32_t)r < Mt;
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (uint32_t b = lane; b < nb; b += 64) {
+        float xb[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 f = ((const float4 *)(x + (b << 5)))[i];
+            xb[4 * i + 0] = f.x;
+            xb[4 * i + 1] = f.y;
+            xb[4 * i + 2] = f.z;
+            xb[4 * i + 3] = f.w;
+        }
+        if (nw) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 w = ((const float4 *)(nw + (b << 5)))[i];
+                xb[4 * i + 0] = xb[4 * i + 0] * rms * w.x;
+                xb[4 * i + 1] = xb[4 * i + 1] * rms * w.y;
+                xb[4 * i + 2] = xb[4 * i + 2] * rms * w.z;
+                xb[4 * i + 3] = xb[4 * i + 3] * rms * w.w;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *p = rowp[r] + (size_t)b * 34u;
+            const float d = f16_to_f32(ld2(p));
+            float f = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t q = ld4_a2(p + 2 + 4 * k);
+                f = __builtin_fmaf(sb(q, 0), xb[4 * k + 0], f);
+                f = __builtin_fmaf(sb(q, 1), xb[4 * k + 1], f);
+                f = __builtin_fmaf(sb(q, 2), xb[4 * k + 2], f);
+                f = __builtin_fmaf(sb(q, 3), xb[4 * k + 3], f);
+            }
+            acc[r] = __builtin_fmaf(d, f, acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<64>(acc[r]);
+    if (lane != 0) return;
+#pragma unroll
+    for (int r = 0; r < OR; ++r) {
+        if (!live[r]) continue;
+        if constexpr (EPI == ER_EPI_Q8_SILU) {
+            *(float *)yrow[r] = silu(acc[r]) * acc[OR + r];
+        } else {
+            const float v = res[r] ? acc[r] + *res[r] : acc[r];
+            if (half[r])
+                *(_Float16 *)yrow[r] = (_Float16)v;
+            else
+                *(float *)yrow[r] = v;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Entry points (extern "C" so hipModuleGetFunction resolves them by name).
 //   er_gemv_<fmt>_i8_l<LPR>_n<NS>_r<R> : integer-dot family (er_gemv_cfg.h; q4k, q8_0, q6k)
@@ -1840,4 +1971,43 @@ extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)
 er_gemv_q8_0_any(const uint8_t *__restrict__ W, const float *__restrict__ x,
                  float *__restrict__ y, uint32_t M, uint32_t K) {
     gemv_q8_0_any<2>(W, x, y, M, K);
+}
+
+// Q6_K top-1 over the fp32 family (rows the integer-dot kernels do not take):
+// er_gemv_q6k_top1_l<LPR>_<s|g>, one partial per workgroup.
+#define ER_GEMV_TOP1_ENTRY(lpr, xg, tag)                                                        \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                             \
+        er_gemv_q6k_top1_l##lpr##_##tag(const uint8_t *__restrict__ W, const float *__restrict__ x, \
+                                        float *__restrict__ pv, uint32_t *__restrict__ pi,        \
+                                        uint32_t M, uint32_t K) {                                 \
+        gemv_q6k<lpr, ER_Q6K_ROWS, xg, true>(W, x, nullptr, M, K, pv, pi);                       \
+    }
+ER_GEMV_TOP1_ENTRY(64, false, s)
+ER_GEMV_TOP1_ENTRY(32, false, s)
+ER_GEMV_TOP1_ENTRY(16, false, s)
+ER_GEMV_TOP1_ENTRY(8, false, s)
+ER_GEMV_TOP1_ENTRY(4, false, s)
+ER_GEMV_TOP1_ENTRY(64, true, g)
+ER_GEMV_TOP1_ENTRY(32, true, g)
+ER_GEMV_TOP1_ENTRY(16, true, g)
+ER_GEMV_TOP1_ENTRY(8, true, g)
+ER_GEMV_TOP1_ENTRY(4, true, g)
+
+// Q4_K dual GeGLU for rows longer than the integer-dot kernels cover: fp32
+// kernel, x from global memory, ER_Q4K_ROWS / 2 output rows per lane group.
+extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)
+er_gemv_q4k_geglu_l64_g(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,
+                        const float *__restrict__ x, float *__restrict__ y, uint32_t M, uint32_t K) {
+    gemv_q4k<64, ER_Q4K_ROWS, true, ER_EPI_GEGLU>(Wg, x, y, M, K, Wu);
+}
+
+// Fused Q8_0 row lists and gate/up SiLU pairs for any K % 32 == 0: 2 rows
+// (ROWS) or 2 gate/up pairs (SILU) per wave.
+extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)
+er_gemv_q8_0_any_multi(Q8Multi mm, const float *__restrict__ x, uint32_t K) {
+    gemv_q8_0_any_fused<2, ER_EPI_Q8_ROWS>(mm, x, K);
+}
+extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)
+er_gemv_q8_0_any_silu(Q8Multi mm, const float *__restrict__ x, uint32_t K) {
+    gemv_q8_0_any_fused<4, ER_EPI_Q8_SILU>(mm, x, K);
 }

@@ -64,6 +64,19 @@ using er_detail::fail;
     X(GEMV_Q4K_L64_G, "er_gemv_q4k_l64_g")                                             \
     X(GEMV_Q8_0_L64_G, "er_gemv_q8_0_l64_g")                                           \
     X(GEMV_Q8_0_ANY, "er_gemv_q8_0_any")                                               \
+    X(GEMV_Q6K_TOP1_L64_S, "er_gemv_q6k_top1_l64_s")                                   \
+    X(GEMV_Q6K_TOP1_L32_S, "er_gemv_q6k_top1_l32_s")                                   \
+    X(GEMV_Q6K_TOP1_L16_S, "er_gemv_q6k_top1_l16_s")                                   \
+    X(GEMV_Q6K_TOP1_L8_S, "er_gemv_q6k_top1_l8_s")                                     \
+    X(GEMV_Q6K_TOP1_L4_S, "er_gemv_q6k_top1_l4_s")                                     \
+    X(GEMV_Q6K_TOP1_L64_G, "er_gemv_q6k_top1_l64_g")                                   \
+    X(GEMV_Q6K_TOP1_L32_G, "er_gemv_q6k_top1_l32_g")                                   \
+    X(GEMV_Q6K_TOP1_L16_G, "er_gemv_q6k_top1_l16_g")                                   \
+    X(GEMV_Q6K_TOP1_L8_G, "er_gemv_q6k_top1_l8_g")                                     \
+    X(GEMV_Q6K_TOP1_L4_G, "er_gemv_q6k_top1_l4_g")                                     \
+    X(GEMV_Q4K_GEGLU_L64_G, "er_gemv_q4k_geglu_l64_g")                                 \
+    X(GEMV_Q8_0_ANY_MULTI, "er_gemv_q8_0_any_multi")                                   \
+    X(GEMV_Q8_0_ANY_SILU, "er_gemv_q8_0_any_silu")                                     \
     X(GEMM_Q4K_T128, "er_gemm_q4k_t128")                                               \
     X(GEMM_Q4K_T256, "er_gemm_q4k_t256")                                               \
     X(GEMM_Q8_0_T128, "er_gemm_q8_0_t128")                                             \
@@ -519,11 +532,26 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
 // reference's validation, then device x / y, one encode on the device's null
 // stream, a wait and the copy-out.  Host-side allocation or copy failures are
 // encodingFailed, as the reference's failed makeBuffer.
-er_status execute_gemv(er_hip_ctx *ctx, Fmt f, er_buffer W, const float *x, uint64_t xCount, float *y,
-                       uint64_t yCount, uint32_t batch, bool batched, uint32_t M, uint32_t K) {
+// The reference's order of the x.count and shape checks: the single-vector
+// forms check x.count == K first (validateKQuantInputShape's vectorCount);
+// the batched form runs the K and weight-size rules with vectorCount = K
+// first, then batchSeq > 0 && x.count == batchSeq * K
+// (executeBatchedQ4KWeights, GEMVKernel.swift:623-640).
+er_status check_x_count(Fmt f, uint64_t wBytes, uint64_t xCount, uint32_t batch, bool batched, uint32_t M,
+                        uint32_t K) {
+    if (batched) {
+        er_status st = validate_gemv_shape(f, er_buffer{nullptr, wBytes}, (uint64_t)K * 4u, (uint64_t)M * 4u, 1, M, K);
+        if (st != ER_OK) return st;
+    }
     if (batched ? (batch == 0 || xCount != (uint64_t)batch * K) : xCount != K)
         return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s execute: x.count %llu does not match K=%u x batch %u",
                     fmt_name(f), (unsigned long long)xCount, K, batch);
+    return ER_OK;
+}
+
+er_status execute_gemv(er_hip_ctx *ctx, Fmt f, er_buffer W, const float *x, uint64_t xCount, float *y,
+                       uint64_t yCount, uint32_t batch, bool batched, uint32_t M, uint32_t K) {
+    if (er_status cs = check_x_count(f, W.length, xCount, batch, batched, M, K); cs != ER_OK) return cs;
     const uint64_t yNeed = (uint64_t)batch * M;
     er_status st = validate_gemv_shape(f, W, xCount * 4u, yNeed * 4u, batch, M, K);
     if (st != ER_OK) return st;
@@ -561,9 +589,7 @@ er_status execute_gemv(er_hip_ctx *ctx, Fmt f, er_buffer W, const float *x, uint
 er_status execute_gemv_host(er_hip_ctx *ctx, Fmt f, const void *raw, uint64_t rawBytes, const float *x,
                             uint64_t xCount, float *y, uint64_t yCount, uint32_t batch, bool batched, uint32_t M,
                             uint32_t K) {
-    if (batched ? (batch == 0 || xCount != (uint64_t)batch * K) : xCount != K)
-        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s execute: x.count %llu does not match K=%u x batch %u",
-                    fmt_name(f), (unsigned long long)xCount, K, batch);
+    if (er_status cs = check_x_count(f, rawBytes, xCount, batch, batched, M, K); cs != ER_OK) return cs;
     er_status st = validate_gemv_shape(f, er_buffer{nullptr, rawBytes}, xCount * 4u, (uint64_t)batch * M * 4u, batch,
                                        M, K);
     if (st != ER_OK) return st;
@@ -620,13 +646,23 @@ er_status launch_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buf
         return fail(ER_ERR_INVALID_ARGUMENT,
                     "Q6_K top-1: weight and input must be 16-byte, partial and index buffers 4-byte aligned");
     const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
-    if (K > kI8MaxK || lds + 1024u > ctx->info.lds_per_workgroup)
-        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "Q6_K top-1: K=%u exceeds the supported %u", K, kI8MaxK);
+    // rows the integer-dot kernels do not take run the fp32 family, as the
+    // plain GEMV over the same matrix does
+    const bool fp32 = K > kI8MaxK || lds + 1024u > ctx->info.lds_per_workgroup || ctx->gemv_fp32 != 0;
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     uint32_t count = 0;
     CuPlan cp;
-    if (M > 0 && plan_cu(ctx, Fmt::Q6_K, M, K, 1u, cp)) {
+    if (M > 0 && fp32) {
+        const bool xg = (uint64_t)K * 4u > kLdsXLimit;
+        const uint32_t lpr = lanes_per_row((K / 256u) * 4u);
+        const KernelId k = (KernelId)(K_GEMV_Q6K_TOP1_L64_S + lpr_index(lpr) + (xg ? 5 : 0));
+        const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / lpr) * kQ6KRows;  // >= 8: at most M/4 partials
+        count = (M + rowsPerBlock - 1u) / rowsPerBlock;
+        void *args[] = {&W.data, &x.data, &pv, &pi, &M, &K};
+        st = launch(ctx, k, dim3(count, 1, 1), dim3(kGemvThreads, 1, 1), xg ? 0u : K * 4u, stream, args);
+        if (st != ER_OK) return st;
+    } else if (M > 0 && plan_cu(ctx, Fmt::Q6_K, M, K, 1u, cp)) {
         // one partial per workgroup (rowsPerWg >= 8, so at most M/4); the
         // row values of a workgroup reuse its x area of LDS
         count = (M + cp.rowsPerWg - 1u) / cp.rowsPerWg;
@@ -732,7 +768,11 @@ GemmLPlan plan_gemml(const er_hip_ctx *ctx, uint32_t T, uint32_t N, uint32_t K) 
     const uint64_t tiles2 = nT * ((N + 255u) / 256u), tiles1 = nT * ((N + 127u) / 128u);
     const uint64_t cu = (uint64_t)ctx->cu_count;
     const bool fits = K % 256u == 0 && (uint64_t)T * N * 4u < (1ull << 32) && tiles1 <= 8ull * 65535u;
-    if (fits && ctx->gemm_variant == 0) p.r = 4u * tiles2 >= 3u * cu ? 2 : 2u * tiles1 >= cu ? 1 : 0;
+    // ER_HIP_GEMM_TILE forces the tile / split-K kernels: the loader kernel
+    // then takes no shape (unless ER_HIP_GEMM_VARIANT names it)
+    const bool tileForced = ctx->gemm_tt != 0 || ctx->gemm_sk != 0;
+    if (fits && ctx->gemm_variant == 0 && !tileForced)
+        p.r = 4u * tiles2 >= 3u * cu ? 2 : 2u * tiles1 >= cu ? 1 : 0;
     if (fits && ctx->gemm_variant == 4) p.r = 2;
     if (fits && ctx->gemm_variant == 5) p.r = 1;
     p.tiles = p.r == 2 ? tiles2 : p.r == 1 ? tiles1 : 0;
@@ -897,12 +937,17 @@ er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_b
     if (st != ER_OK) return st;
     st = check_ctx(ctx);
     if (st != ER_OK || M == 0) return st;
-    const int ci = K <= kI8MaxK ? pick_multi(ctx, K / 64u, 2u * M) : -1;
-    if (ci < 0)
-        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "Q4_K dual GeGLU: K=%u exceeds the fused kernel's %u", K,
-                    kI8MaxK);
+    const int ci = K <= kI8MaxK && ctx->gemv_fp32 == 0 ? pick_multi(ctx, K / 64u, 2u * M) : -1;
     st = bind_device(ctx);
     if (st != ER_OK) return st;
+    if (ci < 0) {
+        // rows longer than the integer-dot kernels cover: fp32 pair kernel,
+        // x from global memory
+        const uint32_t rowsPerBlock = ER_GEMV_WAVES * (kQ4KRows / 2u);
+        void *args[] = {&Wg.data, &Wu.data, &x.data, &y.data, &M, &K};
+        return launch(ctx, K_GEMV_Q4K_GEGLU_L64_G, dim3((M + rowsPerBlock - 1) / rowsPerBlock, 1, 1),
+                      dim3(kGemvThreads, 1, 1), 0, stream, args);
+    }
     const I8Cfg &c = kI8MultiCfg[ci];
     const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * (c.r / 2u);
     const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
@@ -915,8 +960,10 @@ er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_b
 // Fused Q8_0 projections (Dequant_Q8_0.metal:199-586, encoded by name in
 // LlamaLanguageModel.swift:260-275).  The reference dispatches them without
 // checks; here every buffer must hold what the shapes imply (weights
-// INVALID_MATRIX_SHAPE, vectors ENCODING_FAILED), and the integer-dot kernels
-// need K % 64 == 0 and K <= 16384 (INVALID_VECTOR_SHAPE).
+// INVALID_MATRIX_SHAPE, vectors ENCODING_FAILED).  Any K % 32 == 0 is taken,
+// as the reference's kernels take any blocksPerRow: the integer-dot kernels
+// run rows of K % 64 == 0 up to 16384 weights, the fp32 kernels
+// (gemv_q8_0_any_fused) the rest.
 struct Q8FusedSpec {
     const char *name;
     int count;          // matrices (1..3); 2 for gate/up
@@ -932,9 +979,8 @@ er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &
                           uint32_t tokens, uint32_t K) {
     if (K == 0 || K % 32u != 0)
         return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s: K=%u must be a positive multiple of 32", f.name, K);
-    if (K % 64u != 0 || K > kI8MaxK)
-        return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s: the fused kernels need K %% 64 == 0 and K <= %u (K=%u)",
-                    f.name, kI8MaxK, K);
+    // odd block counts (rows only 2-byte aligned) and long rows: fp32 kernels
+    bool anyK = K % 64u != 0 || K > kI8MaxK;
     if (tokens == 0 || tokens > 65535u)
         return fail(ER_ERR_ENCODING_FAILED, "%s: tokenCount %u outside [1, 65535]", f.name, tokens);
     uint64_t Mt = 0;
@@ -962,6 +1008,7 @@ er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &
                     (unsigned long long)f.normW.length, (unsigned long long)K * 4u);
     er_status st = check_ctx(ctx);
     if (st != ER_OK) return st;
+    anyK = anyK || ctx->gemv_fp32 != 0;
     if (f.silu) Mt = f.M[0];
     if (Mt == 0) return ER_OK;
     if (Mt > 0x7fffffffull) return fail(ER_ERR_INVALID_MATRIX_SHAPE, "%s: too many rows", f.name);
@@ -969,18 +1016,37 @@ er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &
         return fail(ER_ERR_INVALID_ARGUMENT, "%s: input and norm weight must be 16-byte aligned", f.name);
     for (int m = 0; m < f.count; ++m) {
         if (f.M[m] == 0) continue;
-        if (!f.W[m].data || !aligned(f.W[m].data, 4) || ((!f.silu || m == 0) && !f.y[m].data) ||
+        if (!f.W[m].data || !aligned(f.W[m].data, anyK ? 2 : 4) || ((!f.silu || m == 0) && !f.y[m].data) ||
             (f.res[m].data && !aligned(f.res[m].data, 4)))
-            return fail(ER_ERR_INVALID_ARGUMENT, "%s: null or misaligned buffer (weights and residual 4-byte aligned)",
-                        f.name);
+            return fail(ER_ERR_INVALID_ARGUMENT,
+                        "%s: null or misaligned buffer (weights %d-byte, residual 4-byte aligned)", f.name,
+                        anyK ? 2 : 4);
         if ((!f.silu || m == 0) && !aligned(f.y[m].data, (f.halfMask >> m) & 1u ? 2 : 4))
             return fail(ER_ERR_INVALID_ARGUMENT, "%s: misaligned output", f.name);
     }
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     const uint32_t S = K / 64u;
-    const int ci = pick_multi(ctx, S, (uint32_t)(f.silu ? 2u * Mt : Mt));
-    if (ci < 0) return fail(ER_ERR_INVALID_VECTOR_SHAPE, "%s: no configuration for K=%u", f.name, K);
+    const int ci = anyK ? -1 : pick_multi(ctx, S, (uint32_t)(f.silu ? 2u * Mt : Mt));
+    if (ci < 0) {
+        Q8MultiArgs a{};
+        for (int m = 0; m < 3; ++m) {
+            const int j = m < f.count ? m : 0;
+            a.W[m] = f.W[j].data;
+            a.y[m] = f.y[j].data;
+            a.res[m] = m < f.count ? (const float *)f.res[m].data : nullptr;
+            a.M[m] = m < f.count ? f.M[m] : 0u;
+        }
+        a.halfMask = f.halfMask;
+        a.normW = (const float *)f.normW.data;
+        a.eps = f.eps;
+        // 2 rows (or 2 gate/up pairs) per wave
+        const uint32_t rowsPerBlock = ER_GEMV_WAVES * 2u;
+        void *args[] = {&a, &x.data, &K};
+        dim3 grid((uint32_t)((Mt + rowsPerBlock - 1) / rowsPerBlock), tokens, 1);
+        return launch(ctx, f.silu ? K_GEMV_Q8_0_ANY_SILU : K_GEMV_Q8_0_ANY_MULTI, grid, dim3(kGemvThreads, 1, 1), 0,
+                      stream, args);
+    }
     const I8Cfg &c = kI8MultiCfg[ci];
     const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
     const float *normW = (const float *)f.normW.data;

@@ -207,7 +207,8 @@ er_status er_hip_encode_q4k_weights_triple(er_hip_ctx *ctx, er_stream stream, er
                                            uint32_t rows_c, uint32_t K);
 /* GEMVKernel.encodeQ4KWeightsDualGeGLU (GEMVKernel.swift:930-976, kernel
  * q4_k_gemv_dual_geglu_f32): y = gelu_tanh(Wgate.x) * (Wup.x), gelu_tanh
- * saturated outside [-10, 10].  K <= 16384 (else INVALID_VECTOR_SHAPE). */
+ * saturated outside [-10, 10].  Any K % 256 == 0, as the reference: rows
+ * beyond 16384 weights run an fp32 pair kernel. */
 er_status er_hip_encode_q4k_weights_dual_geglu(er_hip_ctx *ctx, er_stream stream,
                                                er_buffer gate_weight, er_buffer up_weight,
                                                er_buffer input, er_buffer output, uint32_t M,
@@ -284,7 +285,9 @@ er_status er_hip_execute_batched_q4k_weights(er_hip_ctx *ctx, const void *raw_we
  * and partial_indices of >= M/4 fp32 / uint32 entries (q6KTop1PartialCount,
  * GEMVKernel.swift:50-52) and output_index >= 4 bytes, else ENCODING_FAILED.
  * The partial buffers are scratch; their contents afterwards are unspecified.
- * K <= 16384 (else INVALID_VECTOR_SHAPE). */
+ * Any K % 256 == 0, as the reference: the row values are those the plain
+ * er_hip_encode_q6k_weights computes over the same matrix (fp32 kernels for
+ * rows beyond 16384 weights). */
 er_status er_hip_encode_q6k_weights_packed_top1(er_hip_ctx *ctx, er_stream stream, er_buffer weight,
                                                 er_buffer input, er_buffer partial_values,
                                                 er_buffer partial_indices, er_buffer output_index,
@@ -327,7 +330,9 @@ er_status er_hip_quantize_q8_0_rows(er_hip_ctx *ctx, er_stream stream, er_buffer
  * per token.  The reference encodes these without checks; here weights must
  * hold rows*(cols/32)*34 bytes (INVALID_MATRIX_SHAPE), inputs, outputs, norm
  * weight and residual their implied sizes (ENCODING_FAILED), and cols must be
- * a multiple of 64 no larger than 16384 (INVALID_VECTOR_SHAPE). ---- */
+ * a positive multiple of 32 (INVALID_VECTOR_SHAPE); any block count is taken,
+ * as the reference's kernels take any blocksPerRow (rows of an odd block
+ * count or beyond 16384 weights run fp32 kernels). ---- */
 
 /* dequant_q8_0_fused_qkv (ERFusedQKVParams{qRows, kvRows, cols, blocksPerRow,
  * tokenCount, rmsEps}, Dequant_Q8_0.metal:199-314): per token t, q = Wq.n,

@@ -191,3 +191,27 @@ def test_execute_validation_without_device():
     assert b(None, w.ctypes.data, w.size, xb.ctypes.data, 3 * K, yb.ctypes.data, 3 * M, 3, M, K) == 8
     assert b(None, w.ctypes.data, w.size, xb.ctypes.data, 3 * K, yb.ctypes.data, 3 * M, 0, M, K) == 5
     assert b(None, w.ctypes.data, w.size, xb.ctypes.data, 2 * K, yb.ctypes.data, 3 * M, 3, M, K) == 5
+    # executeBatchedQ4KWeights (GEMVKernel.swift:623-640) runs the K and weight
+    # rules before batchSeq / x.count: a short weight buffer is
+    # invalidMatrixShape even when batchSeq or x.count is also wrong
+    assert b(None, w.ctypes.data, w.size - 1, xb.ctypes.data, 3 * K, yb.ctypes.data, 3 * M, 0, M, K) == 4
+    assert b(None, w.ctypes.data, w.size - 1, xb.ctypes.data, 2 * K, yb.ctypes.data, 3 * M, 3, M, K) == 4
+    assert b(None, w.ctypes.data, w.size, xb.ctypes.data, 3 * K, yb.ctypes.data, 3 * M, 0, M, K + 32) == 5
+    # the single-vector form checks x.count first (vectorCount == K)
+    assert f(None, w.ctypes.data, w.size - 1, x.ctypes.data, K - 1, y.ctypes.data, M, M, K) == 5
+
+
+def test_noalloc_top1_rejects_heads_past_the_array():
+    """er_hip_encode_q6k_weights_packed_top1_noalloc: heads of more than
+    ER_HIP_TOP1_NOALLOC_MAX_ROWS rows are INVALID_MATRIX_SHAPE, decided from
+    the lengths before the context or any buffer is touched (null context,
+    placeholder pointers never dereferenced)."""
+    lib = _ffi.load()
+    max_rows = 262144
+    M, K = max_rows + 4, 256
+    st = lib.er_hip_encode_q6k_weights_packed_top1_noalloc(None, None, _buf(M * 210), _buf(4 * K), _buf(4), M, K)
+    assert st == 4 and "exceeds" in _ffi.last_error()
+    # at the limit the shape passes and the null context is what fails
+    M = max_rows
+    st = lib.er_hip_encode_q6k_weights_packed_top1_noalloc(None, None, _buf(M * 210), _buf(4 * K), _buf(4), M, K)
+    assert st == 8

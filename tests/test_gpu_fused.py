@@ -62,7 +62,11 @@ def test_triple_shapes_match_oracle_and_single(gemv, rows, K):
         assert np.array_equal(y, gemv.executeQ4KWeights(W, x, m, K))
 
 
-@pytest.mark.parametrize("M,K", [(3072, 1024), (10240, 2560), (33, 768)])
+@pytest.mark.parametrize("M,K", [(3072, 1024), (10240, 2560), (33, 768),
+                                 # beyond the integer-dot kernels' 16384 weights: the fp32
+                                 # pair kernel (encodeQ4KWeightsDualGeGLU takes any K % 256 == 0,
+                                 # GEMVKernel.swift:930-976)
+                                 (512, 16640), (37, 32768)])
 def test_dual_and_geglu_shapes(gemv, M, K):
     G = synth.q4_k(synth.seed(51, 0), M, K)
     U = synth.q4_k(synth.seed(51, 1), M, K)

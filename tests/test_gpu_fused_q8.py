@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import edgerunner_amd.synth as synth
-from edgerunner_amd import EncodingFailed, FusedQ8Kernel, GEMVKernel, InvalidVectorShape
+from edgerunner_amd import EncodingFailed, FusedQ8Kernel, GEMVKernel, InvalidMatrixShape, InvalidVectorShape
 from oracle import ref
 from conftest import rel_l2
 
@@ -39,7 +39,11 @@ def oracle_proj(W, x_t, nw, M, K):
 
 
 @pytest.mark.parametrize("dim,qd,kvd,T", [(128, 64, 32, 1), (128, 64, 32, 3), (4096, 4096, 1024, 1),
-                                          (4096, 4096, 1024, 4), (2048, 2048, 512, 2)])
+                                          (4096, 4096, 1024, 4), (2048, 2048, 512, 2),
+                                          # odd block count and rows beyond 16384 weights: the fp32
+                                          # kernels (the reference takes any blocksPerRow,
+                                          # Dequant_Q8_0.metal:214-483)
+                                          (96, 64, 32, 2), (16416, 256, 128, 2), (160, 96, 40, 3)])
 def test_fused_qkv(ctx, fk, dim, qd, kvd, T):
     Wq, Wk, Wv = q8(qd, dim, 1), q8(kvd, dim, 2), q8(kvd, dim, 3)
     x = synth.normal_f32(synth.seed(70, 10 + T), T * dim)
@@ -63,7 +67,8 @@ def test_fused_qkv(ctx, fk, dim, qd, kvd, T):
         assert rel_l2(v[t].astype(np.float32), ev) < TOL
 
 
-@pytest.mark.parametrize("dim,inter,T", [(128, 96, 3), (128, 96, 1), (4096, 14336, 2), (1024, 3072, 5)])
+@pytest.mark.parametrize("dim,inter,T", [(128, 96, 3), (128, 96, 1), (4096, 14336, 2), (1024, 3072, 5),
+                                         (96, 96, 3), (16416, 512, 2), (20480, 70, 1)])
 def test_fused_gate_up_silu(ctx, fk, dim, inter, T):
     Wg, Wu = q8(inter, dim, 4), q8(inter, dim, 5)
     x = synth.normal_f32(synth.seed(70, 20 + T), T * dim)
@@ -84,7 +89,7 @@ def test_fused_gate_up_silu(ctx, fk, dim, inter, T):
         assert rel_l2(got[t], ref.silu(g) * u) < TOL
 
 
-@pytest.mark.parametrize("rows,dim", [(256, 128), (32000, 4096), (151936, 1024)])
+@pytest.mark.parametrize("rows,dim", [(256, 128), (32000, 4096), (151936, 1024), (256, 96), (1000, 16416)])
 def test_fused_final_norm_gemv(ctx, fk, rows, dim):
     W = q8(rows, dim, 6)
     x = synth.normal_f32(synth.seed(70, 30), dim)
@@ -101,7 +106,7 @@ def test_fused_final_norm_gemv(ctx, fk, rows, dim):
     assert rel_l2(got, oracle_proj(W, x, nw, rows, dim)) < TOL
 
 
-@pytest.mark.parametrize("rows,dim", [(96, 128), (1024, 4096), (4096, 14336)])
+@pytest.mark.parametrize("rows,dim", [(96, 128), (1024, 4096), (4096, 14336), (96, 96), (501, 16416)])
 def test_gemv_f16out_and_add(ctx, fk, rows, dim):
     W = q8(rows, dim, 7)
     x = synth.normal_f32(synth.seed(70, 31), dim)
@@ -178,9 +183,9 @@ def test_validation(ctx, fk):
     wb, xb, nb = ctx.upload(W), ctx.alloc(4 * 128), ctx.alloc(4 * 128)
     y, small = ctx.alloc(4 * 64), ctx.alloc(4 * 10)
     try:
-        with pytest.raises(InvalidVectorShape):   # K % 64 != 0
-            fk.encodeFusedFinalNormGEMV(None, wb, xb, y, nb, 64, 96, EPS)
-        with pytest.raises(InvalidVectorShape):   # K > 16384
+        with pytest.raises(InvalidVectorShape):   # K % 32 != 0
+            fk.encodeFusedFinalNormGEMV(None, wb, xb, y, nb, 64, 80, EPS)
+        with pytest.raises(InvalidMatrixShape):   # a long row the weight buffer does not hold
             fk.encodeGEMVF16Out(None, wb, xb, y, 1, 16384 + 64)
         with pytest.raises(EncodingFailed):       # output too small
             fk.encodeGEMVAdd(None, wb, xb, y, small, 64, 128)

@@ -3,8 +3,9 @@ warp-specialised kernel at each K split (ER_HIP_GEMM_TILE=128:sk, 1 to 8 ways,
 split-K summing with fp32 atomics into a zero-filled Y), the loader-specialised
 kernel with 256- and 128-row tiles on shapes whose tiles alone would not select
 it (ER_HIP_GEMM_VARIANT=4 / 5: partial token and weight-row tiles, one token
-tile of 33 rows, and K = 768, an odd count of Q4_K super-blocks cycling the
-kernel's header slots), and the
+tile of 33 rows, K = 768, an odd count of Q4_K super-blocks cycling the
+kernel's header slots, and K = 256, fewer weight chunks than the kernel's
+copy-ahead depth), and the
 earlier kernels kept for comparison (=1 single-stage, =2 pipelined, =3
 warp-specialised).  Same bars as test_gpu_gemm.py: <= 1e-5 relative L2
 against the float64 product with the bf16-rounded dequantised weights (the
@@ -44,7 +45,8 @@ CONFIGS = [{"ER_HIP_GEMM_TILE": f"128:{sk}"} for sk in (1, 2, 3, 4, 8)] + \
 
 @pytest.mark.parametrize("env", CONFIGS, ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()))
 @pytest.mark.parametrize("fmt", ["q4_k", "q8_0"])
-@pytest.mark.parametrize("T,N,K", [(200, 300, 4096), (384, 8192, 1024), (33, 520, 2048), (130, 700, 768)])
+@pytest.mark.parametrize("T,N,K", [(200, 300, 4096), (384, 8192, 1024), (33, 520, 2048), (130, 700, 768),
+                                   (130, 700, 256)])
 def test_forced_kernel(env, fmt, T, N, K):
     c, gemm = _gemm(**env)
     try:

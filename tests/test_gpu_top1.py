@@ -27,7 +27,11 @@ def test_reference_top1_case(gemv):
 
 
 @pytest.mark.parametrize("M,K", [(4, 256), (8, 512), (100, 1024), (1000, 3072), (4096, 4096),
-                                 (65536, 1024), (1024, 16384), (12, 2304)])
+                                 (65536, 1024), (1024, 16384), (12, 2304),
+                                 # rows longer than the integer-dot kernels take: the fp32
+                                 # family with the top-1 epilogue (the reference takes any
+                                 # K % 256 == 0, GEMVKernel.swift:1205-1265)
+                                 (64, 16640), (1000, 20480), (8, 33024)])
 def test_top1_matches_rule_on_gemv_logits(gemv, M, K):
     W = q6(M, K, M % 13)
     x = synth.normal_f32(synth.seed(40, 100 + K % 97), K)
