@@ -5,11 +5,15 @@ Headline (BASELINE.json `metric`, configs[1]): Q4_K decode GEMV at
 14336x4096, reported as achieved HBM GB/s = algorithmic bytes per call
 (W + x + y, the reference's formula, GEMVTests.swift:1438-1440) / average
 launch duration.  One step = one GEMV call over one of >= 768 MB of distinct
-weight copies (rotated so every call misses the 256 MB Infinity Cache), with
-x and y resident in HBM.  The `--steps` launches are recorded into a HIP graph
-and replayed; HIP events on the launch stream bracket the replay (after
-`--warmup` untimed launches and UNTIMED_REPLAYS untimed replays, which let
-the clocks and the graph's first-launch work settle).
+weight copies, with x and y resident in HBM.  The `--steps` launches are
+recorded into a HIP graph and replayed; HIP events on the launch stream
+bracket the replay (after `--warmup` untimed launches and UNTIMED_REPLAYS
+untimed replays, which let the clocks and the graph's first-launch work
+settle).  With fewer steps than copies, the calls over the remaining copies
+run untimed before each replay (rotation_time_us), so at any --steps every
+timed call reads weights that >= 768 MB of other reads have pushed out of the
+256 MB Infinity Cache; each result reports its copies, timed launches and the
+distinct bytes one such cycle reads.
 
 Also reported in `results`: the other BASELINE GEMV shapes (Q8_0 3072x1024 and
 14336x4096, Q4_K 4096x14336, Q6_K 151936x1024 and 128256x4096).
@@ -102,7 +106,7 @@ def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int)
     GPU work only (no Python launch overhead); the eager, Python-launched
     rate is reported alongside."""
     import edgerunner_amd.synth as synth
-    from edgerunner_amd import Capture, GEMVKernel
+    from edgerunner_amd import GEMVKernel
 
     gemv = GEMVKernel(ctx)
     W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
@@ -116,21 +120,11 @@ def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int)
     for i in range(warmup):
         enc(stream, wbufs[i % copies], xb, yb, M, K)
     stream.synchronize()
-    with Capture(ctx, stream) as cap:
-        for i in range(steps):
-            enc(stream, wbufs[i % copies], xb, yb, M, K)
-    graph = cap.graph
-    for _ in range(UNTIMED_REPLAYS):
-        graph.launch(stream)
-    stream.synchronize()
+    avg_us = rotation_time_us(ctx, stream, lambda i: enc(stream, wbufs[i % copies], xb, yb, M, K), steps, copies)
+    ms = avg_us * steps / 1000.0
+    # eager: Python-launched back-to-back (includes host launch cost), from
+    # the cold cache state rotation_time_us leaves
     e0, e1 = ctx.event(), ctx.event()
-    e0.record(stream)
-    graph.launch(stream)
-    e1.record(stream)
-    stream.synchronize()
-    ms = e0.elapsed_ms(e1)
-    avg_us = ms * 1000.0 / steps
-    # eager: Python-launched back-to-back (includes host launch cost)
     e0.record(stream)
     for i in range(steps):
         enc(stream, wbufs[i % copies], xb, yb, M, K)
@@ -139,7 +133,6 @@ def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int)
     eager_us = e0.elapsed_ms(e1) * 1000.0 / steps
     nbytes = algorithmic_bytes(fmt, M, K)
     y = yb.download(np.float32, stream=stream)
-    graph.destroy()
     for b in wbufs:
         b.free()
     xb.free()
@@ -148,7 +141,7 @@ def bench_gemv(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int)
     e1.destroy()
     stream.destroy()
     return {
-        "fmt": fmt, "M": M, "K": K, "copies": copies, "bytes_per_call": nbytes,
+        "fmt": fmt, "M": M, "K": K, **rotation_fields(copies, W.nbytes, steps), "bytes_per_call": nbytes,
         "us_per_call": avg_us, "GBps": nbytes / (avg_us * 1e-6) / 1e9,
         "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
         "us_per_call_eager": eager_us,
@@ -161,7 +154,7 @@ def bench_top1(ctx, M: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
     one-workgroup reduce): `steps` calls over rotating weight copies in a HIP
     graph, as bench_gemv.  Bytes per call: W + x + the 4-byte index."""
     import edgerunner_amd.synth as synth
-    from edgerunner_amd import Capture, GEMVKernel
+    from edgerunner_amd import GEMVKernel
 
     gemv = GEMVKernel(ctx)
     W = synth.weights("q6_k", synth.seed(cfg, 0), M, K, **DSCALE["q6_k"])
@@ -179,27 +172,14 @@ def bench_top1(ctx, M: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
     for i in range(warmup):
         enc(i)
     stream.synchronize()
-    with Capture(ctx, stream) as cap:
-        for i in range(steps):
-            enc(i)
-    for _ in range(UNTIMED_REPLAYS):
-        cap.graph.launch(stream)
-    stream.synchronize()
-    e0, e1 = ctx.event(), ctx.event()
-    e0.record(stream)
-    cap.graph.launch(stream)
-    e1.record(stream)
-    stream.synchronize()
-    avg_us = e0.elapsed_ms(e1) * 1000.0 / steps
+    avg_us = rotation_time_us(ctx, stream, enc, steps, copies)
     nbytes = weight_bytes("q6_k", M, K) + 4 * K + 4
     idx = int(ob.download(np.uint32, 1, stream=stream)[0])
-    cap.graph.destroy()
     for b in wbufs + [xb, pv, pi, ob]:
         b.free()
-    e0.destroy()
-    e1.destroy()
     stream.destroy()
-    return {"M": M, "K": K, "copies": copies, "bytes_per_call": nbytes, "us_per_call": avg_us,
+    return {"M": M, "K": K, **rotation_fields(copies, W.nbytes, steps), "bytes_per_call": nbytes,
+            "us_per_call": avg_us,
             "GBps": nbytes / (avg_us * 1e-6) / 1e9,
             "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "launches_per_call": 2, "index": idx}
@@ -210,7 +190,7 @@ def bench_quant(ctx, rows: int, K: int, cfg: int, steps: int, warmup: int) -> di
     copies, in a HIP graph.  Bytes per call: 4 per value read + 34 per block
     written."""
     import edgerunner_amd.synth as synth
-    from edgerunner_amd import Capture, QuantizeQ8RowsKernel
+    from edgerunner_amd import QuantizeQ8RowsKernel
 
     qk = QuantizeQ8RowsKernel(ctx)
     src = synth.normal_f32(synth.seed(cfg, 9), rows * K)
@@ -221,26 +201,14 @@ def bench_quant(ctx, rows: int, K: int, cfg: int, steps: int, warmup: int) -> di
     for i in range(warmup):
         qk.encode(stream, sbufs[i % copies], db, rows, K, 0, K // 32)
     stream.synchronize()
-    with Capture(ctx, stream) as cap:
-        for i in range(steps):
-            qk.encode(stream, sbufs[i % copies], db, rows, K, 0, K // 32)
-    for _ in range(UNTIMED_REPLAYS):
-        cap.graph.launch(stream)
-    stream.synchronize()
-    e0, e1 = ctx.event(), ctx.event()
-    e0.record(stream)
-    cap.graph.launch(stream)
-    e1.record(stream)
-    stream.synchronize()
-    avg_us = e0.elapsed_ms(e1) * 1000.0 / steps
+    avg_us = rotation_time_us(ctx, stream, lambda i: qk.encode(stream, sbufs[i % copies], db, rows, K, 0, K // 32),
+                              steps, copies)
     nbytes = rows * K * 4 + rows * (K // 32) * 34
-    cap.graph.destroy()
     for b in sbufs + [db]:
         b.free()
-    e0.destroy()
-    e1.destroy()
     stream.destroy()
-    return {"rows": rows, "K": K, "copies": copies, "bytes_per_call": nbytes, "us_per_call": avg_us,
+    return {"rows": rows, "K": K, **rotation_fields(copies, src.nbytes, steps), "bytes_per_call": nbytes,
+            "us_per_call": avg_us,
             "GBps": nbytes / (avg_us * 1e-6) / 1e9,
             "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
@@ -281,7 +249,7 @@ def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warm
     """Prefill GEMM: `steps` launches over rotating weight copies, recorded
     into a HIP graph and replayed between HIP events (as bench_gemv)."""
     import edgerunner_amd.synth as synth
-    from edgerunner_amd import Capture, QuantGEMMKernel
+    from edgerunner_amd import QuantGEMMKernel
 
     gemm = QuantGEMMKernel(ctx)
     W = synth.weights(fmt, synth.seed(cfg, 0), N, K, **DSCALE[fmt])
@@ -295,32 +263,18 @@ def bench_gemm(ctx, fmt: str, T: int, N: int, K: int, cfg: int, steps: int, warm
     for i in range(warmup):
         enc(stream, wbufs[i % copies], xb, yb, T, N, K)
     stream.synchronize()
-    with Capture(ctx, stream) as cap:
-        for i in range(steps):
-            enc(stream, wbufs[i % copies], xb, yb, T, N, K)
-    graph = cap.graph
-    for _ in range(UNTIMED_REPLAYS):
-        graph.launch(stream)
-    stream.synchronize()
-    e0, e1 = ctx.event(), ctx.event()
-    e0.record(stream)
-    graph.launch(stream)
-    e1.record(stream)
-    stream.synchronize()
-    us = e0.elapsed_ms(e1) * 1000.0 / steps
+    us = rotation_time_us(ctx, stream, lambda i: enc(stream, wbufs[i % copies], xb, yb, T, N, K), steps, copies)
     y = yb.download(np.float32, count=min(T * N, 1 << 20), stream=stream)
     clock = gemm_clock(ctx, stream, fmt, wbufs, xb, yb, T, N, K)
-    graph.destroy()
     for b in wbufs:
         b.free()
     xb.free()
     yb.free()
-    e0.destroy()
-    e1.destroy()
     stream.destroy()
     flops = 2.0 * T * N * K
     tflops = flops / (us * 1e-6) / 1e12
-    out = {"fmt": fmt, "T": T, "N": N, "K": K, "us_per_call": us, "TFLOPs": tflops,
+    out = {"fmt": fmt, "T": T, "N": N, "K": K, **rotation_fields(copies, W.nbytes, steps),
+           "us_per_call": us, "TFLOPs": tflops,
            "frac_of_mfma_bf16_peak": tflops / MFMA_BF16_PEAK_TFLOPS,
            "min_bytes": gemm_min_bytes(fmt, T, N, K), "y_finite": bool(np.all(np.isfinite(y)))}
     if clock:
@@ -337,15 +291,15 @@ def gemm_clock(ctx, stream, fmt: str, wbufs, xb, yb, T: int, N: int, K: int) -> 
     give d(shader clock) / d(real time).  Empty where the loader-specialised
     kernel does not take the shape."""
     import ctypes as C
-    from edgerunner_amd import _ffi
-    lib = _ffi.load()
+    pctx = probe_context(ctx)
+    lib = pctx.lib
     nT = -(-T // 128)
     stamps = ctx.alloc(32 * nT * -(-N // 128))  # enough for either tile height
     items = C.c_uint32(0)
     typ = 12 if fmt == "q4_k" else 8  # ER_TYPE_Q4_K / ER_TYPE_Q8_0
     try:
         for i in range(CLOCK_LAUNCHES):
-            st = lib.er_hip_probe_gemm_clock(ctx.handle, stream.handle, typ, wbufs[i % len(wbufs)].raw, xb.raw, yb.raw,
+            st = lib.er_hip_probe_gemm_clock(pctx.handle, stream.handle, typ, wbufs[i % len(wbufs)].raw, xb.raw, yb.raw,
                                              T, N, K, stamps.raw, C.byref(items))
             if st != 0:
                 return {}
@@ -356,6 +310,21 @@ def gemm_clock(ctx, stream, fmt: str, wbufs, xb, yb, T: int, N: int, K: int) -> 
     mhz = (s[:, 3] - s[:, 2]) / (s[:, 1] - s[:, 0]) * 100.0
     return {"sclk_mhz": float(np.median(mhz)), "sclk_mhz_min": float(mhz.min()), "sclk_mhz_max": float(mhz.max()),
             "workgroup_us_median": float(np.median(s[:, 1] - s[:, 0]) / 100.0), "clock_workgroups": int(items.value)}
+
+
+_PROBE_CTX = {}
+
+
+def probe_context(ctx):
+    """A context of the measurement library (libedgerunner_probe.so) on ctx's
+    device, created once: the probes and the clock-stamped GEMM copy live
+    there, not in the product library.  Device buffers and streams of ctx
+    pass to it."""
+    from edgerunner_amd import Context
+    dev = int(ctx.info.device)
+    if dev not in _PROBE_CTX:
+        _PROBE_CTX[dev] = Context(dev, probes=True)
+    return _PROBE_CTX[dev]
 
 
 def bench_chain(ctx, steps: int, warmup: int) -> dict:
@@ -401,6 +370,58 @@ def bench_chain(ctx, steps: int, warmup: int) -> dict:
     return out
 
 
+def rotation_time_us(ctx, stream, enc, steps: int, copies: int) -> float:
+    """Average GPU time per call of calls enc(0..steps-1), where call i reads
+    weight copy i % copies and `copies` copies hold >= ROTATE_BYTES.  The
+    `steps` calls are recorded into one HIP graph, replayed between HIP events
+    (after UNTIMED_REPLAYS untimed replays).  When steps < copies, an untimed
+    graph of calls steps..copies-1 runs before every replay of the timed one
+    (and is left as the last work before return, so an eager loop that follows
+    starts cold too): between two reads of any copy every other copy is read,
+    >= ROTATE_BYTES - one copy, so no timed call finds its weights in the
+    256 MB Infinity Cache, whatever `steps` is."""
+    from edgerunner_amd import Capture
+    with Capture(ctx, stream) as cap:
+        for i in range(steps):
+            enc(i)
+    timed = cap.graph
+    flush = None
+    if steps < copies:
+        with Capture(ctx, stream) as cap:
+            for i in range(steps, copies):
+                enc(i)
+        flush = cap.graph
+    for _ in range(UNTIMED_REPLAYS):
+        if flush:
+            flush.launch(stream)
+        timed.launch(stream)
+    if flush:
+        flush.launch(stream)
+    stream.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record(stream)
+    timed.launch(stream)
+    e1.record(stream)
+    stream.synchronize()
+    us = e0.elapsed_ms(e1) * 1000.0 / steps
+    if flush:
+        flush.launch(stream)
+        stream.synchronize()
+        flush.destroy()
+    timed.destroy()
+    e0.destroy()
+    e1.destroy()
+    return us
+
+
+def rotation_fields(copies: int, per_call_bytes: int, steps: int) -> dict:
+    """What every rotated workload reports about its cache state: the copies,
+    the distinct bytes one cycle (timed calls + flush calls) reads, and the
+    timed calls."""
+    return {"copies": copies, "timed_launches": steps,
+            "distinct_bytes_per_cycle": max(steps, copies) * per_call_bytes}
+
+
 def _graph_time_us(ctx, stream, enc, steps: int) -> float:
     """Average GPU time per call of `steps` calls of enc(i) recorded into one
     HIP graph (after untimed replays), bracketed by HIP events."""
@@ -441,8 +462,9 @@ def bench_ceilings(ctx, steps: int) -> dict:
       - per-CU rates behind the prefill GEMM: LDS reads (A-fragment layout)
         with 4 / 8 / 16 waves per CU, and bf16 MFMA / fp32 FMA overlap within
         one wave and across two waves of a SIMD (best of 3 launches each)."""
-    import ctypes as C
-    lib = ctx.lib
+    pctx = probe_context(ctx)
+    lib = pctx.lib
+    _check = pctx.check
     stream = ctx.stream()
     out = {}
     for name, nbytes in STREAM_WORKLOADS:
@@ -453,21 +475,22 @@ def bench_ceilings(ctx, steps: int) -> dict:
         best = None
         for wgs in (1024, 2048, 4096):
             sink = ctx.alloc(wgs * 256 * 4)
-            enc = lambda i: _check(lib.er_hip_probe_stream_read(ctx.handle, stream.handle, bufs[i % copies].raw,
+            enc = lambda i: _check(lib.er_hip_probe_stream_read(pctx.handle, stream.handle, bufs[i % copies].raw,
                                                                  nbytes, wgs, sink.raw))  # noqa: E731
             for i in range(5):
                 enc(i)
-            us = _graph_time_us(ctx, stream, enc, steps)
+            us = rotation_time_us(ctx, stream, enc, steps, copies)
             sink.free()
             if best is None or us < best[0]:
                 best = (us, wgs)
         for b in bufs:
             b.free()
-        out[name] = {"bytes": nbytes, "copies": copies, "us_per_call": best[0], "workgroups": best[1],
+        out[name] = {"bytes": nbytes, **rotation_fields(copies, nbytes, steps), "us_per_call": best[0],
+                     "workgroups": best[1],
                      "GBps": nbytes / (best[0] * 1e-6) / 1e9,
                      "frac_of_hbm_peak": nbytes / (best[0] * 1e-6) / 1e9 / HBM_PEAK_GBS}
         log(f"{name}: {best[0]:.2f} us, {out[name]['GBps']:.0f} GB/s ({best[1]} workgroups)")
-    us = _graph_time_us(ctx, stream, lambda i: _check(lib.er_hip_probe_empty(ctx.handle, stream.handle)), steps)
+    us = _graph_time_us(ctx, stream, lambda i: _check(lib.er_hip_probe_empty(pctx.handle, stream.handle)), steps)
     out["empty_kernel_in_graph"] = {"us_per_launch": us, "launches": steps}
     log(f"empty kernel in a graph: {us:.2f} us per launch")
     counter, res = ctx.alloc(16), ctx.alloc(16)
@@ -477,9 +500,10 @@ def bench_ceilings(ctx, steps: int) -> dict:
         if wgs > ctx.compute_units:
             continue
         t = {}
+        res.upload(np.zeros(4, np.uint32), stream=stream)  # the launches add to it
         for r in (0, rounds, 0, rounds):
             e0.record(stream)
-            _check(lib.er_hip_probe_grid_barrier(ctx.handle, stream.handle, wgs, r, 1 << 20, counter.raw, res.raw))
+            _check(lib.er_hip_probe_grid_barrier(pctx.handle, stream.handle, wgs, r, 1 << 20, counter.raw, res.raw))
             e1.record(stream)
             stream.synchronize()
             t[r] = min(t.get(r, 1e30), e0.elapsed_ms(e1) * 1000.0)
@@ -503,12 +527,12 @@ def bench_ceilings(ctx, steps: int) -> dict:
         return best
     iters = 20000
     for waves in (4, 8, 16):
-        us = timed(lambda: _check(lib.er_hip_probe_lds_read(ctx.handle, stream.handle, waves, iters, sink.raw)))
+        us = timed(lambda: _check(lib.er_hip_probe_lds_read(pctx.handle, stream.handle, waves, iters, sink.raw)))
         per_cu = iters * 8 * 1024 * waves / (us * 1000.0)
         out[f"lds_read_{waves}_waves"] = {"us": us, "bytes_per_ns_per_cu": per_cu, "iters": iters}
         log(f"LDS reads, {waves} waves per CU: {per_cu:.0f} B/ns per CU")
     for mode, tag in enumerate(("mfma_alone", "fma_alone", "mfma_and_fma_two_waves", "mfma_and_fma_one_wave")):
-        us = timed(lambda: _check(lib.er_hip_probe_mfma_valu(ctx.handle, stream.handle, mode, iters, sink.raw)))
+        us = timed(lambda: _check(lib.er_hip_probe_mfma_valu(pctx.handle, stream.handle, mode, iters, sink.raw)))
         out[f"overlap_{tag}"] = {"us": us, "ns_per_iteration": us * 1000.0 / iters, "iters": iters}
         log(f"overlap {tag}: {us * 1000.0 / iters:.1f} ns per iteration (8 MFMA and/or 64 FMA per wave)")
     sink.free()
@@ -523,8 +547,8 @@ def bench_ceilings(ctx, steps: int) -> dict:
 def bench_chain_breakdown(ctx, steps: int) -> dict:
     """Where the decode chain's time goes: each distinct projection of a layer
     (and the head), and the fused triple / dual launches, timed alone like a
-    GEMV workload (graph of `steps` launches over >= 768 MB of rotating weight
-    copies, so each launch reads HBM as it does inside the 398 MB step).  The
+    GEMV workload (rotation_time_us over >= 768 MB of rotating weight copies,
+    so each launch reads HBM as it does inside the 398 MB step).  The
     sums per step (x 28 layers + head) are set beside the measured chain."""
     import edgerunner_amd.synth as synth
     from edgerunner_amd import GEMVKernel
@@ -552,9 +576,9 @@ def bench_chain_breakdown(ctx, steps: int) -> dict:
         f = lambda i: enc(stream, ws[i % len(ws)], xs[src], yb, M, K)  # noqa: E731
         for i in range(3):
             f(i)
-        us = _graph_time_us(ctx, stream, f, steps)
-        out[name] = {"fmt": fmt, "M": M, "K": K, "weight_bytes": wbytes, "us_per_call": us,
-                     "GBps": wbytes / (us * 1e-6) / 1e9}
+        us = rotation_time_us(ctx, stream, f, steps, len(ws))
+        out[name] = {"fmt": fmt, "M": M, "K": K, "weight_bytes": wbytes, **rotation_fields(len(ws), wbytes, steps),
+                     "us_per_call": us, "GBps": wbytes / (us * 1e-6) / 1e9}
         for b in ws:
             b.free()
         yb.free()
@@ -566,8 +590,9 @@ def bench_chain_breakdown(ctx, steps: int) -> dict:
     f = lambda i: gemv.encodeQ4KWeightsTriple(stream, tri[0][0][i % n], tri[1][0][i % n], tri[2][0][i % n],  # noqa
                                               xs["h"], ys[0], ys[1], ys[2], spec.q_dim, spec.kv_dim, spec.kv_dim,
                                               spec.hidden)
-    us = _graph_time_us(ctx, stream, f, steps)
-    out["qkv_triple"] = {"us_per_call": us, "weight_bytes": sum(w[1] for w in tri)}
+    us = rotation_time_us(ctx, stream, f, steps, n)
+    out["qkv_triple"] = {"us_per_call": us, "weight_bytes": sum(w[1] for w in tri),
+                         **rotation_fields(n, sum(w[1] for w in tri), steps)}
     for w in tri:
         for b in w[0]:
             b.free()
@@ -579,8 +604,9 @@ def bench_chain_breakdown(ctx, steps: int) -> dict:
     n = min(len(w[0]) for w in du)
     f = lambda i: gemv.encodeQ4KWeightsDual(stream, du[0][0][i % n], du[1][0][i % n], xs["h"], ys[0], ys[1],  # noqa
                                             spec.ffn, spec.hidden)
-    us = _graph_time_us(ctx, stream, f, steps)
-    out["gate_up_dual"] = {"us_per_call": us, "weight_bytes": sum(w[1] for w in du)}
+    us = rotation_time_us(ctx, stream, f, steps, n)
+    out["gate_up_dual"] = {"us_per_call": us, "weight_bytes": sum(w[1] for w in du),
+                           **rotation_fields(n, sum(w[1] for w in du), steps)}
     for w in du:
         for b in w[0]:
             b.free()
@@ -692,9 +718,10 @@ def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None, chain_steps: int
         dst.copy_from(src, stream=stream)
     stream.synchronize()
     order = []
+    pctx = probe_context(ctx)
 
     def separator():
-        _check(ctx.lib.er_hip_probe_empty(ctx.handle, stream.handle))
+        pctx.check(pctx.lib.er_hip_probe_empty(pctx.handle, stream.handle))
     gemv = GEMVKernel(ctx)
     for name, fmt, M, K, cfg in todo:
         W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
@@ -1010,8 +1037,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded xoshiro256**, BASELINE.json config distributions)",
-        "config": {"workload": "Q4_K decode GEMV, W 14336x4096 (BASELINE configs[1]), x fp32, "
-                               "y fp32, 24 rotating weight copies",
+        "config": {"workload": f"Q4_K decode GEMV, W 14336x4096 (BASELINE configs[1]), x fp32, "
+                               f"y fp32, {h['copies']} rotating weight copies",
                    "M": head[2], "K": head[3], "format": "Q4_K"},
         "roofline": {
             "bound": "hbm",

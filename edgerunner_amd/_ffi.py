@@ -14,6 +14,7 @@ PKG = Path(__file__).resolve().parent
 # ER_HIP_LIB selects another build of the same library (the sanitizer build
 # of the host-side tests); by default the in-tree library.
 LIB_PATH = Path(os.environ["ER_HIP_LIB"]) if os.environ.get("ER_HIP_LIB") else PKG / "libedgerunner_hip.so"
+PROBE_LIB_PATH = PKG / "libedgerunner_probe.so"
 
 ER_OK = 0
 STATUS_NAMES = {
@@ -204,6 +205,12 @@ SIGNATURES = {
     "er_hip_gguf_upload": (C.c_int, [_ctx_p, _stream, C.c_void_p, C.POINTER(er_buffer)]),
     "er_gguf_tensor_storage": (C.c_int, [C.c_void_p, C.c_uint64, er_buffer,
                                          C.POINTER(er_tensor_storage)]),
+    "er_hip_encode_projection": (
+        C.c_int, [_ctx_p, _stream, C.POINTER(er_tensor_storage), er_buffer, er_buffer, _u32]),
+}
+
+# The measurement library's extra entry points (csrc/er_hip_probe.h).
+PROBE_SIGNATURES = {
     "er_hip_probe_stream_read": (C.c_int, [_ctx_p, _stream, er_buffer, _u64, _u32, er_buffer]),
     "er_hip_probe_empty": (C.c_int, [_ctx_p, _stream]),
     "er_hip_probe_grid_barrier": (C.c_int, [_ctx_p, _stream, _u32, _u32, _u32, er_buffer, er_buffer]),
@@ -211,35 +218,50 @@ SIGNATURES = {
     "er_hip_probe_mfma_valu": (C.c_int, [_ctx_p, _stream, _u32, _u32, er_buffer]),
     "er_hip_probe_gemm_clock": (C.c_int, [_ctx_p, _stream, C.c_int, er_buffer, er_buffer, er_buffer, _u32, _u32, _u32,
                                           er_buffer, C.POINTER(C.c_uint32)]),
-    "er_hip_encode_projection": (
-        C.c_int, [_ctx_p, _stream, C.POINTER(er_tensor_storage), er_buffer, er_buffer, _u32]),
 }
 
 _lib = None
+_probe_lib = None
 
 
 class LibraryMissing(RuntimeError):
     pass
 
 
-def load() -> C.CDLL:
-    """Load libedgerunner_hip.so and bind every declared entry point."""
-    global _lib
-    if _lib is not None:
-        return _lib
-    if not LIB_PATH.exists():
+def _bind(path: Path, signatures: dict) -> C.CDLL:
+    if not path.exists():
         raise LibraryMissing(
-            f"{LIB_PATH} is not built; run `python -m edgerunner_amd.build` "
+            f"{path} is not built; run `python -m edgerunner_amd.build` "
             "(the HIP library is required, there is no CPU fallback)")
-    lib = C.CDLL(str(LIB_PATH))
-    for name, (res, args) in SIGNATURES.items():
+    lib = C.CDLL(str(path))
+    for name, (res, args) in signatures.items():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    _lib = lib
     return lib
 
 
-def last_error() -> str:
-    msg = load().er_hip_last_error()
+def load() -> C.CDLL:
+    """Load libedgerunner_hip.so and bind every declared entry point."""
+    global _lib
+    if _lib is None:
+        _lib = _bind(LIB_PATH, SIGNATURES)
+    return _lib
+
+
+def load_probe() -> C.CDLL:
+    """Load the measurement library (libedgerunner_probe.so: every entry point
+    of the product library plus the probes), for bench.py's ceilings and GEMM
+    clock legs.  Its contexts, like its entry points, are its own; device
+    buffers are plain device memory and pass between the two."""
+    global _probe_lib
+    if _probe_lib is None:
+        _probe_lib = _bind(PROBE_LIB_PATH, {**SIGNATURES, **PROBE_SIGNATURES})
+    return _probe_lib
+
+
+def last_error(lib: C.CDLL | None = None) -> str:
+    """The calling thread's last error message of `lib` (default: the product
+    library)."""
+    msg = (lib or load()).er_hip_last_error()
     return msg.decode() if msg else ""

@@ -1,9 +1,13 @@
 """Build the gfx950 code object and the host libraries in-tree.
 
 Produces (next to this file, so they travel with the source tree):
-  libedgerunner_hip.so -- the C-ABI library (include/er_hip.h) with the gfx950
-                          code object embedded
-  liber_synth.so       -- seeded synthetic workload generator (host only)
+  libedgerunner_hip.so   -- the C-ABI library (include/er_hip.h, er_gguf.h) with
+                            the gfx950 code object embedded
+  libedgerunner_probe.so -- the measurement library: the same sources built with
+                            -DER_WITH_PROBES (every er_hip.h entry point plus
+                            csrc/er_hip_probe.h); bench.py's ceilings and GEMM
+                            clock legs only
+  liber_synth.so         -- seeded synthetic workload generator (host only)
 
 Usage: python -m edgerunner_amd.build
 """
@@ -34,8 +38,11 @@ DEVICE_FLAGS = [
 ]
 
 LIB = PKG / "libedgerunner_hip.so"
+PROBE_LIB = PKG / "libedgerunner_probe.so"
 SYNTH = PKG / "liber_synth.so"
 CODE_OBJECT = BUILD / "er_kernels.hsaco"
+PROBE_CODE_OBJECT = BUILD / "er_kernels_probe.hsaco"
+PROBE_DEFINES = ["-DER_WITH_PROBES=1"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -43,11 +50,29 @@ def _run(cmd: list[str]) -> None:
     subprocess.run(cmd, check=True)
 
 
-def build_code_object(extra: list[str] | None = None) -> Path:
+def _code_object_cmd(out: Path, extra: list[str] | None = None) -> list[str]:
+    return [HIPCC, *DEVICE_FLAGS, *(extra or []), "--genco", "-I", str(CSRC),
+            str(CSRC / "er_kernels.hip"), "-o", str(out)]
+
+
+def build_code_object(extra: list[str] | None = None, out: Path = CODE_OBJECT) -> Path:
     BUILD.mkdir(exist_ok=True)
-    _run([HIPCC, *DEVICE_FLAGS, *(extra or []), "--genco", "-I", str(CSRC),
-          str(CSRC / "er_kernels.hip"), "-o", str(CODE_OBJECT)])
-    return CODE_OBJECT
+    _run(_code_object_cmd(out, extra))
+    return out
+
+
+def build_code_objects() -> None:
+    """The product and the measurement code objects, compiled concurrently
+    (one hipcc process each)."""
+    BUILD.mkdir(exist_ok=True)
+    cmds = [_code_object_cmd(CODE_OBJECT), _code_object_cmd(PROBE_CODE_OBJECT, PROBE_DEFINES)]
+    procs = []
+    for c in cmds:
+        print("+", " ".join(c), flush=True)
+        procs.append(subprocess.Popen(c))
+    bad = [c for c, p in zip(cmds, procs) if p.wait() != 0]
+    if bad:
+        raise subprocess.CalledProcessError(1, bad[0])
 
 
 def _blob_source(code_object: Path) -> str:
@@ -63,16 +88,17 @@ def _blob_source(code_object: Path) -> str:
             "    .section .note.GNU-stack,\"\",@progbits\n")
 
 
-def build_host_library(code_object: Path = CODE_OBJECT, out: Path = LIB) -> Path:
+def build_host_library(code_object: Path = CODE_OBJECT, out: Path = LIB, defines: list[str] | None = None) -> Path:
     BUILD.mkdir(exist_ok=True)
-    blob = BUILD / "er_blob.S"
+    tag = out.stem
+    blob = BUILD / f"{tag}_blob.S"
     blob.write_text(_blob_source(code_object))
-    blob_o = BUILD / "er_blob.o"
-    host_o = BUILD / "er_hip.o"
+    blob_o = BUILD / f"{tag}_blob.o"
+    host_o = BUILD / f"{tag}_er_hip.o"
     _run(["gcc", "-c", str(blob), "-o", str(blob_o)])
-    gguf_o = BUILD / "er_gguf.o"
+    gguf_o = BUILD / f"{tag}_er_gguf.o"
     for src, obj in ((CSRC / "er_hip.cpp", host_o), (CSRC / "er_gguf.cpp", gguf_o)):
-        _run(["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+        _run(["g++", "-O2", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__", *(defines or []),
               "-I", str(ROCM / "include"), "-I", str(ROOT / "include"), "-I", str(CSRC),
               "-c", str(src), "-o", str(obj)])
     tmp = out.with_suffix(".so.tmp")
@@ -125,8 +151,9 @@ def build_synth() -> Path:
 
 
 def build_all() -> None:
-    build_code_object()
+    build_code_objects()
     build_host_library()
+    build_host_library(PROBE_CODE_OBJECT, PROBE_LIB, PROBE_DEFINES)
     build_synth()
 
 

@@ -726,16 +726,17 @@ ER_DEV void gemml_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// stamps (null in the product path): thread 0 of each work item's
-// workgroup writes stamps[4 item ..] = the 100 MHz real-time counter and the
-// shader-clock counter at its start and after its epilogue, so the clock the
-// workgroup ran at is d(shader clock) / d(real time) x 100 MHz.
-template <bool Q4K, int R>
+// STAMPED (the measurement build's clock probe only; the product kernels are
+// built without it): thread 0 of each work item's workgroup writes
+// stamps[4 item ..] = the 100 MHz real-time counter and the shader-clock
+// counter at its start and after its epilogue, so the clock the workgroup ran
+// at is d(shader clock) / d(real time) x 100 MHz.
+template <bool Q4K, int R, bool STAMPED = false>
 ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y,
-                    uint32_t T, uint32_t N, uint32_t K, uint64_t *__restrict__ stamps) {
+                    uint32_t T, uint32_t N, uint32_t K, uint64_t *__restrict__ stamps = nullptr) {
     using G = GemmL<Q4K, R>;
     uint64_t rt0 = 0, ct0 = 0;
-    if (stamps) {
+    if constexpr (STAMPED) {
         rt0 = __builtin_amdgcn_s_memrealtime();
         ct0 = __builtin_amdgcn_s_memtime();
     }
@@ -970,7 +971,7 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
                 *(float *)((uint8_t *)Y + (t * N + nc) * 4u) = acc[f][i][r];
             }
     }
-    if (stamps && threadIdx.x == 0) {
+    if (STAMPED && threadIdx.x == 0) {
         const uint64_t rt1 = __builtin_amdgcn_s_memrealtime(), ct1 = __builtin_amdgcn_s_memtime();
         stamps[4u * item + 0u] = rt0;
         stamps[4u * item + 1u] = rt1;
@@ -982,11 +983,25 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
 #define ER_GEMML_ENTRY(name, q4k, r)                                                                         \
     extern "C" __global__ void __launch_bounds__(512, 1)                                                     \
         name(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y, uint32_t T, \
-             uint32_t N, uint32_t K, uint64_t *__restrict__ stamps) {                                        \
-        gemm_ls<q4k, r>(W, X, Y, T, N, K, stamps);                                                           \
+             uint32_t N, uint32_t K) {                                                                       \
+        gemm_ls<q4k, r>(W, X, Y, T, N, K);                                                                   \
     }
 
 ER_GEMML_ENTRY(er_gemml_q4k, true, 2)
 ER_GEMML_ENTRY(er_gemml_q8_0, false, 2)
 ER_GEMML_ENTRY(er_gemml_q4k_r1, true, 1)
 ER_GEMML_ENTRY(er_gemml_q8_0_r1, false, 1)
+
+#ifdef ER_WITH_PROBES
+// measurement build: the same kernels with per-workgroup clock stamps
+#define ER_GEMML_STAMPED_ENTRY(name, q4k, r)                                                                 \
+    extern "C" __global__ void __launch_bounds__(512, 1)                                                     \
+        name(const uint8_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ Y, uint32_t T, \
+             uint32_t N, uint32_t K, uint64_t *__restrict__ stamps) {                                        \
+        gemm_ls<q4k, r, true>(W, X, Y, T, N, K, stamps);                                                     \
+    }
+ER_GEMML_STAMPED_ENTRY(er_gemml_q4k_stamped, true, 2)
+ER_GEMML_STAMPED_ENTRY(er_gemml_q8_0_stamped, false, 2)
+ER_GEMML_STAMPED_ENTRY(er_gemml_q4k_r1_stamped, true, 1)
+ER_GEMML_STAMPED_ENTRY(er_gemml_q8_0_r1_stamped, false, 1)
+#endif

@@ -1,4 +1,7 @@
 // er_hip.cpp -- host side of the EdgeRunnerHIP C ABI (include/er_hip.h).
+// Built a second time with -DER_WITH_PROBES (and the code object built the
+// same way) as libedgerunner_probe.so, the measurement library: the same
+// entry points plus er_hip_probe.h.
 //
 // The gfx950 code object is embedded in this library at build time
 // (er_blob.S) and loaded with hipModuleLoadData; kernels are resolved by name
@@ -9,7 +12,9 @@
 // (Sources/EdgeRunnerMetal/GEMVKernel.swift:1276-1300, 1415-1432) and the
 // Dequant*Kernel.dequantise checks (Sources/EdgeRunnerIO/DequantQ4KMKernel.swift:23-29).
 #include "er_hip.h"
+#ifdef ER_WITH_PROBES
 #include "er_hip_probe.h"
+#endif
 #include "er_error.h"
 #include "er_gemv_cfg.h"
 #include "er_scratch.h"
@@ -97,11 +102,22 @@ using er_detail::fail;
     X(GEMML_Q8_0, "er_gemml_q8_0")                                                     \
     X(GEMML_Q4K_R1, "er_gemml_q4k_r1")                                                 \
     X(GEMML_Q8_0_R1, "er_gemml_q8_0_r1")                                               \
+    ER_PROBE_KERNEL_LIST(X)
+
+#ifdef ER_WITH_PROBES
+#define ER_PROBE_KERNEL_LIST(X)                                                        \
+    X(GEMML_Q4K_STAMPED, "er_gemml_q4k_stamped")                                       \
+    X(GEMML_Q8_0_STAMPED, "er_gemml_q8_0_stamped")                                     \
+    X(GEMML_Q4K_R1_STAMPED, "er_gemml_q4k_r1_stamped")                                 \
+    X(GEMML_Q8_0_R1_STAMPED, "er_gemml_q8_0_r1_stamped")                               \
     X(PROBE_STREAM_READ, "er_probe_stream_read")                                       \
     X(PROBE_EMPTY, "er_probe_empty")                                                   \
     X(PROBE_GRID_BARRIER, "er_probe_grid_barrier")                                     \
     X(PROBE_LDS_READ, "er_probe_lds_read")                                             \
     X(PROBE_MFMA_VALU, "er_probe_mfma_valu")
+#else
+#define ER_PROBE_KERNEL_LIST(X)
+#endif
 
 enum KernelId {
 #define ER_ENUM(id, name) K_##id,
@@ -779,7 +795,8 @@ GemmLPlan plan_gemml(const er_hip_ctx *ctx, uint32_t T, uint32_t N, uint32_t K) 
     return p;
 }
 
-// stamps: null, or 32 bytes per work item (the kernel's clock stamps)
+// stamps: null, or (measurement build) 32 bytes per work item for the
+// clock-stamped copy of the kernel
 er_status launch_gemml(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_buffer x, er_buffer y, uint32_t T,
                        uint32_t N, uint32_t K, const GemmLPlan &p, uint64_t *stamps) {
     void *args[] = {&W.data, &x.data, &y.data, &T, &N, &K, &stamps};
@@ -792,8 +809,13 @@ er_status launch_gemml(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er
     if (lds > ctx->info.lds_per_workgroup)
         return fail(ER_ERR_ENCODING_FAILED, "GEMM: %u B of LDS per workgroup needed, %u available", lds,
                     (unsigned)ctx->info.lds_per_workgroup);
-    const KernelId k = f == Fmt::Q4_K ? (p.r == 2 ? K_GEMML_Q4K : K_GEMML_Q4K_R1)
-                                      : (p.r == 2 ? K_GEMML_Q8_0 : K_GEMML_Q8_0_R1);
+    KernelId k = f == Fmt::Q4_K ? (p.r == 2 ? K_GEMML_Q4K : K_GEMML_Q4K_R1)
+                                : (p.r == 2 ? K_GEMML_Q8_0 : K_GEMML_Q8_0_R1);
+#ifdef ER_WITH_PROBES
+    if (stamps)
+        k = f == Fmt::Q4_K ? (p.r == 2 ? K_GEMML_Q4K_STAMPED : K_GEMML_Q4K_R1_STAMPED)
+                           : (p.r == 2 ? K_GEMML_Q8_0_STAMPED : K_GEMML_Q8_0_R1_STAMPED);
+#endif
     return launch(ctx, k, dim3((uint32_t)(8u * ((p.tiles + 7u) / 8u)), 1, 1), dim3(512, 1, 1), lds, stream, args);
 }
 
@@ -1798,7 +1820,8 @@ er_status er_hip_encode_projection(er_hip_ctx *ctx, er_stream stream,
 
 }  // extern "C"
 
-// ---- measurement kernels (include/er_hip_probe.h) ----
+#ifdef ER_WITH_PROBES
+// ---- measurement kernels (er_hip_probe.h; the measurement library only) ----
 
 // One workgroup per CU for the per-CU rate probes: 96 KB of LDS each, so no
 // second workgroup fits beside it.
@@ -1886,9 +1909,7 @@ er_status er_hip_probe_grid_barrier(er_hip_ctx *ctx, er_stream stream, uint32_t 
     void *za[] = {&counter.data, &one};
     st = launch(ctx, K_FILL_ZERO, dim3(1, 1, 1), dim3(256, 1, 1), 0, stream, za);
     if (st != ER_OK) return st;
-    void *zb[] = {&out.data, &one};
-    st = launch(ctx, K_FILL_ZERO, dim3(1, 1, 1), dim3(256, 1, 1), 0, stream, zb);
-    if (st != ER_OK) return st;
     void *args[] = {&counter.data, &rounds, &spin_limit, &out.data};
     return launch(ctx, K_PROBE_GRID_BARRIER, dim3(workgroups, 1, 1), dim3(64, 1, 1), 0, stream, args);
 }
+#endif  // ER_WITH_PROBES

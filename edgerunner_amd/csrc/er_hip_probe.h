@@ -1,10 +1,13 @@
 /*
  * er_hip_probe.h -- measurement entry points of EdgeRunnerHIP.
  *
- * Not part of the drop-in interface (no reference counterpart): kernels
- * whose timings are the ceilings the GEMV and decode-chain designs are
- * measured against (bench.py's "ceilings" leg), launched through the same
- * context, streams and graphs as the product entry points.
+ * Not part of the drop-in interface (no reference counterpart) and not in
+ * the product library: libedgerunner_probe.so, the measurement build of the
+ * same sources (-DER_WITH_PROBES), exports them beside every er_hip.h entry
+ * point.  Kernels whose timings are the ceilings the GEMV and decode-chain
+ * designs are measured against (bench.py's "ceilings" leg) and a
+ * clock-stamped copy of the prefill GEMM, launched through a context of that
+ * library on the same streams and graphs as the product entry points.
  */
 #ifndef ER_HIP_PROBE_H
 #define ER_HIP_PROBE_H
@@ -35,10 +38,11 @@ er_status er_hip_probe_gemm_clock(er_hip_ctx *ctx, er_stream stream, er_tensor_t
 /* One launch of an empty 64-thread kernel. */
 er_status er_hip_probe_empty(er_hip_ctx *ctx, er_stream stream);
 /* `rounds` grid-wide barriers across `workgroups` single-wave workgroups
- * (1 <= workgroups <= the CU count, so all are resident).  counter and out
- * (16 bytes each, 16-byte aligned) are cleared by a fill kernel first; every
- * wait is bounded by spin_limit polls; out[0] receives the total polls and
- * out[1] the number of waits that ran out (uint32 each). */
+ * (1 <= workgroups <= the CU count, so all are resident).  counter (16
+ * bytes, 16-byte aligned) is cleared by a fill kernel first; every wait is
+ * bounded by spin_limit polls; the launch adds its total polls to out[0] and
+ * the number of waits that ran out to out[1] (uint32 each, 16 bytes, 16-byte
+ * aligned), so out sums over the launches since the caller last cleared it. */
 er_status er_hip_probe_grid_barrier(er_hip_ctx *ctx, er_stream stream, uint32_t workgroups, uint32_t rounds,
                                     uint32_t spin_limit, er_buffer counter, er_buffer out);
 

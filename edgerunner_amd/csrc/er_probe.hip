@@ -1,4 +1,5 @@
-// er_probe.hip -- measurement kernels behind include/er_hip_probe.h: the
+// er_probe.hip -- measurement kernels behind er_hip_probe.h (built only into
+// the measurement library, -DER_WITH_PROBES): the
 // ceilings the GEMV and decode-chain designs are judged against, measured
 // with the same launch machinery as the product kernels.
 //

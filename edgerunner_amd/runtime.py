@@ -117,11 +117,13 @@ _BY_STATUS = {cls.status: cls for cls in (
     TensorNotFound)}
 
 
-def check(status: int) -> None:
+def check(status: int, lib=None) -> None:
+    """Raise the error class of a non-OK status with the message `lib` (the
+    library that returned it; default the product library) recorded."""
     if status == _ffi.ER_OK:
         return
     cls = _BY_STATUS.get(status, EdgeRunnerHIPError)
-    raise cls(f"{_ffi.STATUS_NAMES.get(status, status)}: {_ffi.last_error()}")
+    raise cls(f"{_ffi.STATUS_NAMES.get(status, status)}: {_ffi.last_error(lib)}")
 
 
 # --------------------------------------------------------------------------- objects
@@ -151,7 +153,7 @@ class Buffer:
 
     def upload(self, host: np.ndarray, offset: int = 0, stream: "Optional[Stream]" = None) -> None:
         a = np.ascontiguousarray(host)
-        check(self.ctx.lib.er_hip_upload(self.ctx.handle, _sh(stream), self.raw, offset,
+        self.ctx.check(self.ctx.lib.er_hip_upload(self.ctx.handle, _sh(stream), self.raw, offset,
                                          a.ctypes.data_as(C.c_void_p), a.nbytes))
 
     def download(self, dtype, count: Optional[int] = None, offset: int = 0,
@@ -160,7 +162,7 @@ class Buffer:
         if count is None:
             count = (self.length - offset) // dtype.itemsize
         out = np.empty(count, dtype=dtype)
-        check(self.ctx.lib.er_hip_download(self.ctx.handle, _sh(stream),
+        self.ctx.check(self.ctx.lib.er_hip_download(self.ctx.handle, _sh(stream),
                                            out.ctypes.data_as(C.c_void_p), self.raw, offset,
                                            out.nbytes))
         return out
@@ -169,12 +171,12 @@ class Buffer:
                   src_offset: int = 0, stream: "Optional[Stream]" = None) -> None:
         """Device-to-device copy enqueued on `stream`."""
         n = src.length - src_offset if nbytes is None else nbytes
-        check(self.ctx.lib.er_hip_copy(self.ctx.handle, _sh(stream), self.raw, dst_offset, src.raw,
+        self.ctx.check(self.ctx.lib.er_hip_copy(self.ctx.handle, _sh(stream), self.raw, dst_offset, src.raw,
                                        src_offset, n))
 
     def free(self) -> None:
         if self.owned and self.raw.data:
-            check(self.ctx.lib.er_hip_free(self.ctx.handle, self.raw))
+            self.ctx.check(self.ctx.lib.er_hip_free(self.ctx.handle, self.raw))
         self.raw = _ffi.er_buffer(None, 0)
 
     def __del__(self):
@@ -189,15 +191,15 @@ class Stream:
     def __init__(self, ctx: "Context"):
         self.ctx = ctx
         h = C.c_void_p()
-        check(ctx.lib.er_hip_stream_create(ctx.handle, C.byref(h)))
+        ctx.check(ctx.lib.er_hip_stream_create(ctx.handle, C.byref(h)))
         self.handle = h
 
     def synchronize(self) -> None:
-        check(self.ctx.lib.er_hip_synchronize(self.ctx.handle, self.handle))
+        self.ctx.check(self.ctx.lib.er_hip_synchronize(self.ctx.handle, self.handle))
 
     def destroy(self) -> None:
         if self.handle:
-            check(self.ctx.lib.er_hip_stream_destroy(self.ctx.handle, self.handle))
+            self.ctx.check(self.ctx.lib.er_hip_stream_destroy(self.ctx.handle, self.handle))
             self.handle = C.c_void_p()
 
 
@@ -205,21 +207,21 @@ class Event:
     def __init__(self, ctx: "Context"):
         self.ctx = ctx
         h = C.c_void_p()
-        check(ctx.lib.er_hip_event_create(ctx.handle, C.byref(h)))
+        ctx.check(ctx.lib.er_hip_event_create(ctx.handle, C.byref(h)))
         self.handle = h
 
     def record(self, stream: "Optional[Stream]" = None) -> None:
-        check(self.ctx.lib.er_hip_event_record(self.ctx.handle, self.handle, _sh(stream)))
+        self.ctx.check(self.ctx.lib.er_hip_event_record(self.ctx.handle, self.handle, _sh(stream)))
 
     def elapsed_ms(self, end: "Event") -> float:
         ms = C.c_float()
-        check(self.ctx.lib.er_hip_event_elapsed_ms(self.ctx.handle, self.handle, end.handle,
+        self.ctx.check(self.ctx.lib.er_hip_event_elapsed_ms(self.ctx.handle, self.handle, end.handle,
                                                    C.byref(ms)))
         return float(ms.value)
 
     def destroy(self) -> None:
         if self.handle:
-            check(self.ctx.lib.er_hip_event_destroy(self.ctx.handle, self.handle))
+            self.ctx.check(self.ctx.lib.er_hip_event_destroy(self.ctx.handle, self.handle))
             self.handle = C.c_void_p()
 
 
@@ -231,11 +233,11 @@ class Graph:
         self.handle = handle
 
     def launch(self, stream: "Optional[Stream]" = None) -> None:
-        check(self.ctx.lib.er_hip_graph_launch(self.ctx.handle, self.handle, _sh(stream)))
+        self.ctx.check(self.ctx.lib.er_hip_graph_launch(self.ctx.handle, self.handle, _sh(stream)))
 
     def destroy(self) -> None:
         if self.handle:
-            check(self.ctx.lib.er_hip_graph_destroy(self.ctx.handle, self.handle))
+            self.ctx.check(self.ctx.lib.er_hip_graph_destroy(self.ctx.handle, self.handle))
             self.handle = C.c_void_p()
 
 
@@ -253,14 +255,14 @@ class Capture:
         self.graph: Optional[Graph] = None
 
     def __enter__(self) -> "Capture":
-        check(self.ctx.lib.er_hip_graph_begin(self.ctx.handle, self.stream.handle))
+        self.ctx.check(self.ctx.lib.er_hip_graph_begin(self.ctx.handle, self.stream.handle))
         return self
 
     def __exit__(self, exc_type, exc, tb) -> bool:
         h = C.c_void_p()
         st = self.ctx.lib.er_hip_graph_end(self.ctx.handle, self.stream.handle, C.byref(h))
         if exc_type is None:
-            check(st)
+            self.ctx.check(st)
             self.graph = Graph(self.ctx, h)
         elif st == _ffi.ER_OK and h:
             self.ctx.lib.er_hip_graph_destroy(self.ctx.handle, h)
@@ -274,14 +276,18 @@ def _sh(stream: Optional[Stream]):
 class Context:
     """One GPU with the gfx950 code object loaded and every kernel resolved."""
 
-    def __init__(self, device: int = 0):
-        self.lib = _ffi.load()
+    def __init__(self, device: int = 0, probes: bool = False):
+        # probes: a context of the measurement library (libedgerunner_probe.so)
+        self.lib = _ffi.load_probe() if probes else _ffi.load()
         h = C.c_void_p()
-        check(self.lib.er_hip_create(device, C.byref(h)))
+        self.check(self.lib.er_hip_create(device, C.byref(h)))
         self.handle = h
         info = _ffi.er_device_info()
-        check(self.lib.er_hip_get_device_info(self.handle, C.byref(info)))
+        self.check(self.lib.er_hip_get_device_info(self.handle, C.byref(info)))
         self.info = info
+
+    def check(self, status: int) -> None:
+        check(status, self.lib)
 
     @property
     def compute_units(self) -> int:
@@ -293,7 +299,7 @@ class Context:
 
     def alloc(self, nbytes: int) -> Buffer:
         raw = _ffi.er_buffer()
-        check(self.lib.er_hip_alloc(self.handle, nbytes, C.byref(raw)))
+        self.check(self.lib.er_hip_alloc(self.handle, nbytes, C.byref(raw)))
         return Buffer(self, raw)
 
     def upload(self, host: np.ndarray, stream: Optional[Stream] = None) -> Buffer:
@@ -309,7 +315,7 @@ class Context:
         return Event(self)
 
     def synchronize(self, stream: Optional[Stream] = None) -> None:
-        check(self.lib.er_hip_synchronize(self.handle, _sh(stream)))
+        self.check(self.lib.er_hip_synchronize(self.handle, _sh(stream)))
 
     def close(self) -> None:
         if self.handle:

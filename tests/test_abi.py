@@ -215,3 +215,25 @@ def test_noalloc_top1_rejects_heads_past_the_array():
     M = max_rows
     st = lib.er_hip_encode_q6k_weights_packed_top1_noalloc(None, None, _buf(M * 210), _buf(4 * K), _buf(4), M, K)
     assert st == 8
+
+
+def _exported(path):
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_product_library_exports_exactly_the_boundary():
+    """libedgerunner_hip.so exports what include/*.h declares and nothing
+    else: no measurement entry point (those live in libedgerunner_probe.so)."""
+    exported = _exported(_ffi.LIB_PATH)
+    declared = set(declared_symbols()) | {"er_status_string"}
+    assert exported == declared, (sorted(exported - declared), sorted(declared - exported))
+
+
+def test_probe_library_is_a_superset():
+    if not _ffi.PROBE_LIB_PATH.exists():
+        pytest.skip("measurement library not built")
+    exported = _exported(_ffi.PROBE_LIB_PATH)
+    assert set(declared_symbols()) <= exported
+    assert set(_ffi.PROBE_SIGNATURES) <= exported

@@ -145,22 +145,25 @@ def test_validation(ctx, gemm):
 
 @pytest.mark.parametrize("fmt,T,N,items", [("q4_k", 512, 4096, 128), ("q8_0", 512, 14336, 224)])
 def test_clock_probe(ctx, gemm, fmt, T, N, items):
-    """er_hip_probe_gemm_clock runs the product kernel: Y is bit-identical to
-    the plain call, one stamp set per work item (128-row tiles at N = 4096,
-    256-row tiles at 14336), each with both counters advancing and a clock
-    between 100 MHz and 3.5 GHz."""
+    """er_hip_probe_gemm_clock (the measurement library) runs a stamped copy
+    of the product kernel: Y is bit-identical to the product library's call,
+    one stamp set per work item (128-row tiles at N = 4096, 256-row tiles at
+    14336), each with both counters advancing and a clock between 100 MHz and
+    3.5 GHz.  Buffers of the product context pass to the measurement
+    library's context (plain device memory)."""
     import ctypes as C
-    from edgerunner_amd import _ffi
+    from edgerunner_amd import Context
     K = 1024
     W, X = case(fmt, T, N, K, 5)
     want = gemm.execute(fmt, W, X, T, N, K)
-    lib = _ffi.load()
+    pctx = Context(ctx.info.device, probes=True)
+    lib = pctx.lib
     typ = 12 if fmt == "q4_k" else 8
     wb, xb, yb = ctx.upload(W), ctx.upload(X), ctx.alloc(4 * T * N)
     stamps = ctx.alloc(32 * items)
     n = C.c_uint32(0)
     try:
-        assert lib.er_hip_probe_gemm_clock(ctx.handle, None, typ, wb.raw, xb.raw, yb.raw, T, N, K, stamps.raw,
+        assert lib.er_hip_probe_gemm_clock(pctx.handle, None, typ, wb.raw, xb.raw, yb.raw, T, N, K, stamps.raw,
                                            C.byref(n)) == 0
         ctx.synchronize()
         assert n.value == items
@@ -173,14 +176,15 @@ def test_clock_probe(ctx, gemm, fmt, T, N, items):
         # too few stamps, a shape the kernel does not take, a format without it
         small = ctx.alloc(32 * items - 8)
         try:
-            assert lib.er_hip_probe_gemm_clock(ctx.handle, None, typ, wb.raw, xb.raw, yb.raw, T, N, K, small.raw,
+            assert lib.er_hip_probe_gemm_clock(pctx.handle, None, typ, wb.raw, xb.raw, yb.raw, T, N, K, small.raw,
                                                C.byref(n)) != 0
         finally:
             small.free()
-        assert lib.er_hip_probe_gemm_clock(ctx.handle, None, typ, wb.raw, xb.raw, yb.raw, 33, 64, K, stamps.raw,
+        assert lib.er_hip_probe_gemm_clock(pctx.handle, None, typ, wb.raw, xb.raw, yb.raw, 33, 64, K, stamps.raw,
                                            C.byref(n)) != 0
-        assert lib.er_hip_probe_gemm_clock(ctx.handle, None, 14, wb.raw, xb.raw, yb.raw, T, N, K, stamps.raw,
+        assert lib.er_hip_probe_gemm_clock(pctx.handle, None, 14, wb.raw, xb.raw, yb.raw, T, N, K, stamps.raw,
                                            C.byref(n)) != 0
     finally:
         for b in (wb, xb, yb, stamps):
             b.free()
+        pctx.close()
