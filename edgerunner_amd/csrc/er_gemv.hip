@@ -186,13 +186,14 @@ ER_DEV void gemv_q4k_i8_core(const uint8_t *const (&rowp)[R], float *const (&yro
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    if (nf_any_chunk(X.x16, K >> 4)) {
+    const bool ill = xl_ill(X, 4.0f);
+    if (ill || nf_any_chunk(X.x16, K >> 4)) {
         float sp[R], hits = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sp[r] = 0.0f;
         const uint32_t ln = lane_id();
         nf_terms<R>([&](int r, uint32_t k) { return q4k_weight_at(rowAt(ln, r), k); },
-                    [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, ln % LPR, LPR, sp, hits);
+                    [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, ln % LPR, LPR, sp, hits, ill);
         hits = group_sum<LPR>(hits);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -412,7 +413,8 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    if (nf_any_chunk(X.x16, K >> 4)) {
+    const bool ill = xl_ill(X, 1.0f);
+    if (ill || nf_any_chunk(X.x16, K >> 4)) {
         float sp[R], hits = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sp[r] = 0.0f;
@@ -421,7 +423,7 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
         nf_terms<R>([&](int r, uint32_t k) {
                         return q8_0_weight_at(W + (size_t)min(fr0 + (uint32_t)r, M - 1u) * rowBytes, k);
                     },
-                    [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, ln % LPR, LPR, sp, hits);
+                    [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, ln % LPR, LPR, sp, hits, ill);
         hits = group_sum<LPR>(hits);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -528,7 +530,8 @@ ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    if (nf_any_chunk(X.x16, C16)) {
+    const bool ill = xl_ill(X, 1.0f);
+    if (ill || nf_any_chunk(X.x16, C16)) {
         // the staged values: x, or x * rms * normW as the prologue formed them
         // (rms recomputed from the same wave sums, so it is the same value)
         float rms = 1.0f;
@@ -544,7 +547,7 @@ ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const
         const uint32_t ln = lane_id();
         nf_terms<R>([&](int r, uint32_t k) { return q8_0_weight_at(rowAt(ln, r), k); },
                     [&](uint32_t k) { return normW ? x[k] * rms * normW[k] : x[k]; }, X.x16, C16, ln % LPR, LPR,
-                    sp, hits);
+                    sp, hits, ill);
         hits = group_sum<LPR>(hits);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -896,7 +899,8 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    if (nf_any_chunk(X.x16, K >> 4)) {
+    const bool ill = xl_ill(X, 4.0f);
+    if (ill || nf_any_chunk(X.x16, K >> 4)) {
         float sp[R], hits = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sp[r] = 0.0f;
@@ -905,7 +909,7 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
         nf_terms<R>([&](int r, uint32_t k) {
                         return q6k_weight_at(W + (size_t)min(fr0 + (uint32_t)r, M - 1u) * rowBytes, k);
                     },
-                    [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, ln % LPR, LPR, sp, hits);
+                    [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, ln % LPR, LPR, sp, hits, ill);
         hits = group_sum<LPR>(hits);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -1295,7 +1299,23 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) step(i0, u, true);
-    if (nf_any_chunk(X.x16, K >> 4)) {
+    const bool ill = xl_ill(X, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f);
+    if (ill) {
+        // x the limbs do not carry precisely enough: every row of this lane
+        // group again, in fp32 over every position from the raw weights, the
+        // group's lanes splitting the 16-value chunks as the lane-group kernels
+        // do; the sum of step st is parked where the row loop parked it
+#pragma unroll 1
+        for (uint32_t st = 0; st < J; ++st) {
+            const uint32_t row = min(rowAt(st, wave, g), M - 1u);
+            float sp1[1] = {0.0f}, h = 0.0f;
+            nf_terms<1>([&](int, uint32_t k) { return weight_at<F::FMT>(W + (size_t)row * rowBytes, k); },
+                        [&](uint32_t k) { return ((const float *)xraw)[k]; }, X.x16, K >> 4, li, LPR, sp1, h, true);
+            const float v = group_sum<LPR>(sp1[0]);
+#pragma unroll
+            for (int q = 0; q < NPARK; ++q) res[q] = (li == st % LPR && (uint32_t)q == st / LPR) ? v : res[q];
+        }
+    } else if (nf_any_chunk(X.x16, K >> 4)) {
         // each lane redoes its own parked rows over every chunk; raw x is in LDS
         float sp[NPARK], hits = 0.0f;
 #pragma unroll

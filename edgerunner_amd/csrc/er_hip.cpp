@@ -147,9 +147,11 @@ struct I8Cfg {
 constexpr I8Cfg kI8Cfg[] = {ER_I8_CONFIGS(ER_I8_ROW)};
 #undef ER_I8_ROW
 constexpr int kI8Count = (int)(sizeof(kI8Cfg) / sizeof(kI8Cfg[0]));
-// Integer-dot kernels stage 3K + K/4 + K/16 bytes of x in LDS; rows up to this
-// length use them (the default dynamic LDS limit is 64 KiB).
+// Integer-dot kernels stage 3K + K/4 + K/8 bytes of x in LDS (limb planes,
+// chunk sums, group scales and conditioning marks, er_xlimbs.h); rows up to
+// this length use them (the default dynamic LDS limit is 64 KiB).
 constexpr uint32_t kI8MaxK = 16384;
+constexpr uint32_t xl_lds_bytes(uint32_t K) { return 3u * K + (K / 16u) * 4u + (K / 64u) * 8u; }
 
 // CU-resident Q4_K / Q8_0 / Q6_K configurations {LPR, NS, MAXJ} (er_gemv_cfg.h): kernels
 // for 1..maxJ unrolled steps, and a rolled one when maxJ == ER_CU_MAX_STEPS.
@@ -166,9 +168,9 @@ constexpr int kCuCountQ8 = (int)(sizeof(kCuCfgQ8) / sizeof(kCuCfgQ8[0]));
 constexpr int kCuCountQ6K = (int)(sizeof(kCuCfgQ6K) / sizeof(kCuCfgQ6K[0]));
 // The CU-resident family covers Q4_K rows of up to 256 slots and Q8_0 / Q6_K
 // rows of up to 64 (pick_cu finds no configuration beyond), and holds limbs plus raw x
-// in LDS: 3K + K/4 + K/16 + 4K bytes.
+// in LDS: 3K + K/4 + K/8 + 4K bytes.
 constexpr uint32_t kCuMaxK = 16384;
-constexpr uint32_t cu_lds_bytes(uint32_t K) { return 3u * K + K / 16u * 4u + K / 64u * 4u + 4u * K; }
+constexpr uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 
 // Multi-matrix / GeGLU Q4_K configurations {LPR, NS, R} (er_gemv_cfg.h).
 #define ER_I8_ROW(LPR, NS, R) {LPR, NS, R},
@@ -512,7 +514,7 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
         if (ci >= 0) {
             const I8Cfg &c = kI8Cfg[ci];
             const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
-            const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+            const uint32_t lds = xl_lds_bytes(K);
             dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, batch, 1);
             hipFunction_t fn = f == Fmt::Q4_K ? ctx->fnQ4KI8[ci]
                                               : (f == Fmt::Q8_0 ? ctx->fnQ8I8[ci] : ctx->fnQ6KI8[ci]);
@@ -661,7 +663,7 @@ er_status launch_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buf
         !aligned(out.data, 4))
         return fail(ER_ERR_INVALID_ARGUMENT,
                     "Q6_K top-1: weight and input must be 16-byte, partial and index buffers 4-byte aligned");
-    const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+    const uint32_t lds = xl_lds_bytes(K);
     // rows the integer-dot kernels do not take run the fp32 family, as the
     // plain GEMV over the same matrix does
     const bool fp32 = K > kI8MaxK || lds + 1024u > ctx->info.lds_per_workgroup || ctx->gemv_fp32 != 0;
@@ -944,7 +946,7 @@ er_status encode_q4k_multi(er_hip_ctx *ctx, er_stream stream, const er_buffer *W
         a.M[i] = i < count ? Ms[i] : 0u;
     }
     const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
-    const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+    const uint32_t lds = xl_lds_bytes(K);
     void *args[] = {&a, &x.data, &K};
     dim3 grid((uint32_t)((Mt + rowsPerBlock - 1) / rowsPerBlock), 1, 1);
     return launch_fn(ctx->fnQ4KMulti[ci], "er_gemv_q4k_multi", grid, dim3(kGemvThreads, 1, 1), lds,
@@ -972,7 +974,7 @@ er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_b
     }
     const I8Cfg &c = kI8MultiCfg[ci];
     const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * (c.r / 2u);
-    const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+    const uint32_t lds = xl_lds_bytes(K);
     void *args[] = {&Wg.data, &Wu.data, &x.data, &y.data, &M, &K};
     dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock, 1, 1);
     return launch_fn(ctx->fnQ4KGeglu[ci], "er_gemv_q4k_geglu", grid, dim3(kGemvThreads, 1, 1), lds,
@@ -1070,7 +1072,7 @@ er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &
                       stream, args);
     }
     const I8Cfg &c = kI8MultiCfg[ci];
-    const uint32_t lds = 3u * K + (K / 16u) * 4u + (K / 64u) * 4u;
+    const uint32_t lds = xl_lds_bytes(K);
     const float *normW = (const float *)f.normW.data;
     float eps = f.eps;
     if (f.silu) {

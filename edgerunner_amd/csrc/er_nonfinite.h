@@ -93,17 +93,21 @@ ER_DEV bool nf_any_value(const float *v, uint32_t K) {
 // whose sum x16[c] is non-finite when x16 is given), and counts those values
 // in hits.  A NaN value's term is NaN whatever the weight, so no weight is
 // read for it; the scan ends once every sp[r] is NaN.
+// all: every term of those chunks, finite or not (the fp32 evaluation of
+// rows whose x the limbs do not carry precisely enough, er_xlimbs.h; with
+// non-finite values present its IEEE sum is the one above, since finite
+// terms cannot cancel an infinite one).
 template <int NR, class WAt, class VAt>
 ER_DEV void nf_terms(WAt weight, VAt v, const float *x16, uint32_t C16, uint32_t c0, uint32_t cs,
-                     float (&sp)[NR], float &hits) {
+                     float (&sp)[NR], float &hits, bool all = false) {
 #pragma unroll 1
     for (uint32_t c = c0; c < C16; c += cs) {
-        if (x16 && __builtin_isfinite(x16[c])) continue;
+        if (!all && x16 && __builtin_isfinite(x16[c])) continue;
 #pragma unroll 1
         for (uint32_t i = 0; i < 16u; ++i) {
             const uint32_t k = 16u * c + i;
             const float xv = v(k);
-            if (__builtin_isfinite(xv)) continue;
+            if (!all && __builtin_isfinite(xv)) continue;
             hits += 1.0f;
 #pragma unroll
             for (int r = 0; r < NR; ++r) sp[r] += __builtin_isnan(xv) ? xv : weight(r, k) * xv;

@@ -18,11 +18,27 @@
 // the fp32 spacing is 1, so the FMA's single rounding is rint and the low 23
 // bits of the result are u; its bytes are the digits (v_perm gathers them).
 //
+// Conditioning: a group whose maximum dwarfs its other values leaves those
+// values few bits (an outlier 10^5 times its neighbours' size leaves them
+// about 5), and a row whose weight at the outlier is zero sums exactly those
+// neighbours.  Each group's rounding error has energy ~ 64 s_g^2 / 12; the
+// launch compares their total with the energy R of the values the limbs
+// carry well (per group, the squares in the lanes not holding its maximum):
+//   f * sum over groups (64 / 12) s_g^2  >  2^-24 * R
+// (f = 1 for Q8_0; 4 for Q4_K and Q6_K, whose unsigned nibbles weigh the
+// error against a smaller signed weight), i.e. when the limbs' error would
+// exceed ~2^-12 of a row built from the well-carried values, the launch
+// evaluates its rows in fp32 from the raw weights instead (the non-finite
+// path of er_nonfinite.h with every term).  A few outlier channels of 10^3
+// or 10^4 among thousands of ordinary ones stay on the integer path; many
+// groups with 10^4 outliers, or any at 10^5, do not.
+//
 // LDS layout (K a multiple of 64):
 //   [0, 3K)        planes 0..2: limb bytes l0, l1, l2; 16-byte granules swizzled by xl_gswz
 //   [3K, 3K+K/4)   x16[K/16]  fp32 sums of each 16-value chunk (exact fp32 x),
 //                  summed as (x0 + .. + x7) + (x8 + .. + x15), each half in order
 //   then           sg64[K/64] the group scales s_g
+//   then           rest64[K/64] each group's energy outside its maximum's lanes (xl_rest_energy)
 #pragma once
 
 #include "er_common.h"
@@ -36,12 +52,17 @@
 // 0-1 spreads them over all 8 four-bank groups.
 ER_DEV uint32_t xl_gswz(uint32_t G) { return G ^ ((G >> 3) & 3u); }
 
-ER_DEV uint32_t xl_lds_bytes(uint32_t K) { return ER_XL_PLANES * K + (K / 16u) * 4u + (K / 64u) * 4u; }
+ER_DEV uint32_t xl_lds_bytes(uint32_t K) { return ER_XL_PLANES * K + (K / 16u) * 4u + (K / 64u) * 8u; }
+
+// 2^-24: the launch takes the fp32 path when its limbs' error energy exceeds
+// this fraction of the energy they carry well (xl_ill)
+#define ER_XL_EPS2 5.9604645e-08f
 
 struct XLimbs {
     const uint8_t *planes;
     const float *x16;
     const float *sg64;
+    const float *rest64;
     uint32_t K;
 };
 
@@ -50,9 +71,57 @@ ER_DEV XLimbs xl_view(const uint32_t *lds, uint32_t K) {
     v.planes = (const uint8_t *)lds;
     v.x16 = (const float *)(lds + (ER_XL_PLANES * K) / 4u);
     v.sg64 = v.x16 + (K >> 4);
+    v.rest64 = v.sg64 + (K >> 6);
     v.K = K;
     return v;
 }
+
+// Wave-uniform: does the staged x call for the fp32 path (the conditioning
+// rule above; f the format's factor)?  Every wave computes it from the same
+// LDS values in the same order, so all agree.
+ER_DEV bool xl_ill(const XLimbs &X, float f) {
+    float e = 0.0f, r = 0.0f;
+#pragma unroll 1
+    for (uint32_t g = lane_id(); g < (X.K >> 6); g += 64u) {
+        const float rg = X.rest64[g], sg = X.sg64[g];
+        e = __builtin_fmaf(rg > 0.0f ? sg : 0.0f, sg, e);
+        r += rg;
+    }
+    e = group_sum<64>(e);
+    r = group_sum<64>(r);
+    return f * (64.0f / 12.0f) * e > ER_XL_EPS2 * r;
+}
+
+// The group's energy outside its maximum's lanes, from this lane's values
+// v[0..N), this lane's maximum lmx and the group maximum mx: each lane sums
+// its squares (one FMA per value), the lane(s) holding mx contribute nothing,
+// and the group sums over its lanes with the DPP steps `reduce` applies, so
+// 48 (or 56) of the 63 other values count.  Leaving a whole lane out, rather
+// than subtracting max^2 from a sum holding it, keeps the value free of
+// cancellation (the square of the maximum has an ulp far above it).  0 for
+// an all-zero or non-finite group; squares past ~1.8e19 overflow to infinity,
+// which keeps the launch on the integer path (its error is then negligible).
+template <int N, class Reduce>
+ER_DEV float xl_rest_energy(const float (&v)[N], float lmx, float mx, Reduce reduce) {
+    float s2 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < N; ++q) s2 = __builtin_fmaf(v[q], v[q], s2);
+    const float rest = reduce(lmx == mx ? 0.0f : s2);
+    return mx > 0.0f && mx < __builtin_inff() ? rest : 0.0f;
+}
+
+// Sums over the 4 lanes (16-value chunks) or 8 lanes (8-value halves) that
+// hold one 64-group.
+ER_DEV float xl_group_sum4(float r) {
+    r = dpp_add<ER_DPP_QUAD_XOR1>(r);
+    return dpp_add<ER_DPP_QUAD_XOR2>(r);
+}
+ER_DEV float xl_group_sum8(float r) {
+    r = dpp_add<ER_DPP_QUAD_XOR1>(r);
+    r = dpp_add<ER_DPP_QUAD_XOR2>(r);
+    return dpp_add<ER_DPP_ROW_HALF_MIRROR>(r);  // quads 2k and 2k+1 of each 8 lanes
+}
+
 
 // Loads of chunk c (16 values) of x for thread `tid`; XG chunks per thread.
 // Out-of-range chunks reload the last chunk (always in bounds, never stored).
@@ -108,10 +177,12 @@ ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uin
         sb += v[q];
     }
     const float sm = sa + sb;
+    const float lmx = mx;
     mx = dpp_max<ER_DPP_QUAD_XOR1>(mx);
     mx = dpp_max<ER_DPP_QUAD_XOR2>(mx);
     float sg, inv;
     xl_scale(mx, &sg, &inv);
+    const float rest = xl_rest_energy(v, lmx, mx, xl_group_sum4);
     // digits of u = xi + C are bytes 0..2 of fma(v, 1/s_g, 2^23 + C)
     uint32_t u[16];
 #pragma unroll
@@ -145,7 +216,10 @@ ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uin
             *(u32x4 *)__builtin_assume_aligned(planes + (size_t)l * K + 16u * G, 16) =
                 u32x4{lb[l][0], lb[l][1], lb[l][2], lb[l][3]};
         x16[tRaw] = sm;
-        if ((tRaw & 3u) == 0) sg64[tRaw >> 2] = sg;
+        if ((tRaw & 3u) == 0) {
+            sg64[tRaw >> 2] = sg;
+            sg64[C16 / 4u + (tRaw >> 2)] = rest;
+        }
     }
 }
 
@@ -164,11 +238,13 @@ ER_DEV void xl_store_half(uint32_t *lds, uint32_t K, const float4 (&xr)[2], uint
         sh += v[q];
     }
     const float sm = dpp_add<ER_DPP_QUAD_XOR1>(sh);  // even lane: own half + the odd lane's
+    const float lmx = mx;
     mx = dpp_max<ER_DPP_QUAD_XOR1>(mx);
     mx = dpp_max<ER_DPP_QUAD_XOR2>(mx);
     mx = dpp_max<ER_DPP_ROW_HALF_MIRROR>(mx);  // quads 2k and 2k+1 of each 8 lanes
     float sg, inv;
     xl_scale(mx, &sg, &inv);
+    const float rest = xl_rest_energy(v, lmx, mx, xl_group_sum8);
     uint32_t u[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) u[q] = __float_as_uint(__builtin_fmaf(v[q], inv, ER_XL_MAGIC));
@@ -196,7 +272,10 @@ ER_DEV void xl_store_half(uint32_t *lds, uint32_t K, const float4 (&xr)[2], uint
         for (int l = 0; l < ER_XL_PLANES; ++l)
             *(u32x2 *)__builtin_assume_aligned(planes + (size_t)l * K + off, 8) = u32x2{lb[l][0], lb[l][1]};
         if ((hRaw & 1u) == 0) x16[hRaw >> 1] = sm;
-        if ((hRaw & 7u) == 0) sg64[hRaw >> 3] = sg;
+        if ((hRaw & 7u) == 0) {
+            sg64[hRaw >> 3] = sg;
+            sg64[(K >> 6) + (hRaw >> 3)] = rest;
+        }
     }
 }
 
