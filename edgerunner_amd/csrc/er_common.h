@@ -114,6 +114,15 @@ template <int CTRL>
 ER_DEV float dpp_max(float v) {
     return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false)));
 }
+// dpp_max for v >= 0 that is never NaN (a maximum of magnitudes formed with
+// fmaxf): such floats order as their bit patterns, so an unsigned maximum
+// gives fmaxf's result in one DPP instruction (no NaN canonicalisation).
+template <int CTRL>
+ER_DEV float dpp_max_nonneg(float v) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)b, CTRL, 0xf, 0xf, false);
+    return __uint_as_float(b > o ? b : o);
+}
 
 // Sum over the lanes of an aligned group of W lanes (W in {1, 2, 4, 8, 16,
 // 32, 64}); every lane of the group gets the sum.  Within a 16-lane row the

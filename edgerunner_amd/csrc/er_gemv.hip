@@ -963,6 +963,9 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // kernel with the same LPR and NS.
 
 #define ER_CU_SPIN_LIMIT (1u << 22)   // bound on the staging-counter wait (s_sleep 1 per poll)
+#ifndef ER_CUK_X16
+#define ER_CUK_X16 1  // gemv_cuk converts x 16 values per lane per pass (0: 8)
+#endif
 // units of weight loads in flight per wave in the unrolled kernels: the
 // format's choice (F::UNITS: 3 for Q4_K slots of 48 bytes, which beat 2 and 4
 // and the former 2 whole rows; 2 for Q8_0 slots of 68), except 2 for 7-slot
@@ -1353,6 +1356,127 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
             const uint32_t row = rowOf(st);
             if (st < J && row < M) y[row] = res[q];
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Long rows (128 < K / 64 <= 256 slots): the workgroup's waves split K.
+//
+// With whole rows per lane group (gemv_cu), every row reads all of x's limbs
+// back from LDS (3 bytes per weight: 688 KB per CU at 4096 x 14336, as much
+// LDS time as the dot products take), and no wave starts before the whole of
+// x is converted.  Here wave w owns the slots [spw w, spw (w + 1)) of every
+// row of its workgroup, spw = 4 ceil(S / 32) <= 32 (whole 256-weight blocks,
+// so a Q6_K slot's x groups are the wave's own).  It loads and converts only
+// that slice of x, keeps each lane's slot of limbs in registers, and walks
+// the workgroup's rows two at a time: lane 32 g + li takes row parity g and
+// slot spw w + li (lanes past the slice reuse the slice's last slot with
+// weight 0).  Row step j of parity g is row (j * gridDim.x + blockIdx.x) * 2
+// + g; a step's slot dots are summed over the 32 lanes (group_sum) and parked
+// in lane j.  At the end the 8 wave partials of each row meet in LDS and are
+// added in wave order, so a row's value depends on K alone, not on the row
+// partition or the batch.  J row steps per lane group, F::UNITS in flight.
+template <class F, int J>
+ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
+                     uint32_t M, uint32_t K) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    __shared__ float part[ER_CU_WAVES][2 * J];  // [wave][local row 2 j + g]
+    static_assert(J >= 1 && J <= ER_CUK_MAX_STEPS, "row sums parked one per lane of a 32-lane group");
+    constexpr int D = F::UNITS < J ? F::UNITS : J;
+    // x passes per wave: 16-value chunks (4 spw <= 128, 64 per pass) or
+    // 8-value half-chunks (8 spw <= 256)
+    constexpr int VPL = (ER_CUK_X16 && J > 0) ? 16 : 8;  // values per lane per pass
+    constexpr int NPASS = VPL == 16 ? 2 : 4;
+    x += (size_t)blockIdx.y * K;
+    y += (size_t)blockIdx.y * M;
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t g = lane >> 5, li = lane & 31u;
+    const uint32_t S = K >> 6;
+    const uint32_t spw = 4u * ((S + 31u) >> 5);
+    const uint32_t s0 = wave * spw, s1 = min(s0 + spw, S);  // empty (s0 >= S) only for short rows
+    auto rowAt = [&](uint32_t j, uint32_t gg) { return (j * gridDim.x + blockIdx.x) * 2u + gg; };
+    const size_t rowBytes = F::row_bytes(K);
+    float res = 0.0f;
+    if (s0 < S) {
+        const uint32_t s = s0 + li;
+        const uint32_t sc = min(s, s1 - 1u);
+        const float live = s < s1 ? 1.0f : 0.0f;
+        // x slice: pieces [n s0, n s1) of VPL values (n = 64 / VPL), lanes
+        // nk..nk+n-1 one 64-group; loads clamped into the slice, issued before
+        // the weights
+        constexpr uint32_t PPG = 64u / VPL;  // pieces per 64-group
+        const uint32_t h0 = PPG * s0, h1 = PPG * s1;
+        float4 xr[NPASS][VPL / 4];
+#pragma unroll
+        for (int p = 0; p < NPASS; ++p) {
+            const uint32_t hc = min(h0 + 64u * p + lane, h1 - 1u);
+#pragma unroll
+            for (int q = 0; q < VPL / 4; ++q) xr[p][q] = *(const float4 *)(x + VPL * hc + 4u * q);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        typename F::Wt wb[D];
+        auto issue = [&](uint32_t j, int b) {
+            const uint32_t row = min(rowAt(j, g), M - 1u);
+            wb[b] = F::load(W + (size_t)row * rowBytes, sc);
+        };
+#pragma unroll
+        for (int v = 0; v < D; ++v) {
+            issue((uint32_t)v, v);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // convert the slice (pieces past it are not stored: index K / VPL).
+        // Every pass runs: a pass under a branch had its x loads sunk behind
+        // the weight loads, and the conversion then waited for those too.
+#pragma unroll
+        for (int p = 0; p < NPASS; ++p) {
+            const uint32_t hc = h0 + 64u * p + lane;
+            if constexpr (VPL == 16)
+                xl_store_chunk(lds, K, xr[p], hc < h1 ? hc : K >> 4);
+            else
+                xl_store_half(lds, K, xr[p], hc < h1 ? hc : K >> 3);
+        }
+        // the wave reads back only what it stored; its LDS accesses run in order
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+        const XLimbs X = xl_view(lds, K);
+        const uint32_t M0F = vreg_const(0x0f0f0f0fu);
+        const typename F::Xs xs = F::xside(X, sc, live);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            float acc = F::dot(wb[j % D], xs, 0.0f, M0F);
+            __builtin_amdgcn_sched_barrier(0);
+            if (j + D < J) issue((uint32_t)(j + D), j % D);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = group_sum<32>(acc);
+            res = li == (uint32_t)j ? acc : res;
+        }
+    }
+    if (li < (uint32_t)J) part[wave][2u * li + g] = res;
+    __syncthreads();  // every wave's partials, limbs, chunk sums and scales are in LDS
+    const XLimbs X = xl_view(lds, K);
+    const bool ill = xl_ill(X, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f);
+    const bool nf = !ill && nf_any_chunk(X.x16, K >> 4);
+    // lane group (wave, g) finishes steps wave, wave + 8, ..., parity g
+#pragma unroll 1
+    for (uint32_t st = wave; st < (uint32_t)J; st += ER_CU_WAVES) {
+        const uint32_t lr = 2u * st + g;
+        const uint32_t row = rowAt(st, g);
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < ER_CU_WAVES; ++w) v += part[w][lr];
+        if (ill || nf) {
+            // fp32 from the raw weights (every term, or the non-finite ones),
+            // the group's lanes splitting the 16-value chunks
+            const uint32_t rc = min(row, M - 1u);
+            float sp1[1] = {0.0f}, h = 0.0f;
+            nf_terms<1>([&](int, uint32_t k) { return weight_at<F::FMT>(W + (size_t)rc * rowBytes, k); },
+                        [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, li, 32u, sp1, h, ill);
+            const float fv = group_sum<32>(sp1[0]);
+            h = group_sum<32>(h);
+            v = (ill || h > 0.0f) ? fv : v;
+        }
+        if (li == 0 && row < M) y[row] = v;
     }
 }
 
@@ -1930,6 +2054,22 @@ ER_I8_CONFIGS(ER_I8_ENTRY)
 ER_CU_CONFIGS_Q4K(ER_CU_ENTRY_Q4K)
 ER_CU_CONFIGS_Q8(ER_CU_ENTRY_Q8)
 ER_CU_CONFIGS_Q6K(ER_CU_ENTRY_Q6K)
+
+// K-sliced CU-resident kernels: er_gemv_<fmt>_cuk_j<J>, J = 1..ER_CUK_MAX_STEPS row
+// steps of 2 rows per workgroup, grid (ceil(M / 2J), batch), dynamic LDS xl_lds_bytes(K).
+#define ER_CUK_ENTRY(fmt, F, J)                                                                     \
+    extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                                 \
+        er_gemv_##fmt##_cuk_j##J(const uint8_t *__restrict__ W, const float *__restrict__ x,         \
+                                 float *__restrict__ y, uint32_t M, uint32_t K) {                   \
+        gemv_cuk<F, J>(W, x, y, M, K);                                                              \
+    }
+#define ER_CUK_ENTRIES(fmt, F)                                                                        \
+    ER_CUK_ENTRY(fmt, F, 1) ER_CUK_ENTRY(fmt, F, 2) ER_CUK_ENTRY(fmt, F, 3) ER_CUK_ENTRY(fmt, F, 4)   \
+    ER_CUK_ENTRY(fmt, F, 5) ER_CUK_ENTRY(fmt, F, 6) ER_CUK_ENTRY(fmt, F, 7) ER_CUK_ENTRY(fmt, F, 8)   \
+    ER_CUK_ENTRY(fmt, F, 9) ER_CUK_ENTRY(fmt, F, 10) ER_CUK_ENTRY(fmt, F, 11) ER_CUK_ENTRY(fmt, F, 12) \
+    ER_CUK_ENTRY(fmt, F, 13) ER_CUK_ENTRY(fmt, F, 14) ER_CUK_ENTRY(fmt, F, 15) ER_CUK_ENTRY(fmt, F, 16)
+ER_CUK_ENTRIES(q4k, CuQ4K)
+ER_CUK_ENTRIES(q8_0, CuQ8)
 
 // Multi-matrix and GeGLU Q4_K kernels: R counts row computations per lane
 // group (GeGLU: R/2 gate rows + the matching up rows).

@@ -42,3 +42,7 @@
     X(16, 1, 8) X(16, 2, 8) X(32, 1, 8) X(32, 2, 8) X(64, 1, 8) X(64, 2, 8) X(64, 3, 2) X(64, 4, 2) X(32, 7, 1)
 #define ER_CU_CONFIGS_Q8(X) X(16, 1, 8) X(32, 1, 8) X(64, 1, 8)
 #define ER_CU_CONFIGS_Q6K(X) X(16, 1, 8) X(32, 1, 8) X(64, 1, 8)
+
+// K-sliced CU-resident Q4_K / Q8_0 kernels for 8192 < K <= 16384 (gemv_cuk):
+// one kernel per row-step count 1..ER_CUK_MAX_STEPS (2 rows per step).
+#define ER_CUK_MAX_STEPS 16

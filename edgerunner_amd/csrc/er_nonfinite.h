@@ -68,10 +68,24 @@ ER_DEV float weight_at(const uint8_t *row, uint32_t k) {
 }
 
 // Wave-uniform: does any of the C16 chunk sums hold a non-finite value?
+// x16 is 16-byte aligned and C16 % 4 == 0 (K % 64 == 0): each lane reads
+// four 16-byte pieces per 1024 chunks, all issued before one wait (a scan of
+// one value per read waited ~100 cycles per 64 chunks at the end of every
+// launch).
 ER_DEV bool nf_any_chunk(const float *x16, uint32_t C16) {
+    const float4 *v = (const float4 *)__builtin_assume_aligned(x16, 16);
+    const uint32_t n4 = C16 >> 2, ln = lane_id();
     bool f = false;
 #pragma unroll 1
-    for (uint32_t c = lane_id(); c < C16; c += 64u) f |= !__builtin_isfinite(x16[c]);
+    for (uint32_t b = 0; b < n4; b += 256u) {
+        float4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) q[u] = v[min(b + 64u * u + ln, n4 - 1u)];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            f |= !(__builtin_isfinite(q[u].x) && __builtin_isfinite(q[u].y) && __builtin_isfinite(q[u].z) &&
+                   __builtin_isfinite(q[u].w));
+    }
     return __builtin_amdgcn_ballot_w64(f) != 0;
 }
 

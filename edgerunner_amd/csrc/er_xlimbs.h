@@ -79,13 +79,27 @@ ER_DEV XLimbs xl_view(const uint32_t *lds, uint32_t K) {
 // Wave-uniform: does the staged x call for the fp32 path (the conditioning
 // rule above; f the format's factor)?  Every wave computes it from the same
 // LDS values in the same order, so all agree.
+// Each lane sums groups lane, lane + 64, ... in that order; the reads of four
+// of them are issued before one wait (the clamped reads past the last group
+// add exact zeros).
 ER_DEV bool xl_ill(const XLimbs &X, float f) {
     float e = 0.0f, r = 0.0f;
+    const uint32_t S = X.K >> 6, ln = lane_id();
 #pragma unroll 1
-    for (uint32_t g = lane_id(); g < (X.K >> 6); g += 64u) {
-        const float rg = X.rest64[g], sg = X.sg64[g];
-        e = __builtin_fmaf(rg > 0.0f ? sg : 0.0f, sg, e);
-        r += rg;
+    for (uint32_t b = 0; b < S; b += 256u) {
+        float rg[4], sg[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t gi = min(b + 64u * u + ln, S - 1u);
+            rg[u] = X.rest64[gi];
+            sg[u] = X.sg64[gi];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const bool in = b + 64u * u + ln < S;
+            e = __builtin_fmaf(in && rg[u] > 0.0f ? sg[u] : 0.0f, sg[u], e);
+            r += in ? rg[u] : 0.0f;
+        }
     }
     e = group_sum<64>(e);
     r = group_sum<64>(r);
@@ -178,8 +192,8 @@ ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uin
     }
     const float sm = sa + sb;
     const float lmx = mx;
-    mx = dpp_max<ER_DPP_QUAD_XOR1>(mx);
-    mx = dpp_max<ER_DPP_QUAD_XOR2>(mx);
+    mx = dpp_max_nonneg<ER_DPP_QUAD_XOR1>(mx);
+    mx = dpp_max_nonneg<ER_DPP_QUAD_XOR2>(mx);
     float sg, inv;
     xl_scale(mx, &sg, &inv);
     const float rest = xl_rest_energy(v, lmx, mx, xl_group_sum4);
@@ -239,9 +253,9 @@ ER_DEV void xl_store_half(uint32_t *lds, uint32_t K, const float4 (&xr)[2], uint
     }
     const float sm = dpp_add<ER_DPP_QUAD_XOR1>(sh);  // even lane: own half + the odd lane's
     const float lmx = mx;
-    mx = dpp_max<ER_DPP_QUAD_XOR1>(mx);
-    mx = dpp_max<ER_DPP_QUAD_XOR2>(mx);
-    mx = dpp_max<ER_DPP_ROW_HALF_MIRROR>(mx);  // quads 2k and 2k+1 of each 8 lanes
+    mx = dpp_max_nonneg<ER_DPP_QUAD_XOR1>(mx);
+    mx = dpp_max_nonneg<ER_DPP_QUAD_XOR2>(mx);
+    mx = dpp_max_nonneg<ER_DPP_ROW_HALF_MIRROR>(mx);  // quads 2k and 2k+1 of each 8 lanes
     float sg, inv;
     xl_scale(mx, &sg, &inv);
     const float rest = xl_rest_energy(v, lmx, mx, xl_group_sum8);

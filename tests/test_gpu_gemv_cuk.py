@@ -1,0 +1,161 @@
+"""K-sliced CU-resident GEMV kernels (Q4_K and Q8_0 rows of 8192 < K <= 16384
+weights, the Llama FFN down projection 4096 x 14336 among them): each wave of
+a workgroup owns a slice of K, so a row's value is the sum of 8 wave partials.
+Against the CPU oracle at the GEMV parity bar (relative L2 <= 1e-3) on 61
+rows spread over each matrix, and every row against the whole-row kernels
+(ER_HIP_GEMV_CUK=0) at 1e-5; every unrolled step count 1..16; slices that end
+mid-wave and a wave with no slice (K = 8448: 20 slots per wave, 132 slots);
+exact one-hot columns at the slice boundaries; the same row bit for bit
+whatever the row partition or the batch; non-finite and heavy-tailed x."""
+import os
+
+import numpy as np
+import pytest
+
+import edgerunner_amd.synth as synth
+from edgerunner_amd import Context, GEMVKernel
+from oracle import ref
+from oracle import restate_np as rn
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+DSCALE = {"q8_0": {"dscale": 0.02}, "q4_k": {"dscale": 0.01, "dminscale": 0.01}}
+EXEC = {"q8_0": "executeQ8_0Weights", "q4_k": "executeQ4KWeights"}
+EXEC_B = {"q8_0": "executeBatchedQ8_0Weights", "q4_k": "executeBatchedQ4KWeights"}
+FMTS = ["q4_k", "q8_0"]
+
+
+def _ctx(**env):
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return Context(int(os.environ.get("ER_DEVICE", "0")))
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.fixture(scope="module")
+def whole_rows():
+    c = _ctx(ER_HIP_GEMV_CUK="0")
+    yield GEMVKernel(c)
+    c.close()
+
+
+def sample_rows(M):
+    return np.unique(np.linspace(0, M - 1, 61).astype(np.int64))
+
+
+def oracle_rows(fmt, W, x, M, K, rows):
+    Wr = W.reshape(M, -1)[rows].reshape(-1)
+    return ref.gemv(fmt, Wr, x, len(rows), K)
+
+
+# K: 132 slots (20 per wave, the last wave empty), 172 (24 per wave, 4 in the
+# last), 192, 224 (28 per wave, half of the last conversion pass), 256
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("K", [8448, 11008, 12288, 14336, 16384])
+def test_every_step_count(gemv, whole_rows, fmt, K):
+    cus = gemv.ctx.compute_units
+    x = synth.normal_f32(synth.seed(110, K % 97), K)
+    for j in range(1, 17):
+        M = cus * 2 * j
+        W = synth.weights(fmt, synth.seed(110, 10 * j + K % 7), M, K, **DSCALE[fmt])
+        y = getattr(gemv, EXEC[fmt])(W, x, M, K)
+        assert np.all(np.isfinite(y)), (fmt, K, j)
+        rows = sample_rows(M)
+        assert rel_l2(y[rows], oracle_rows(fmt, W, x, M, K, rows)) < TOL, (fmt, K, j)
+        other = getattr(whole_rows, EXEC[fmt])(W, x, M, K)
+        assert rel_l2(y, other) < 1e-5, (fmt, K, j, rel_l2(y, other))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,K", [(1, 14336), (37, 12288), (4095, 14336), (14336, 14336), (5000, 16384),
+                                 (5120, 13824)])
+def test_partial_and_many_workgroups(gemv, fmt, M, K):
+    """A single row, a partial last workgroup, 10 row steps (5000 / 5120
+    rows), and more workgroups than CUs (14336 rows: 448 workgroups of 32)."""
+    W = synth.weights(fmt, synth.seed(111, M % 89), M, K, **DSCALE[fmt])
+    x = synth.normal_f32(synth.seed(111, 1), K)
+    y = getattr(gemv, EXEC[fmt])(W, x, M, K)
+    rows = sample_rows(M)
+    assert rel_l2(y[rows], oracle_rows(fmt, W, x, M, K, rows)) < TOL
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_one_hot_columns_at_slice_edges(gemv, fmt):
+    """K = 14336: 28 slots (1792 weights) per wave.  A one-hot x reads one
+    weight column exactly, at each end of a wave's slice and mid-slice."""
+    M, K = 600, 14336
+    W = synth.weights(fmt, synth.seed(112, 0), M, K, **DSCALE[fmt])
+    cols = rn.weights_f32(fmt, W, M, K)
+    for j in (0, 63, 64, 1791, 1792, 1793, 5 * 1792 + 700, 7 * 1792, K - 1):
+        x = np.zeros(K, np.float32)
+        x[j] = 1.0
+        y = getattr(gemv, EXEC[fmt])(W, x, M, K)
+        assert np.array_equal(y, cols[:, j]), j
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_row_value_independent_of_partition(gemv, fmt):
+    """A row's sum is the same bits whether its workgroup holds 2 rows
+    (M = 512: one step) or 16 (M = 4096: eight steps), and batched calls
+    equal per-token ones."""
+    K = 14336
+    W = synth.weights(fmt, synth.seed(113, 0), 4096, K, **DSCALE[fmt])
+    x = synth.normal_f32(synth.seed(113, 1), 3 * K)
+    full = getattr(gemv, EXEC[fmt])(W, x[:K], 4096, K)
+    head = getattr(gemv, EXEC[fmt])(W.reshape(4096, -1)[:512].reshape(-1), x[:K], 512, K)
+    assert np.array_equal(full[:512].view(np.uint32), head.view(np.uint32))
+    yb = getattr(gemv, EXEC_B[fmt])(W, x, 3, 4096, K).reshape(3, 4096)
+    for t in range(3):
+        single = getattr(gemv, EXEC[fmt])(W, x[t * K:(t + 1) * K], 4096, K)
+        assert np.array_equal(yb[t].view(np.uint32), single.view(np.uint32)), t
+
+
+def _poison(x, kind):
+    x = x.copy()
+    K = x.size
+    if kind == "nan":
+        x[K // 3] = np.nan
+    elif kind == "pinf":
+        x[5000] = np.inf
+    elif kind == "pm_inf":
+        x[100] = np.inf
+        x[K - 7] = -np.inf
+    elif kind == "inf_group":
+        x[1792 * 3:1792 * 3 + 64] = np.inf
+    return x
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("kind", ["nan", "pinf", "pm_inf", "inf_group"])
+def test_nonfinite(gemv, fmt, kind):
+    M, K = 512, 14336
+    W = synth.weights(fmt, synth.seed(114, 0), M, K, **DSCALE[fmt])
+    x = _poison(synth.normal_f32(synth.seed(114, 1), K), kind)
+    y = getattr(gemv, EXEC[fmt])(W, x, M, K)
+    exp = ref.gemv(fmt, W, x, M, K, threads=ref.max_threads())
+    assert np.array_equal(np.isnan(y), np.isnan(exp)), kind
+    inf = np.isinf(exp)
+    assert np.array_equal(y[inf], exp[inf]), kind
+    fin = np.isfinite(exp)
+    assert np.all(np.isfinite(y[fin])) and (not fin.any() or rel_l2(y[fin], exp[fin]) < TOL), kind
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("amp", [1e3, 1e4, 1e5])
+def test_heavy_tailed_x(gemv, fmt, amp):
+    """N(0, 1) activations with one channel at amp in six 64-groups spread
+    over the wave slices, and every even row's weight zero at those channels
+    (those rows sum only the ordinary values)."""
+    from test_gpu_heavy_tail import heavy_case, check
+    M, K = 1024, 14336
+    W, x = heavy_case(fmt, M, K, amp, 3)
+    y = getattr(gemv, EXEC[fmt])(W, x, M, K)
+    check(y, ref.gemv(fmt, W, x, M, K, threads=ref.max_threads()))
