@@ -95,6 +95,19 @@ ER_DEV u32x2 ld8_u2(const uint8_t *p) { return *(const u32x2_a2 *)p; }
 // 4 bytes at a 2-byte-aligned address (two 16-bit loads, never over-reads).
 ER_DEV uint32_t ld4_a2(const uint8_t *p) { return ld2(p) | (ld2(p + 2) << 16); }
 
+// a . b (4 int8 products) + 0 in one VOP3P v_dot4_i32_i8.  The compiler
+// forms every sdot4 as v_dot4c_i32_i8, which accumulates into its destination,
+// so each chain started from 0 cost a v_mov of 0 (6 to 12 per slot dot).
+ER_DEV int sdot4_0(int a, int b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+// sdot4 accumulating into c, or starting a chain (first: c is not read)
+ER_DEV int sdot4_acc(int a, int b, int c, bool first) {
+    return first ? sdot4_0(a, b) : __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
 // DPP lane moves (GFX9 encodings): quad permutations, row (16-lane) mirrors
 // and the row broadcasts of lane 15 / lane 31 into the next rows.
 #define ER_DPP_QUAD_XOR1 0xb1   // quad_perm [1,0,3,2]

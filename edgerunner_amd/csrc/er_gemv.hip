@@ -93,8 +93,8 @@ ER_DEV float q4k_slot_dot(const u32x4 &h, const u32x4 &qa, const u32x4 &qb,
         const int hi = (int)((qw[k] >> 4) & M0F);
 #pragma unroll
         for (int l = 0; l < ER_XL_PLANES; ++l) {
-            cL[l] = __builtin_amdgcn_sdot4(lo, (int)xv[l][k >> 2][k & 3], cL[l], false);
-            cH[l] = __builtin_amdgcn_sdot4(hi, (int)xv[l][2 + (k >> 2)][k & 3], cH[l], false);
+            cL[l] = sdot4_acc(lo, (int)xv[l][k >> 2][k & 3], cL[l], k == 0);
+            cH[l] = sdot4_acc(hi, (int)xv[l][2 + (k >> 2)][k & 3], cH[l], k == 0);
         }
     }
     const float T0 = xl_combine(cL[0], cL[1], cL[2]);
@@ -342,6 +342,9 @@ ER_DEV Q8Slot q8_slot_load(const uint8_t *p) {
 }
 
 // acc + sg * (dA * (qA . x) + dB * (qB . x)) over the slot's 64 weights.
+// Z0: start the limb chains with sdot4_0 (off where the VOP3P form's
+// registers tipped kernels holding 8 slots of weights into spilling).
+template <bool Z0 = true>
 ER_DEV float q8_slot_dot(const Q8Slot &w, const u32x4 (&xv)[ER_XL_PLANES][4], float sg, float acc) {
     const uint32_t v[17] = {w.v0.x, w.v0.y, w.v0.z, w.v0.w, w.v1.x, w.v1.y, w.v1.z, w.v1.w, w.v2.x,
                             w.v2.y, w.v2.z, w.v2.w, w.v3.x, w.v3.y, w.v3.z, w.v3.w, w.v4};
@@ -352,8 +355,8 @@ ER_DEV float q8_slot_dot(const Q8Slot &w, const u32x4 (&xv)[ER_XL_PLANES][4], fl
         const int qb = (int)v[9 + k];
 #pragma unroll
         for (int l = 0; l < ER_XL_PLANES; ++l) {
-            cA[l] = __builtin_amdgcn_sdot4(qa, (int)xv[l][k >> 2][k & 3], cA[l], false);
-            cB[l] = __builtin_amdgcn_sdot4(qb, (int)xv[l][2 + (k >> 2)][k & 3], cB[l], false);
+            cA[l] = sdot4_acc(qa, (int)xv[l][k >> 2][k & 3], cA[l], Z0 && k == 0);
+            cB[l] = sdot4_acc(qb, (int)xv[l][2 + (k >> 2)][k & 3], cB[l], Z0 && k == 0);
         }
     }
     const float TA = xl_combine(cA[0], cA[1], cA[2]);
@@ -407,7 +410,7 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
         xl_read_group(X, s, xv);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            acc[r] = q8_slot_dot(w[j][r], xv, sg, acc[r]);
+            acc[r] = q8_slot_dot<(NS * R < 8)>(w[j][r], xv, sg, acc[r]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -524,7 +527,7 @@ ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const
         xl_read_group(X, s, xv);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            acc[r] = q8_slot_dot(w[j][r], xv, sg, acc[r]);
+            acc[r] = q8_slot_dot<(NS * R < 8)>(w[j][r], xv, sg, acc[r]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -882,7 +885,7 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
                 for (int m = 0; m < 4; ++m)
 #pragma unroll
                     for (int l = 0; l < ER_XL_PLANES; ++l)
-                        cq[m][l] = __builtin_amdgcn_sdot4((int)q[m], (int)xv[l][m][k], cq[m][l], false);
+                        cq[m][l] = sdot4_acc((int)q[m], (int)xv[l][m][k], cq[m][l], k == 0);
             }
             // scales: m = 0, 1 in dword x (bytes c, 2 + c), m = 2, 3 in dword y
             const float s0 = (float)(int8_t)(fs[j][r].x >> (8u * c));
@@ -1094,7 +1097,7 @@ struct CuQ6K {
             for (int m = 0; m < 4; ++m)
 #pragma unroll
                 for (int l = 0; l < ER_XL_PLANES; ++l)
-                    cq[m][l] = __builtin_amdgcn_sdot4((int)q[m], (int)xs.xv[l][m][k], cq[m][l], false);
+                    cq[m][l] = sdot4_acc((int)q[m], (int)xs.xv[l][m][k], cq[m][l], k == 0);
         }
         // scales: m = 0, 1 in dword x (bytes c, 2 + c), m = 2, 3 in dword y
         const float s0 = (float)(int8_t)(w.s.x >> (8u * xs.c));
@@ -1444,7 +1447,7 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            float acc = F::dot(wb[j % D], xs, 0.0f, M0F);
+            float acc = F::dot(wb[j % D], xs, -0.0f, M0F);  // -0 + v == v: the add folds away
             __builtin_amdgcn_sched_barrier(0);
             if (j + D < J) issue((uint32_t)(j + D), j % D);
             __builtin_amdgcn_sched_barrier(0);
