@@ -966,9 +966,6 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // kernel with the same LPR and NS.
 
 #define ER_CU_SPIN_LIMIT (1u << 22)   // bound on the staging-counter wait (s_sleep 1 per poll)
-#ifndef ER_CUK_X16
-#define ER_CUK_X16 1  // gemv_cuk converts x 16 values per lane per pass (0: 8)
-#endif
 // units of weight loads in flight per wave in the unrolled kernels: the
 // format's choice (F::UNITS: 3 for Q4_K slots of 48 bytes, which beat 2 and 4
 // and the former 2 whole rows; 2 for Q8_0 slots of 68), except 2 for 7-slot
@@ -1363,41 +1360,45 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
 }
 
 // ---------------------------------------------------------------------------
-// Long rows (128 < K / 64 <= 256 slots): the workgroup's waves split K.
+// K-sliced CU-resident kernels: the workgroup's waves split K.
 //
 // With whole rows per lane group (gemv_cu), every row reads all of x's limbs
 // back from LDS (3 bytes per weight: 688 KB per CU at 4096 x 14336, as much
 // LDS time as the dot products take), and no wave starts before the whole of
 // x is converted.  Here wave w owns the slots [spw w, spw (w + 1)) of every
-// row of its workgroup, spw = 4 ceil(S / 32) <= 32 (whole 256-weight blocks,
-// so a Q6_K slot's x groups are the wave's own).  It loads and converts only
-// that slice of x, keeps each lane's slot of limbs in registers, and walks
-// the workgroup's rows two at a time: lane 32 g + li takes row parity g and
-// slot spw w + li (lanes past the slice reuse the slice's last slot with
-// weight 0).  Row step j of parity g is row (j * gridDim.x + blockIdx.x) * 2
-// + g; a step's slot dots are summed over the 32 lanes (group_sum) and parked
-// in lane j.  At the end the 8 wave partials of each row meet in LDS and are
-// added in wave order, so a row's value depends on K alone, not on the row
-// partition or the batch.  J row steps per lane group, F::UNITS in flight.
-template <class F, int J>
+// row of its workgroup, spw = ceil(S / 8) <= LPR = 64 / PAR (Q4_K and Q8_0
+// slots are single 64-groups, so a slot's x is the wave's own).  It loads and
+// converts only that slice of x, keeps each lane's slot of limbs in
+// registers, and walks the workgroup's rows PAR at a time: lane LPR g + li
+// takes row g of the step and slot spw w + li (lanes past the slice reuse its
+// last slot with weight 0).  Row step j, row g is row (j * gridDim.x +
+// blockIdx.x) * PAR + g; a step's slot dots are summed over the LPR lanes
+// (group_sum) and parked in lane j.  At the end the 8 wave partials of each
+// row meet in LDS and are added in wave order, so a row's value depends on K
+// alone, not on the row partition or the batch.  J row steps per lane group,
+// F::UNITS in flight.
+template <class F, int PAR, int J>
 ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
                      uint32_t M, uint32_t K) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-    __shared__ float part[ER_CU_WAVES][2 * J];  // [wave][local row 2 j + g]
-    static_assert(J >= 1 && J <= ER_CUK_MAX_STEPS, "row sums parked one per lane of a 32-lane group");
+    constexpr uint32_t LPR = 64u / PAR;  // lanes per row slice
+    __shared__ float part[ER_CU_WAVES][PAR * J];  // [wave][local row PAR j + g]
+    static_assert(PAR == 2 || PAR == 4 || PAR == 8, "2, 4 or 8 rows per step");
+    static_assert(F::FMT != ER_FMT_Q6_K, "a Q6_K slot spans two x groups");
+    static_assert(J >= 1 && J <= (int)LPR && J <= ER_CUK_MAX_STEPS, "row sums parked one per lane of a slice");
     constexpr int D = F::UNITS < J ? F::UNITS : J;
-    // x passes per wave: 16-value chunks (4 spw <= 128, 64 per pass) or
-    // 8-value half-chunks (8 spw <= 256)
-    constexpr int VPL = (ER_CUK_X16 && J > 0) ? 16 : 8;  // values per lane per pass
-    constexpr int NPASS = VPL == 16 ? 2 : 4;
+    // x pieces per wave: 16-value chunks (4 spw <= 4 LPR, 64 per pass), or for
+    // 8-lane slices 8-value halves (8 spw <= 64: one pass)
+    constexpr int VPL = PAR == 8 ? 8 : 16;  // values per lane per pass
+    constexpr int NPASS = PAR == 2 ? 2 : 1;
     x += (size_t)blockIdx.y * K;
     y += (size_t)blockIdx.y * M;
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t g = lane >> 5, li = lane & 31u;
+    const uint32_t g = lane / LPR, li = lane % LPR;
     const uint32_t S = K >> 6;
-    const uint32_t spw = 4u * ((S + 31u) >> 5);
-    const uint32_t s0 = wave * spw, s1 = min(s0 + spw, S);  // empty (s0 >= S) only for short rows
-    auto rowAt = [&](uint32_t j, uint32_t gg) { return (j * gridDim.x + blockIdx.x) * 2u + gg; };
+    const uint32_t spw = (S + ER_CU_WAVES - 1u) / ER_CU_WAVES;
+    const uint32_t s0 = wave * spw, s1 = min(s0 + spw, S);  // empty (s0 >= S) only for S < 8
+    auto rowAt = [&](uint32_t j, uint32_t gg) { return (j * gridDim.x + blockIdx.x) * (uint32_t)PAR + gg; };
     const size_t rowBytes = F::row_bytes(K);
     float res = 0.0f;
     if (s0 < S) {
@@ -1451,19 +1452,19 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
             __builtin_amdgcn_sched_barrier(0);
             if (j + D < J) issue((uint32_t)(j + D), j % D);
             __builtin_amdgcn_sched_barrier(0);
-            acc = group_sum<32>(acc);
+            acc = group_sum<LPR>(acc);
             res = li == (uint32_t)j ? acc : res;
         }
     }
-    if (li < (uint32_t)J) part[wave][2u * li + g] = res;
+    if (li < (uint32_t)J) part[wave][PAR * li + g] = res;
     __syncthreads();  // every wave's partials, limbs, chunk sums and scales are in LDS
     const XLimbs X = xl_view(lds, K);
     const bool ill = xl_ill(X, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f);
     const bool nf = !ill && nf_any_chunk(X.x16, K >> 4);
-    // lane group (wave, g) finishes steps wave, wave + 8, ..., parity g
+    // lane group (wave, g) finishes steps wave, wave + 8, ..., row g
 #pragma unroll 1
     for (uint32_t st = wave; st < (uint32_t)J; st += ER_CU_WAVES) {
-        const uint32_t lr = 2u * st + g;
+        const uint32_t lr = PAR * st + g;
         const uint32_t row = rowAt(st, g);
         float v = 0.0f;
 #pragma unroll
@@ -1474,9 +1475,9 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
             const uint32_t rc = min(row, M - 1u);
             float sp1[1] = {0.0f}, h = 0.0f;
             nf_terms<1>([&](int, uint32_t k) { return weight_at<F::FMT>(W + (size_t)rc * rowBytes, k); },
-                        [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, li, 32u, sp1, h, ill);
-            const float fv = group_sum<32>(sp1[0]);
-            h = group_sum<32>(h);
+                        [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, li, LPR, sp1, h, ill);
+            const float fv = group_sum<LPR>(sp1[0]);
+            h = group_sum<LPR>(h);
             v = (ill || h > 0.0f) ? fv : v;
         }
         if (li == 0 && row < M) y[row] = v;
@@ -2058,21 +2059,29 @@ ER_CU_CONFIGS_Q4K(ER_CU_ENTRY_Q4K)
 ER_CU_CONFIGS_Q8(ER_CU_ENTRY_Q8)
 ER_CU_CONFIGS_Q6K(ER_CU_ENTRY_Q6K)
 
-// K-sliced CU-resident kernels: er_gemv_<fmt>_cuk_j<J>, J = 1..ER_CUK_MAX_STEPS row
-// steps of 2 rows per workgroup, grid (ceil(M / 2J), batch), dynamic LDS xl_lds_bytes(K).
-#define ER_CUK_ENTRY(fmt, F, J)                                                                     \
+// K-sliced CU-resident kernels: er_gemv_<fmt>_cuk<PAR>_j<J>, J = 1..ER_CUK_MAX_STEPS
+// row steps of PAR rows per workgroup (J <= 64 / PAR), grid (ceil(M / (PAR J)),
+// batch), dynamic LDS xl_lds_bytes(K).
+#define ER_CUK_ENTRY(fmt, F, PAR, J)                                                                \
     extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                                 \
-        er_gemv_##fmt##_cuk_j##J(const uint8_t *__restrict__ W, const float *__restrict__ x,         \
-                                 float *__restrict__ y, uint32_t M, uint32_t K) {                   \
-        gemv_cuk<F, J>(W, x, y, M, K);                                                              \
+        er_gemv_##fmt##_cuk##PAR##_j##J(const uint8_t *__restrict__ W, const float *__restrict__ x,  \
+                                        float *__restrict__ y, uint32_t M, uint32_t K) {            \
+        gemv_cuk<F, PAR, J>(W, x, y, M, K);                                                         \
     }
-#define ER_CUK_ENTRIES(fmt, F)                                                                        \
-    ER_CUK_ENTRY(fmt, F, 1) ER_CUK_ENTRY(fmt, F, 2) ER_CUK_ENTRY(fmt, F, 3) ER_CUK_ENTRY(fmt, F, 4)   \
-    ER_CUK_ENTRY(fmt, F, 5) ER_CUK_ENTRY(fmt, F, 6) ER_CUK_ENTRY(fmt, F, 7) ER_CUK_ENTRY(fmt, F, 8)   \
-    ER_CUK_ENTRY(fmt, F, 9) ER_CUK_ENTRY(fmt, F, 10) ER_CUK_ENTRY(fmt, F, 11) ER_CUK_ENTRY(fmt, F, 12) \
-    ER_CUK_ENTRY(fmt, F, 13) ER_CUK_ENTRY(fmt, F, 14) ER_CUK_ENTRY(fmt, F, 15) ER_CUK_ENTRY(fmt, F, 16)
-ER_CUK_ENTRIES(q4k, CuQ4K)
-ER_CUK_ENTRIES(q8_0, CuQ8)
+#define ER_CUK_ENTRIES8(fmt, F, PAR)                                                                        \
+    ER_CUK_ENTRY(fmt, F, PAR, 1) ER_CUK_ENTRY(fmt, F, PAR, 2) ER_CUK_ENTRY(fmt, F, PAR, 3)                  \
+    ER_CUK_ENTRY(fmt, F, PAR, 4) ER_CUK_ENTRY(fmt, F, PAR, 5) ER_CUK_ENTRY(fmt, F, PAR, 6)                  \
+    ER_CUK_ENTRY(fmt, F, PAR, 7) ER_CUK_ENTRY(fmt, F, PAR, 8)
+#define ER_CUK_ENTRIES16(fmt, F, PAR)                                                                       \
+    ER_CUK_ENTRIES8(fmt, F, PAR) ER_CUK_ENTRY(fmt, F, PAR, 9) ER_CUK_ENTRY(fmt, F, PAR, 10)                 \
+    ER_CUK_ENTRY(fmt, F, PAR, 11) ER_CUK_ENTRY(fmt, F, PAR, 12) ER_CUK_ENTRY(fmt, F, PAR, 13)               \
+    ER_CUK_ENTRY(fmt, F, PAR, 14) ER_CUK_ENTRY(fmt, F, PAR, 15) ER_CUK_ENTRY(fmt, F, PAR, 16)
+ER_CUK_ENTRIES16(q4k, CuQ4K, 2)
+ER_CUK_ENTRIES16(q4k, CuQ4K, 4)
+ER_CUK_ENTRIES8(q4k, CuQ4K, 8)
+ER_CUK_ENTRIES16(q8_0, CuQ8, 2)
+ER_CUK_ENTRIES16(q8_0, CuQ8, 4)
+ER_CUK_ENTRIES8(q8_0, CuQ8, 8)
 
 // Multi-matrix and GeGLU Q4_K kernels: R counts row computations per lane
 // group (GeGLU: R/2 gate rows + the matching up rows).

@@ -210,8 +210,8 @@ struct er_hip_ctx {
     hipFunction_t fnQ8Cu[kCuCountQ8][ER_CU_MAX_STEPS + 1] = {};
     hipFunction_t fnQ6KCu[kCuCountQ6K][ER_CU_MAX_STEPS + 1] = {};
     hipFunction_t fnQ6KTop1Cu[kCuCountQ6K][ER_CU_MAX_STEPS + 1] = {};
-    hipFunction_t fnQ4KCuk[ER_CUK_MAX_STEPS] = {};  // [row steps - 1]
-    hipFunction_t fnQ8Cuk[ER_CUK_MAX_STEPS] = {};
+    hipFunction_t fnQ4KCuk[3][ER_CUK_MAX_STEPS] = {};  // [2, 4, 8 rows per step][row steps - 1]
+    hipFunction_t fnQ8Cuk[3][ER_CUK_MAX_STEPS] = {};
     hipFunction_t fnQ4KMulti[kI8MultiCount] = {};
     hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
     hipFunction_t fnQ8Multi[kI8MultiCount] = {};
@@ -220,7 +220,7 @@ struct er_hip_ctx {
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
     int multi_override = -1;  // ER_HIP_GEMV_MULTI_CONFIG=lpr:ns:r for the multi-matrix kernels (tests, sweeps)
     int cu_mode = -1;      // ER_HIP_GEMV_CU: 0 never, 1 whenever it applies, unset: by shape
-    int cuk_mode = -1;     // ER_HIP_GEMV_CUK=0: long rows on the whole-row CU kernels (comparisons)
+    int cuk_mode = -1;     // ER_HIP_GEMV_CUK: 0 never, 2 every K <= 16384, unset: K > 8192 (comparisons)
     int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1: non-pipelined GEMM, =2: 256-thread pipelined,
                            // =3: warp-specialised, =4 / =5: loader-specialised with 256 / 128-row tiles
                            // wherever it applies (comparisons, tests)
@@ -485,23 +485,38 @@ bool plan_cu(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batc
     return true;
 }
 
-// K-sliced CU-resident kernels (er_gemv.hip gemv_cuk) for Q4_K / Q8_0 rows of
-// 8192 < K <= 16384 weights (K % 256 == 0): 2 rows per workgroup step, up to
-// ER_CUK_MAX_STEPS steps, about one workgroup per CU for one token's rows
-// (more workgroups beyond 32 rows per CU).  A row's value depends on K alone.
+// K-sliced CU-resident kernels (er_gemv.hip gemv_cuk), PAR = 2, 4 or 8 rows per
+// workgroup step as the row has up to 256, 128 or 64 slots (each wave's slice
+// then fills 16 of 32, 9 of 16 ... all lanes of its row slices), up to
+// ER_CUK_MAX_STEPS steps (8 for PAR 8), about one workgroup per CU for one
+// token's rows (more beyond).  Taken by default for Q4_K / Q8_0 rows of
+// 4096 < K <= 16384 weights at any M, and for Q4_K rows of K = 4096 when one
+// token's rows give each CU at least 8 (A/B in one process against the
+// whole-row kernels: 2048 / 8192 / 14336 / 28672 x 4096 -7 / -3 / -1 / -9%,
+// 1024 x 4096 +11%; Q8_0 14336 x 4096 +1.6%, so Q8_0 keeps its spread kernel
+// there).  ER_HIP_GEMV_CUK=2 takes them for every K <= 16384 (K % 256 == 0),
+// =0 never, and ER_HIP_GEMV_CU=0/1 (lane-group / whole-row CU kernels forced)
+// turns them off.  The choice depends on M and K alone, and a row's value on
+// K alone.
 struct CukPlan {
+    int pi = 0;              // PAR = 2 << pi
     int j = 0;               // row steps per lane group
-    uint32_t rowsPerWg = 0;  // 2 j
+    uint32_t rowsPerWg = 0;  // PAR j
 };
 bool plan_cuk(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batch, CukPlan &p) {
-    if (f == Fmt::Q6_K || K % 256u != 0 || K <= 8192u || K > 16384u || ctx->gemv_fp32 != 0 ||
-        ctx->i8_override >= 0 || ctx->cu_mode == 0 || ctx->cuk_mode == 0 || batch == 0 ||
+    if (f == Fmt::Q6_K || K % 256u != 0 || K > 16384u || ctx->gemv_fp32 != 0 || ctx->i8_override >= 0 ||
+        ctx->cu_mode >= 0 || ctx->cuk_mode == 0 || batch == 0 ||
         (uint64_t)xl_lds_bytes(K) + 1024u > ctx->info.lds_per_workgroup)
         return false;
-    const uint32_t perToken = std::max<uint32_t>(1u, (uint32_t)ctx->cu_count / batch);
+    const uint32_t S = K / 64u, cu = (uint32_t)ctx->cu_count;
+    if (ctx->cuk_mode != 2 && (S < 64u || (S == 64u && (f != Fmt::Q4_K || (M + cu - 1u) / cu < 8u))))
+        return false;
+    p.pi = S <= 64u ? 2 : (S <= 128u ? 1 : 0);
+    const uint32_t par = 2u << p.pi, maxJ = p.pi == 2 ? 8u : (uint32_t)ER_CUK_MAX_STEPS;
+    const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
     const uint32_t rows = (M + perToken - 1u) / perToken;  // per workgroup, one token
-    p.j = (int)std::min<uint32_t>(ER_CUK_MAX_STEPS, std::max<uint32_t>(1u, (rows + 1u) / 2u));
-    p.rowsPerWg = 2u * (uint32_t)p.j;
+    p.j = (int)std::min<uint32_t>(maxJ, std::max<uint32_t>(1u, (rows + par - 1u) / par));
+    p.rowsPerWg = par * (uint32_t)p.j;
     return true;
 }
 
@@ -523,7 +538,7 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     if (plan_cuk(ctx, f, M, K, batch, kp)) {
         dim3 grid((M + kp.rowsPerWg - 1u) / kp.rowsPerWg, batch, 1);
         void *kargs[] = {&W.data, &x.data, &y.data, &M, &K};
-        return launch_fn(f == Fmt::Q4_K ? ctx->fnQ4KCuk[kp.j - 1] : ctx->fnQ8Cuk[kp.j - 1],
+        return launch_fn(f == Fmt::Q4_K ? ctx->fnQ4KCuk[kp.pi][kp.j - 1] : ctx->fnQ8Cuk[kp.pi][kp.j - 1],
                          f == Fmt::Q4_K ? "er_gemv_q4k_cuk" : "er_gemv_q8_0_cuk", grid,
                          dim3(64u * ER_CU_WAVES, 1, 1), xl_lds_bytes(K), stream, kargs);
     }
@@ -1292,17 +1307,19 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
                 }
             }
     }
-    for (int j = 1; j <= ER_CUK_MAX_STEPS; ++j)
-        for (int kind = 0; kind < 2; ++kind) {
-            char name[64];
-            std::snprintf(name, sizeof(name), "er_gemv_%s_cuk_j%d", kind == 0 ? "q4k" : "q8_0", j);
-            e = hipModuleGetFunction(kind == 0 ? &ctx->fnQ4KCuk[j - 1] : &ctx->fnQ8Cuk[j - 1], ctx->module, name);
-            if (e != hipSuccess) {
-                (void)hipModuleUnload(ctx->module);
-                delete ctx;
-                return fail(ER_ERR_FUNCTION_NOT_FOUND, "functionNotFound(%s): %s", name, hipGetErrorString(e));
+    for (int pi = 0; pi < 3; ++pi)
+        for (int j = 1; j <= (pi == 2 ? 8 : ER_CUK_MAX_STEPS); ++j)
+            for (int kind = 0; kind < 2; ++kind) {
+                char name[64];
+                std::snprintf(name, sizeof(name), "er_gemv_%s_cuk%d_j%d", kind == 0 ? "q4k" : "q8_0", 2 << pi, j);
+                e = hipModuleGetFunction(kind == 0 ? &ctx->fnQ4KCuk[pi][j - 1] : &ctx->fnQ8Cuk[pi][j - 1],
+                                         ctx->module, name);
+                if (e != hipSuccess) {
+                    (void)hipModuleUnload(ctx->module);
+                    delete ctx;
+                    return fail(ER_ERR_FUNCTION_NOT_FOUND, "functionNotFound(%s): %s", name, hipGetErrorString(e));
+                }
             }
-        }
     for (int i = 0; i < kI8MultiCount; ++i) {
         char name[64];
         static const char *const kinds[4] = {"q4k_multi", "q4k_geglu", "q8_0_multi", "q8_0_silu"};
@@ -1331,7 +1348,7 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
         }
     }
     if (const char *cv = std::getenv("ER_HIP_GEMV_CU")) ctx->cu_mode = std::atoi(cv) != 0 ? 1 : 0;
-    if (const char *kv = std::getenv("ER_HIP_GEMV_CUK")) ctx->cuk_mode = std::atoi(kv) != 0 ? 1 : 0;
+    if (const char *kv = std::getenv("ER_HIP_GEMV_CUK")) ctx->cuk_mode = std::atoi(kv);
     if (const char *mv = std::getenv("ER_HIP_GEMV_MULTI_CONFIG")) {
         unsigned l = 0, n = 0, r = 0;
         if (std::sscanf(mv, "%u:%u:%u", &l, &n, &r) == 3)

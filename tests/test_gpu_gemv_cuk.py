@@ -47,6 +47,13 @@ def whole_rows():
     c.close()
 
 
+@pytest.fixture(scope="module")
+def cuk_everywhere():
+    c = _ctx(ER_HIP_GEMV_CUK="2")
+    yield GEMVKernel(c)
+    c.close()
+
+
 def sample_rows(M):
     return np.unique(np.linspace(0, M - 1, 61).astype(np.int64))
 
@@ -159,3 +166,46 @@ def test_heavy_tailed_x(gemv, fmt, amp):
     W, x = heavy_case(fmt, M, K, amp, 3)
     y = getattr(gemv, EXEC[fmt])(W, x, M, K)
     check(y, ref.gemv(fmt, W, x, M, K, threads=ref.max_threads()))
+
+
+# ER_HIP_GEMV_CUK=2 takes the K-sliced kernels for every K <= 16384: 8 rows per
+# step for rows of up to 64 slots (K <= 4096), 4 for up to 128.  K = 256 and
+# 512 leave waves with no slice.
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("K", [256, 512, 1024, 3072, 4096, 6144, 8192])
+def test_short_rows_every_step_count(cuk_everywhere, whole_rows, fmt, K):
+    cus = cuk_everywhere.ctx.compute_units
+    par = 8 if K <= 4096 else 4
+    x = synth.normal_f32(synth.seed(115, K % 97), K)
+    for j in range(1, (8 if par == 8 else 16) + 1, 3 if par == 4 else 1):
+        M = cus * par * j
+        W = synth.weights(fmt, synth.seed(115, 10 * j + K % 7), M, K, **DSCALE[fmt])
+        y = getattr(cuk_everywhere, EXEC[fmt])(W, x, M, K)
+        assert np.all(np.isfinite(y)), (fmt, K, j)
+        rows = sample_rows(M)
+        assert rel_l2(y[rows], oracle_rows(fmt, W, x, M, K, rows)) < TOL, (fmt, K, j)
+        other = getattr(whole_rows, EXEC[fmt])(W, x, M, K)
+        assert rel_l2(y, other) < 1e-5, (fmt, K, j, rel_l2(y, other))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("kind", ["nan", "pm_inf"])
+def test_short_rows_nonfinite_and_one_hot(cuk_everywhere, fmt, kind):
+    M, K = 777, 4096
+    W = synth.weights(fmt, synth.seed(116, 0), M, K, **DSCALE[fmt])
+    x = synth.normal_f32(synth.seed(116, 1), K).copy()
+    if kind == "nan":
+        x[1000] = np.nan
+    else:
+        x[3] = np.inf
+        x[4000] = -np.inf
+    y = getattr(cuk_everywhere, EXEC[fmt])(W, x, M, K)
+    exp = ref.gemv(fmt, W, x, M, K, threads=ref.max_threads())
+    assert np.array_equal(np.isnan(y), np.isnan(exp))
+    inf = np.isinf(exp)
+    assert np.array_equal(y[inf], exp[inf])
+    cols = rn.weights_f32(fmt, W, M, K)
+    for j in (0, 511, 512, K - 1):
+        xo = np.zeros(K, np.float32)
+        xo[j] = 1.0
+        assert np.array_equal(getattr(cuk_everywhere, EXEC[fmt])(W, xo, M, K), cols[:, j]), j
