@@ -1366,8 +1366,10 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
 // back from LDS (3 bytes per weight: 688 KB per CU at 4096 x 14336, as much
 // LDS time as the dot products take), and no wave starts before the whole of
 // x is converted.  Here wave w owns the slots [spw w, spw (w + 1)) of every
-// row of its workgroup, spw = ceil(S / 8) <= LPR = 64 / PAR (Q4_K and Q8_0
-// slots are single 64-groups, so a slot's x is the wave's own).  It loads and
+// row of its workgroup, spw = ceil(S / 8) <= LPR = 64 / PAR (a Q4_K or Q8_0
+// slot is one 64-group; a Q6_K slot takes x from two groups of its 256-block,
+// so for Q6_K spw is a multiple of 4 and a wave's slice whole blocks: either
+// way a slot's x is the wave's own).  It loads and
 // converts only that slice of x, keeps each lane's slot of limbs in
 // registers, and walks the workgroup's rows PAR at a time: lane LPR g + li
 // takes row g of the step and slot spw w + li (lanes past the slice reuse its
@@ -1377,15 +1379,21 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
 // row meet in LDS and are added in wave order, so a row's value depends on K
 // alone, not on the row partition or the batch.  J row steps per lane group,
 // F::UNITS in flight.
-template <class F, int PAR, int J>
+// TOP1: instead of storing y, the workgroup's row values go to LDS and wave 0
+// merges their quads into the partial (pv, pi)[blockIdx.x] (M a multiple of
+// 4).  Quads of 4 consecutive rows stay in one workgroup: with PAR = 2 the
+// steps pair up, step j taking rows ((j / 2) * gridDim.x + blockIdx.x) * 4 +
+// 2 (j % 2) + g, and J is even.  The row values are the plain kernel's.
+template <class F, int PAR, int J, bool TOP1 = false>
 ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
-                     uint32_t M, uint32_t K) {
+                     uint32_t M, uint32_t K, float *__restrict__ pv = nullptr, uint32_t *__restrict__ pi = nullptr) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     constexpr uint32_t LPR = 64u / PAR;  // lanes per row slice
     __shared__ float part[ER_CU_WAVES][PAR * J];  // [wave][local row PAR j + g]
+    __shared__ float tv[TOP1 ? PAR * J : 1];      // top-1: the workgroup's row values
     static_assert(PAR == 2 || PAR == 4 || PAR == 8, "2, 4 or 8 rows per step");
-    static_assert(F::FMT != ER_FMT_Q6_K, "a Q6_K slot spans two x groups");
     static_assert(J >= 1 && J <= (int)LPR && J <= ER_CUK_MAX_STEPS, "row sums parked one per lane of a slice");
+    static_assert(!TOP1 || PAR > 2 || J % 2 == 0, "top-1 quads pair the steps of 2-row slices");
     constexpr int D = F::UNITS < J ? F::UNITS : J;
     // x pieces per wave: 16-value chunks (4 spw <= 4 LPR, 64 per pass), or for
     // 8-lane slices 8-value halves (8 spw <= 64: one pass)
@@ -1396,9 +1404,12 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t g = lane / LPR, li = lane % LPR;
     const uint32_t S = K >> 6;
-    const uint32_t spw = (S + ER_CU_WAVES - 1u) / ER_CU_WAVES;
-    const uint32_t s0 = wave * spw, s1 = min(s0 + spw, S);  // empty (s0 >= S) only for S < 8
-    auto rowAt = [&](uint32_t j, uint32_t gg) { return (j * gridDim.x + blockIdx.x) * (uint32_t)PAR + gg; };
+    const uint32_t spw = F::FMT == ER_FMT_Q6_K ? 4u * ((S + 31u) >> 5) : (S + ER_CU_WAVES - 1u) / ER_CU_WAVES;
+    const uint32_t s0 = wave * spw, s1 = min(s0 + spw, S);  // empty (s0 >= S) only for short rows
+    auto rowAt = [&](uint32_t j, uint32_t gg) {
+        return (TOP1 && PAR == 2) ? ((j >> 1) * gridDim.x + blockIdx.x) * 4u + 2u * (j & 1u) + gg
+                                  : (j * gridDim.x + blockIdx.x) * (uint32_t)PAR + gg;
+    };
     const size_t rowBytes = F::row_bytes(K);
     float res = 0.0f;
     if (s0 < S) {
@@ -1480,7 +1491,15 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
             h = group_sum<LPR>(h);
             v = (ill || h > 0.0f) ? fv : v;
         }
-        if (li == 0 && row < M) y[row] = v;
+        if constexpr (TOP1) {
+            if (li == 0) tv[lr] = v;
+        } else {
+            if (li == 0 && row < M) y[row] = v;
+        }
+    }
+    if constexpr (TOP1) {
+        __syncthreads();
+        top1_partial(tv, PAR * J / 4u, M, [&](uint32_t l) { return rowAt(l / PAR, l % PAR); }, pv, pi);
     }
 }
 
@@ -2082,6 +2101,23 @@ ER_CUK_ENTRIES8(q4k, CuQ4K, 8)
 ER_CUK_ENTRIES16(q8_0, CuQ8, 2)
 ER_CUK_ENTRIES16(q8_0, CuQ8, 4)
 ER_CUK_ENTRIES8(q8_0, CuQ8, 8)
+// Q6_K: rows of more than 64 slots (2 and 4 rows per step), and the top-1
+// forms (er_gemv_q6k_top1_cuk<PAR>_j<J>: (W, x, pv, pi, M, K), even J for PAR 2)
+ER_CUK_ENTRIES16(q6k, CuQ6K, 2)
+ER_CUK_ENTRIES16(q6k, CuQ6K, 4)
+#define ER_CUK_TOP1_ENTRY(PAR, J)                                                                      \
+    extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                                    \
+        er_gemv_q6k_top1_cuk##PAR##_j##J(const uint8_t *__restrict__ W, const float *__restrict__ x,    \
+                                         float *__restrict__ pv, uint32_t *__restrict__ pi, uint32_t M, \
+                                         uint32_t K) {                                                  \
+        gemv_cuk<CuQ6K, PAR, J, true>(W, x, nullptr, M, K, pv, pi);                                   \
+    }
+ER_CUK_TOP1_ENTRY(2, 2) ER_CUK_TOP1_ENTRY(2, 4) ER_CUK_TOP1_ENTRY(2, 6) ER_CUK_TOP1_ENTRY(2, 8)
+ER_CUK_TOP1_ENTRY(2, 10) ER_CUK_TOP1_ENTRY(2, 12) ER_CUK_TOP1_ENTRY(2, 14) ER_CUK_TOP1_ENTRY(2, 16)
+ER_CUK_TOP1_ENTRY(4, 1) ER_CUK_TOP1_ENTRY(4, 2) ER_CUK_TOP1_ENTRY(4, 3) ER_CUK_TOP1_ENTRY(4, 4)
+ER_CUK_TOP1_ENTRY(4, 5) ER_CUK_TOP1_ENTRY(4, 6) ER_CUK_TOP1_ENTRY(4, 7) ER_CUK_TOP1_ENTRY(4, 8)
+ER_CUK_TOP1_ENTRY(4, 9) ER_CUK_TOP1_ENTRY(4, 10) ER_CUK_TOP1_ENTRY(4, 11) ER_CUK_TOP1_ENTRY(4, 12)
+ER_CUK_TOP1_ENTRY(4, 13) ER_CUK_TOP1_ENTRY(4, 14) ER_CUK_TOP1_ENTRY(4, 15) ER_CUK_TOP1_ENTRY(4, 16)
 
 // Multi-matrix and GeGLU Q4_K kernels: R counts row computations per lane
 // group (GeGLU: R/2 gate rows + the matching up rows).

@@ -212,6 +212,8 @@ struct er_hip_ctx {
     hipFunction_t fnQ6KTop1Cu[kCuCountQ6K][ER_CU_MAX_STEPS + 1] = {};
     hipFunction_t fnQ4KCuk[3][ER_CUK_MAX_STEPS] = {};  // [2, 4, 8 rows per step][row steps - 1]
     hipFunction_t fnQ8Cuk[3][ER_CUK_MAX_STEPS] = {};
+    hipFunction_t fnQ6KCuk[2][ER_CUK_MAX_STEPS] = {};      // [2, 4 rows per step][row steps - 1]
+    hipFunction_t fnQ6KTop1Cuk[2][ER_CUK_MAX_STEPS] = {};  // even steps only for 2 rows per step
     hipFunction_t fnQ4KMulti[kI8MultiCount] = {};
     hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
     hipFunction_t fnQ8Multi[kI8MultiCount] = {};
@@ -497,22 +499,26 @@ bool plan_cu(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batc
 // there).  ER_HIP_GEMV_CUK=2 takes them for every K <= 16384 (K % 256 == 0),
 // =0 never, and ER_HIP_GEMV_CU=0/1 (lane-group / whole-row CU kernels forced)
 // turns them off.  The choice depends on M and K alone, and a row's value on
-// K alone.
+// K alone.  Q6_K takes them for rows of 4096 < K <= 16384 when one token's
+// rows fill at most one workgroup per CU (4096 x 14336: 13.5 against 18.3 us
+// on the lane-group kernels; 128256 x 4096 heads ran 17% slower over 8
+// workgroups per CU), and its top-1 follows the same plan.
 struct CukPlan {
     int pi = 0;              // PAR = 2 << pi
     int j = 0;               // row steps per lane group
     uint32_t rowsPerWg = 0;  // PAR j
 };
 bool plan_cuk(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batch, CukPlan &p) {
-    if (f == Fmt::Q6_K || K % 256u != 0 || K > 16384u || ctx->gemv_fp32 != 0 || ctx->i8_override >= 0 ||
+    if (K % 256u != 0 || K > 16384u || ctx->gemv_fp32 != 0 || ctx->i8_override >= 0 ||
         ctx->cu_mode >= 0 || ctx->cuk_mode == 0 || batch == 0 ||
         (uint64_t)xl_lds_bytes(K) + 1024u > ctx->info.lds_per_workgroup)
         return false;
-    const uint32_t S = K / 64u, cu = (uint32_t)ctx->cu_count;
-    if (ctx->cuk_mode != 2 && (S < 64u || (S == 64u && (f != Fmt::Q4_K || (M + cu - 1u) / cu < 8u))))
-        return false;
+    const uint32_t S = K / 64u, cu = (uint32_t)ctx->cu_count, rows1 = (M + cu - 1u) / cu;
     p.pi = S <= 64u ? 2 : (S <= 128u ? 1 : 0);
     const uint32_t par = 2u << p.pi, maxJ = p.pi == 2 ? 8u : (uint32_t)ER_CUK_MAX_STEPS;
+    if (f == Fmt::Q6_K ? (S <= 64u || rows1 > par * maxJ)
+                       : (ctx->cuk_mode != 2 && (S < 64u || (S == 64u && (f != Fmt::Q4_K || rows1 < 8u)))))
+        return false;
     const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
     const uint32_t rows = (M + perToken - 1u) / perToken;  // per workgroup, one token
     p.j = (int)std::min<uint32_t>(maxJ, std::max<uint32_t>(1u, (rows + par - 1u) / par));
@@ -538,8 +544,11 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     if (plan_cuk(ctx, f, M, K, batch, kp)) {
         dim3 grid((M + kp.rowsPerWg - 1u) / kp.rowsPerWg, batch, 1);
         void *kargs[] = {&W.data, &x.data, &y.data, &M, &K};
-        return launch_fn(f == Fmt::Q4_K ? ctx->fnQ4KCuk[kp.pi][kp.j - 1] : ctx->fnQ8Cuk[kp.pi][kp.j - 1],
-                         f == Fmt::Q4_K ? "er_gemv_q4k_cuk" : "er_gemv_q8_0_cuk", grid,
+        return launch_fn(f == Fmt::Q4_K   ? ctx->fnQ4KCuk[kp.pi][kp.j - 1]
+                         : f == Fmt::Q8_0 ? ctx->fnQ8Cuk[kp.pi][kp.j - 1]
+                                          : ctx->fnQ6KCuk[kp.pi][kp.j - 1],
+                         f == Fmt::Q4_K ? "er_gemv_q4k_cuk" : (f == Fmt::Q8_0 ? "er_gemv_q8_0_cuk" : "er_gemv_q6k_cuk"),
+                         grid,
                          dim3(64u * ER_CU_WAVES, 1, 1), xl_lds_bytes(K), stream, kargs);
     }
     CuPlan cp;
@@ -717,6 +726,7 @@ er_status launch_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buf
     if (st != ER_OK) return st;
     uint32_t count = 0;
     CuPlan cp;
+    CukPlan kp;
     if (M > 0 && fp32) {
         const bool xg = (uint64_t)K * 4u > kLdsXLimit;
         const uint32_t lpr = lanes_per_row((K / 256u) * 4u);
@@ -725,6 +735,17 @@ er_status launch_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buf
         count = (M + rowsPerBlock - 1u) / rowsPerBlock;
         void *args[] = {&W.data, &x.data, &pv, &pi, &M, &K};
         st = launch(ctx, k, dim3(count, 1, 1), dim3(kGemvThreads, 1, 1), xg ? 0u : K * 4u, stream, args);
+        if (st != ER_OK) return st;
+    } else if (M > 0 && plan_cuk(ctx, Fmt::Q6_K, M, K, 1u, kp)) {
+        // the K-sliced kernel's top-1 form (2 rows per step: an even step
+        // count, so quads stay in one workgroup); one partial per workgroup
+        // of >= 4 rows, so at most M/4
+        const int j = kp.pi == 0 ? (kp.j + 1) & ~1 : kp.j;
+        const uint32_t rowsPerWg = (2u << kp.pi) * (uint32_t)j;
+        count = (M + rowsPerWg - 1u) / rowsPerWg;
+        void *args[] = {&W.data, &x.data, &pv, &pi, &M, &K};
+        st = launch_fn(ctx->fnQ6KTop1Cuk[kp.pi][j - 1], "er_gemv_q6k_top1_cuk", dim3(count, 1, 1),
+                       dim3(64u * ER_CU_WAVES, 1, 1), xl_lds_bytes(K), stream, args);
         if (st != ER_OK) return st;
     } else if (M > 0 && plan_cu(ctx, Fmt::Q6_K, M, K, 1u, cp)) {
         // one partial per workgroup (rowsPerWg >= 8, so at most M/4); the
@@ -1309,11 +1330,18 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
     }
     for (int pi = 0; pi < 3; ++pi)
         for (int j = 1; j <= (pi == 2 ? 8 : ER_CUK_MAX_STEPS); ++j)
-            for (int kind = 0; kind < 2; ++kind) {
+            for (int kind = 0; kind < 4; ++kind) {
+                // q4k, q8_0 (2, 4, 8 rows per step); q6k and its top-1 (2, 4;
+                // the top-1 with 2 rows per step at even step counts)
+                if (kind >= 2 && (pi == 2 || (kind == 3 && pi == 0 && j % 2 != 0))) continue;
+                static const char *const kinds[4] = {"q4k", "q8_0", "q6k", "q6k_top1"};
+                hipFunction_t *const slot = kind == 0   ? &ctx->fnQ4KCuk[pi][j - 1]
+                                            : kind == 1 ? &ctx->fnQ8Cuk[pi][j - 1]
+                                            : kind == 2 ? &ctx->fnQ6KCuk[pi][j - 1]
+                                                        : &ctx->fnQ6KTop1Cuk[pi][j - 1];
                 char name[64];
-                std::snprintf(name, sizeof(name), "er_gemv_%s_cuk%d_j%d", kind == 0 ? "q4k" : "q8_0", 2 << pi, j);
-                e = hipModuleGetFunction(kind == 0 ? &ctx->fnQ4KCuk[pi][j - 1] : &ctx->fnQ8Cuk[pi][j - 1],
-                                         ctx->module, name);
+                std::snprintf(name, sizeof(name), "er_gemv_%s_cuk%d_j%d", kinds[kind], 2 << pi, j);
+                e = hipModuleGetFunction(slot, ctx->module, name);
                 if (e != hipSuccess) {
                     (void)hipModuleUnload(ctx->module);
                     delete ctx;

@@ -1,4 +1,4 @@
-"""K-sliced CU-resident GEMV kernels (Q4_K and Q8_0 rows of 8192 < K <= 16384
+"""K-sliced CU-resident GEMV kernels (Q4_K, Q8_0 and Q6_K rows of up to 16384
 weights, the Llama FFN down projection 4096 x 14336 among them): each wave of
 a workgroup owns a slice of K, so a row's value is the sum of 8 wave partials.
 Against the CPU oracle at the GEMV parity bar (relative L2 <= 1e-3) on 61
@@ -6,7 +6,9 @@ rows spread over each matrix, and every row against the whole-row kernels
 (ER_HIP_GEMV_CUK=0) at 1e-5; every unrolled step count 1..16; slices that end
 mid-wave and a wave with no slice (K = 8448: 20 slots per wave, 132 slots);
 exact one-hot columns at the slice boundaries; the same row bit for bit
-whatever the row partition or the batch; non-finite and heavy-tailed x."""
+whatever the row partition or the batch; non-finite and heavy-tailed x; the
+Q6_K top-1 on the same kernels equal to the selection rule over the plain
+call's logits."""
 import os
 
 import numpy as np
@@ -21,10 +23,12 @@ from conftest import rel_l2
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
-DSCALE = {"q8_0": {"dscale": 0.02}, "q4_k": {"dscale": 0.01, "dminscale": 0.01}}
-EXEC = {"q8_0": "executeQ8_0Weights", "q4_k": "executeQ4KWeights"}
-EXEC_B = {"q8_0": "executeBatchedQ8_0Weights", "q4_k": "executeBatchedQ4KWeights"}
-FMTS = ["q4_k", "q8_0"]
+DSCALE = {"q8_0": {"dscale": 0.02}, "q4_k": {"dscale": 0.01, "dminscale": 0.01}, "q6_k": {"dscale": 0.005}}
+EXEC = {"q8_0": "executeQ8_0Weights", "q4_k": "executeQ4KWeights", "q6_k": "executeQ6KWeights"}
+EXEC_B = {"q8_0": "executeBatchedQ8_0Weights", "q4_k": "executeBatchedQ4KWeights",
+          "q6_k": "executeBatchedQ6KWeights"}
+FMTS = ["q4_k", "q8_0", "q6_k"]  # long rows: all three formats
+FMTS_SHORT = ["q4_k", "q8_0"]     # ER_HIP_GEMV_CUK=2 short rows: Q6_K keeps its whole-row kernels
 
 
 def _ctx(**env):
@@ -63,8 +67,9 @@ def oracle_rows(fmt, W, x, M, K, rows):
     return ref.gemv(fmt, Wr, x, len(rows), K)
 
 
-# K: 132 slots (20 per wave, the last wave empty), 172 (24 per wave, 4 in the
-# last), 192, 224 (28 per wave, half of the last conversion pass), 256
+# K: 132 slots (17 per wave; for Q6_K 20, the last wave empty), 172 (22 per
+# wave; Q6_K 24, 4 in the last), 192, 224 (28 per wave, half of the last
+# conversion pass), 256
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("K", [8448, 11008, 12288, 14336, 16384])
 def test_every_step_count(gemv, whole_rows, fmt, K):
@@ -171,7 +176,7 @@ def test_heavy_tailed_x(gemv, fmt, amp):
 # ER_HIP_GEMV_CUK=2 takes the K-sliced kernels for every K <= 16384: 8 rows per
 # step for rows of up to 64 slots (K <= 4096), 4 for up to 128.  K = 256 and
 # 512 leave waves with no slice.
-@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("fmt", FMTS_SHORT)
 @pytest.mark.parametrize("K", [256, 512, 1024, 3072, 4096, 6144, 8192])
 def test_short_rows_every_step_count(cuk_everywhere, whole_rows, fmt, K):
     cus = cuk_everywhere.ctx.compute_units
@@ -188,7 +193,7 @@ def test_short_rows_every_step_count(cuk_everywhere, whole_rows, fmt, K):
         assert rel_l2(y, other) < 1e-5, (fmt, K, j, rel_l2(y, other))
 
 
-@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("fmt", FMTS_SHORT)
 @pytest.mark.parametrize("kind", ["nan", "pm_inf"])
 def test_short_rows_nonfinite_and_one_hot(cuk_everywhere, fmt, kind):
     M, K = 777, 4096
@@ -209,3 +214,39 @@ def test_short_rows_nonfinite_and_one_hot(cuk_everywhere, fmt, kind):
         xo = np.zeros(K, np.float32)
         xo[j] = 1.0
         assert np.array_equal(getattr(cuk_everywhere, EXEC[fmt])(W, xo, M, K), cols[:, j]), j
+
+
+# Q6_K top-1 over the K-sliced kernels: the index equals the selection rule
+# applied to the same context's plain GEMV output.  Shapes: 2 rows per step
+# at 8 and 16 steps, 2 rows at 1 step (the top-1 form rounds to 2), 4 rows
+# per step at 2 and 16 steps.
+@pytest.mark.parametrize("M,K", [(4096, 14336), (8192, 16384), (400, 10240), (1000, 12288), (2048, 8192),
+                                 (16384, 6144)])
+def test_q6k_top1_matches_rule(gemv, M, K):
+    W = synth.weights("q6_k", synth.seed(117, M % 97), M, K, dscale=0.005)
+    x = synth.normal_f32(synth.seed(117, 200 + K % 89), K)
+    y = gemv.executeQ6KWeights(W, x, M, K)
+    assert gemv.executeQ6KWeightsTop1(W, x, M, K) == ref.top1(y)
+    rows = sample_rows(M)
+    assert rel_l2(y[rows], oracle_rows("q6_k", W, x, M, K, rows)) < TOL
+
+
+def test_q6k_top1_ties_and_nan(gemv):
+    """A copy of the winning row at a lower index wins the tie, at a higher one
+    loses it; all-NaN logits keep row 0."""
+    M, K = 4096, 14336
+    W = synth.weights("q6_k", synth.seed(118, 0), M, K, dscale=0.005).reshape(M, -1).copy()
+    x = synth.normal_f32(synth.seed(118, 1), K)
+    a = gemv.executeQ6KWeightsTop1(W.reshape(-1), x, M, K)
+    for b in (0, 5, a // 2 if a > 0 else 3):
+        if b >= a:
+            continue
+        Wt = W.copy()
+        Wt[b] = W[a]
+        assert gemv.executeQ6KWeightsTop1(Wt.reshape(-1), x, M, K) == b
+    hi = min(M - 1, a + 1000)
+    Wt = W.copy()
+    Wt[hi] = W[a]
+    assert gemv.executeQ6KWeightsTop1(Wt.reshape(-1), x, M, K) == min(a, hi)
+    xn = np.full(K, np.nan, np.float32)
+    assert gemv.executeQ6KWeightsTop1(W.reshape(-1), xn, M, K) == 0
