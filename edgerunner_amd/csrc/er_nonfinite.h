@@ -68,19 +68,29 @@ ER_DEV float weight_at(const uint8_t *row, uint32_t k) {
 }
 
 // Wave-uniform: does any of the C16 chunk sums hold a non-finite value?
-// x16 is 16-byte aligned and C16 % 4 == 0 (K % 64 == 0): each lane reads
-// four 16-byte pieces per 1024 chunks, all issued before one wait (a scan of
-// one value per read waited ~100 cycles per 64 chunks at the end of every
-// launch).
+// Up to 256 chunks (K <= 4096) one read per lane per 64 chunks.  Longer rows
+// (x16 16-byte aligned, C16 % 4 == 0) read up to four 16-byte pieces per lane
+// per 1024 chunks, all issued before one wait: one value per read waited ~100
+// cycles per 64 chunks, ~1 us at K = 14336.  (The 16-byte form measured
+// ~0.3 us slower on rows of 1024 weights, so short rows keep the first.)
 ER_DEV bool nf_any_chunk(const float *x16, uint32_t C16) {
-    const float4 *v = (const float4 *)__builtin_assume_aligned(x16, 16);
-    const uint32_t n4 = C16 >> 2, ln = lane_id();
+    const uint32_t ln = lane_id();
     bool f = false;
+    if (C16 <= 256u) {
+#pragma unroll 1
+        for (uint32_t c = ln; c < C16; c += 64u) f |= !__builtin_isfinite(x16[c]);
+        return __builtin_amdgcn_ballot_w64(f) != 0;
+    }
+    const float4 *v = (const float4 *)__builtin_assume_aligned(x16, 16);
+    const uint32_t n4 = C16 >> 2;
 #pragma unroll 1
     for (uint32_t b = 0; b < n4; b += 256u) {
         float4 q[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) q[u] = v[min(b + 64u * u + ln, n4 - 1u)];
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t i = b + 64u * u + ln;
+            q[u] = i < n4 ? v[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             f |= !(__builtin_isfinite(q[u].x) && __builtin_isfinite(q[u].y) && __builtin_isfinite(q[u].z) &&

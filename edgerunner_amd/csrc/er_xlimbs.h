@@ -79,26 +79,33 @@ ER_DEV XLimbs xl_view(const uint32_t *lds, uint32_t K) {
 // Wave-uniform: does the staged x call for the fp32 path (the conditioning
 // rule above; f the format's factor)?  Every wave computes it from the same
 // LDS values in the same order, so all agree.
-// Each lane sums groups lane, lane + 64, ... in that order; the reads of four
-// of them are issued before one wait (the clamped reads past the last group
-// add exact zeros).
+// Each lane sums groups lane, lane + 64, ... in that order; beyond 64 groups
+// the reads of four of them are issued before one wait (groups past the last
+// are skipped and add exact zeros), as in nf_any_chunk.
 ER_DEV bool xl_ill(const XLimbs &X, float f) {
     float e = 0.0f, r = 0.0f;
     const uint32_t S = X.K >> 6, ln = lane_id();
-#pragma unroll 1
-    for (uint32_t b = 0; b < S; b += 256u) {
-        float rg[4], sg[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t gi = min(b + 64u * u + ln, S - 1u);
-            rg[u] = X.rest64[gi];
-            sg[u] = X.sg64[gi];
+    if (S <= 64u) {
+        if (ln < S) {
+            const float rg = X.rest64[ln], sg = X.sg64[ln];
+            e = __builtin_fmaf(rg > 0.0f ? sg : 0.0f, sg, e);
+            r += rg;
         }
+    } else {
+#pragma unroll 1
+        for (uint32_t b = 0; b < S; b += 256u) {
+            float rg[4], sg[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const bool in = b + 64u * u + ln < S;
-            e = __builtin_fmaf(in && rg[u] > 0.0f ? sg[u] : 0.0f, sg[u], e);
-            r += in ? rg[u] : 0.0f;
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t gi = b + 64u * u + ln;
+                rg[u] = gi < S ? X.rest64[gi] : 0.0f;
+                sg[u] = gi < S ? X.sg64[gi] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                e = __builtin_fmaf(rg[u] > 0.0f ? sg[u] : 0.0f, sg[u], e);
+                r += rg[u];
+            }
         }
     }
     e = group_sum<64>(e);
