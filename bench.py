@@ -9,7 +9,9 @@ weight copies, with x and y resident in HBM.  The `--steps` launches are
 recorded into a HIP graph and replayed; HIP events on the launch stream
 bracket the replay (after `--warmup` untimed launches and UNTIMED_REPLAYS
 untimed replays, which let the clocks and the graph's first-launch work
-settle).  With fewer steps than copies, the calls over the remaining copies
+settle; the timed replay is queued behind one more untimed graph, so the
+start event is not stamped while the host is still submitting the graph to
+an idle GPU).  With fewer steps than copies, the calls over the remaining copies
 run untimed before each replay (rotation_time_us), so at any --steps every
 timed call reads weights that >= 768 MB of other reads have pushed out of the
 256 MB Infinity Cache; each result reports its copies, timed launches and the
@@ -345,6 +347,7 @@ def bench_chain(ctx, steps: int, warmup: int) -> dict:
         g = ch.capture(stream, fused)
         g.launch(stream)
         stream.synchronize()
+        g.launch(stream)  # untimed: the timed replays queue behind it (rotation_time_us)
         e0.record(stream)
         for _ in range(steps):
             g.launch(stream)
@@ -395,10 +398,13 @@ def rotation_time_us(ctx, stream, enc, steps: int, copies: int) -> float:
         if flush:
             flush.launch(stream)
         timed.launch(stream)
-    if flush:
-        flush.launch(stream)
     stream.synchronize()
+    # The timed replay is queued behind untimed work (the flush graph, or one
+    # more replay of the timed graph, which leaves the cache as cold as the
+    # replays above), so the start event is stamped when the GPU reaches it and
+    # not while the host is still submitting the graph to an idle GPU.
     e0, e1 = ctx.event(), ctx.event()
+    (flush or timed).launch(stream)
     e0.record(stream)
     timed.launch(stream)
     e1.record(stream)
@@ -434,6 +440,7 @@ def _graph_time_us(ctx, stream, enc, steps: int) -> float:
         g.launch(stream)
     stream.synchronize()
     e0, e1 = ctx.event(), ctx.event()
+    g.launch(stream)  # untimed: the timed replay queues behind it (rotation_time_us)
     e0.record(stream)
     g.launch(stream)
     e1.record(stream)
