@@ -1,6 +1,7 @@
 """CU-resident GEMV family (K % 256 == 0; Q4_K rows up to 16384 weights, Q8_0
 and Q6_K rows up to 4096, longer rows of those fall back to the lane-group
-family):
+family; Q6_K rows of 4096 < K <= 16384 run here on the default dispatch, whose
+K-sliced CU-resident kernels take them):
 the GEMV parity bar of the other kernels (relative L2 <= 1e-3 against the CPU
 oracle, the reference test's absolute 1e-4 on its case, exact one-hot
 columns, batched equal to per-token) with the family forced on for every
@@ -61,14 +62,18 @@ SHAPES = [(1, 256), (7, 1024), (100, 2048), (333, 3072), (1000, 4096), (64, 5120
 ROLLED = [(28672, 4096), (151936, 1024), (140000, 256)]
 
 
+def _family(cu_gemv, gemv, fmt, K):
+    """The forced whole-row family, or for Q6_K rows beyond 4096 weights (which
+    it does not cover) the default dispatch's K-sliced kernels."""
+    return gemv if fmt == "q6_k" and K > 4096 else cu_gemv
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M,K", SHAPES)
-def test_cu_family_matches_oracle(cu_gemv, fmt, M, K):
-    if fmt == "q6_k" and K > 4096:
-        pytest.skip("Q6_K rows above 4096 weights take the lane-group family")
+def test_cu_family_matches_oracle(cu_gemv, gemv, fmt, M, K):
     W = synth.weights(fmt, synth.seed(80, M % 97), M, K, **DSCALE[fmt])
     x = synth.normal_f32(synth.seed(80, 200 + K % 89), K)
-    y = getattr(cu_gemv, EXEC[fmt])(W, x, M, K)
+    y = getattr(_family(cu_gemv, gemv, fmt, K), EXEC[fmt])(W, x, M, K)
     exp = ref.gemv(fmt, W, x, M, K, threads=ref.max_threads())
     assert rel_l2(y, exp) < TOL
 
@@ -95,9 +100,8 @@ def test_cu_family_reference_q4k_case(cu_gemv):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("K", [1024, 4096, 8192])
-def test_cu_family_one_hot_columns(cu_gemv, fmt, K):
-    if fmt == "q6_k" and K > 4096:
-        pytest.skip("Q6_K rows above 4096 weights take the lane-group family")
+def test_cu_family_one_hot_columns(cu_gemv, gemv, fmt, K):
+    cu_gemv = _family(cu_gemv, gemv, fmt, K)
     M = 40
     W = synth.weights(fmt, synth.seed(81, 0), M, K, **DSCALE[fmt])
     cols = rn.weights_f32(fmt, W, M, K)
@@ -110,9 +114,8 @@ def test_cu_family_one_hot_columns(cu_gemv, fmt, K):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M,K,T", [(300, 1024, 5), (1000, 4096, 3), (77, 8192, 2)])
-def test_cu_family_batched_equals_per_token(cu_gemv, fmt, M, K, T):
-    if fmt == "q6_k" and K > 4096:
-        pytest.skip("Q6_K rows above 4096 weights take the lane-group family")
+def test_cu_family_batched_equals_per_token(cu_gemv, gemv, fmt, M, K, T):
+    cu_gemv = _family(cu_gemv, gemv, fmt, K)
     W = synth.weights(fmt, synth.seed(82, 0), M, K, **DSCALE[fmt])
     x = synth.normal_f32(synth.seed(82, 1), T * K)
     yb = getattr(cu_gemv, EXEC_B[fmt])(W, x, T, M, K).reshape(T, M)
