@@ -868,8 +868,9 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[f][i][r] = 0.0f;
-    // raw bytes of row 32 R wave + 32 f + l32 for `chunk` from its stage
-    auto rawW = [&](uint32_t chunk, int f, WRaw &r) {
+    // raw bytes of row 32 R wave + 32 f + l32 for `chunk` from its stage (sh =
+    // chunk % 4, a constant at every call: the chunk loop is unrolled by 4)
+    auto rawW = [&](uint32_t chunk, uint32_t sh, int f, WRaw &r) {
         const uint32_t rr = 32u * R * wave + 32u * (uint32_t)f + l32;
         const uint8_t *row = wsm + (chunk % G::NW) * G::WSTAGE + rr * G::WROWB;
         if (Q4K) {
@@ -877,12 +878,17 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
             r.b = *(const u32x4 *)(row + 16u * h);
             r.c = 0;
         } else {
-            // blocks 2 chunk + h start at window byte 4 (chunk % 4) + 34 h; the
-            // 4-byte-aligned 36-byte window dequant_w expects starts at 4 (chunk % 4) + 32 h
-            const uint32_t *p = (const uint32_t *)(row + 4u * (chunk & 3u) + 32u * h);
-            r.a = u32x4{p[0], p[1], p[2], p[3]};
-            r.b = u32x4{p[4], p[5], p[6], p[7]};
-            r.c = p[8];
+            // blocks 2 chunk + h start at window byte 4 sh + 34 h; the 4-byte-aligned
+            // 36-byte window dequant_w expects is dwords sh .. sh + 8 of the three
+            // aligned 16-byte granules 2h .. 2h + 2, read whole: rows 80 bytes
+            // apart put the 16 lanes of each read pass on distinct banks, where
+            // dword reads of the window hit 16 of the 64 banks (4-way conflicts)
+            const u32x4 *gp = (const u32x4 *)__builtin_assume_aligned(row + 32u * h, 16);
+            const u32x4 g0 = gp[0], g1 = gp[1], g2 = gp[2];
+            const uint32_t gd[12] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w, g2.x, g2.y, g2.z, g2.w};
+            r.a = u32x4{gd[sh], gd[sh + 1], gd[sh + 2], gd[sh + 3]};
+            r.b = u32x4{gd[sh + 4], gd[sh + 5], gd[sh + 6], gd[sh + 7]};
+            r.c = gd[sh + 8];
         }
     };
     auto readA = [&](uint32_t chunk, int s, bf16x8 (&a)[4]) {
@@ -904,18 +910,19 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
 #pragma unroll
     for (int f = 0; f < R; ++f) {
         WRaw r0;
-        rawW(0u, f, r0);
+        rawW(0u, 0u, f, r0);
         const DqScale q0 = dq_scale<Q4K>(r0, 0u, h);
 #pragma unroll
         for (int s = 0; s < 4; ++s) dq_step<Q4K>(r0, q0, h, s, &wd[0][f][4 * s]);
-        rawW(1u, f, rw[0][f]);
+        rawW(1u, 1u, f, rw[0][f]);
     }
     readA(0u, 0, a[0]);
-    for (uint32_t c = 0; c < NC; c += 2u) {
+    for (uint32_t c = 0; c < NC; c += 4u) {
 #pragma unroll
-        for (int P = 0; P < 2; ++P) {
-            const uint32_t cc = c + (uint32_t)P;
-            // NC is even (K % 256 == 0), so cc < NC on both halves
+        for (int Q = 0; Q < 4; ++Q) {
+            const int P = Q & 1;
+            const uint32_t cc = c + (uint32_t)Q;
+            // NC is a multiple of 4 (K % 256 == 0), so cc < NC in every quarter
             gemml_barrier();  // X chunk cc + 1 and weight chunk cc + 2 are in
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
@@ -924,7 +931,7 @@ ER_DEV void gemm_ls(const uint8_t *__restrict__ W, const uint16_t *__restrict__ 
                 } else {
                     readA(cc + 1u, 0, a[0]);
 #pragma unroll
-                    for (int f = 0; f < R; ++f) rawW(cc + 2u, f, rw[P ^ 1][f]);
+                    for (int f = 0; f < R; ++f) rawW(cc + 2u, (uint32_t)((Q + 2) & 3), f, rw[P ^ 1][f]);
                 }
                 if (s == 0) {
 #pragma unroll
