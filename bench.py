@@ -467,8 +467,9 @@ def bench_ceilings(ctx, steps: int) -> dict:
         64 / 128 / 256 resident workgroups: (time of 200 rounds - time of 0
         rounds) / 200, each one launch bracketed by events;
       - per-CU rates behind the prefill GEMM: LDS reads (A-fragment layout)
-        with 4 / 8 / 16 waves per CU, and bf16 MFMA / fp32 FMA overlap within
-        one wave and across two waves of a SIMD (best of 3 launches each)."""
+        with 4 / 8 / 16 waves per CU, bf16 MFMA / fp32 FMA overlap within
+        one wave and across two waves of a SIMD, and int8 MFMAs alone and with
+        a Q8_0 per-block rescale each (best of 3 launches each)."""
     pctx = probe_context(ctx)
     lib = pctx.lib
     _check = pctx.check
@@ -542,6 +543,17 @@ def bench_ceilings(ctx, steps: int) -> dict:
         us = timed(lambda: _check(lib.er_hip_probe_mfma_valu(pctx.handle, stream.handle, mode, iters, sink.raw)))
         out[f"overlap_{tag}"] = {"us": us, "ns_per_iteration": us * 1000.0 / iters, "iters": iters}
         log(f"overlap {tag}: {us * 1000.0 / iters:.1f} ns per iteration (8 MFMA and/or 64 FMA per wave)")
+    # int8 MFMAs for the Q8_0 prefill: alone, and each with the per-block
+    # rescale of its int32 sums; the second prices the inner loop of such a
+    # kernel at 512x14336x4096 (T/32 * N/32 * K/32 MFMAs over 4 SIMDs per CU)
+    n_i8 = (512 // 32) * (14336 // 32) * (4096 // 32) / (4 * ctx.compute_units)
+    for mode, tag in ((4, "i8_mfma_alone"), (5, "i8_mfma_with_block_rescale")):
+        us = timed(lambda: _check(lib.er_hip_probe_mfma_valu(pctx.handle, stream.handle, mode, iters, sink.raw)))
+        ns = us * 1000.0 / iters
+        out[f"overlap_{tag}"] = {"us": us, "ns_per_iteration": ns, "iters": iters,
+                                 "us_for_512x14336x4096": n_i8 * ns / 8 / 1000.0}
+        log(f"overlap {tag}: {ns:.1f} ns per iteration (8 int8 MFMA per wave), "
+            f"{n_i8 * ns / 8 / 1000.0:.1f} us of such iterations for Q8_0 512x14336x4096")
     sink.free()
     e0.destroy()
     e1.destroy()

@@ -1935,8 +1935,8 @@ er_status er_hip_probe_lds_read(er_hip_ctx *ctx, er_stream stream, uint32_t wave
 er_status er_hip_probe_mfma_valu(er_hip_ctx *ctx, er_stream stream, uint32_t mode, uint32_t iters, er_buffer sink) {
     er_status st = check_ctx(ctx);
     if (st != ER_OK) return st;
-    if (mode > 3u || !sink.data || !aligned(sink.data, 4) || sink.length < (uint64_t)ctx->cu_count * 512u * 4u)
-        return fail(ER_ERR_INVALID_ARGUMENT, "mfma/valu probe: mode %u (0..3), sink %llu bytes", mode,
+    if (mode > 5u || !sink.data || !aligned(sink.data, 4) || sink.length < (uint64_t)ctx->cu_count * 512u * 4u)
+        return fail(ER_ERR_INVALID_ARGUMENT, "mfma/valu probe: mode %u (0..5), sink %llu bytes", mode,
                     (unsigned long long)sink.length);
     st = bind_device(ctx);
     if (st != ER_OK) return st;

@@ -53,7 +53,10 @@ er_status er_hip_probe_lds_read(er_hip_ctx *ctx, er_stream stream, uint32_t wave
 /* Matrix-core / vector-ALU overlap: one 8-wave workgroup per CU, `iters`
  * iterations of 8 bf16 MFMAs and/or 64 fp32 FMAs per wave; mode 0 MFMA
  * alone, 1 FMAs alone, 2 both from different waves of each SIMD, 3 both
- * interleaved in one wave; sink holds CU count * 512 uint32. */
+ * interleaved in one wave; 4 and 5: 8 int8 MFMAs (32x32x32) per iteration
+ * on waves 0-3, alone (4) or each followed by the per-block rescale of its 16
+ * int32 sums per lane (5: convert, scale product, fused multiply-add);
+ * sink holds CU count * 512 uint32. */
 er_status er_hip_probe_mfma_valu(er_hip_ctx *ctx, er_stream stream, uint32_t mode, uint32_t iters, er_buffer sink);
 
 #ifdef __cplusplus

@@ -65,6 +65,8 @@ extern "C" __global__ void __launch_bounds__(64)
 // ---------------------------------------------------------------------------
 typedef __bf16 pb_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pb_f32x16 __attribute__((ext_vector_type(16)));
+typedef int pb_i32x4 __attribute__((ext_vector_type(4)));
+typedef int pb_i32x16 __attribute__((ext_vector_type(16)));
 
 // LDS read rate: every wave issues, per iteration, 8 independent 16-byte-per-
 // lane reads laid out like the GEMM's A fragments (lane l: row l % 32 of a
@@ -95,51 +97,121 @@ extern "C" __global__ void __launch_bounds__(1024)
 // FMAs).  mode: 0 waves 0-3 MFMA, 4-7 idle; 1 waves 0-3 VALU; 2 waves 0-3
 // MFMA and 4-7 VALU (the two on each SIMD from different waves); 3 waves 0-3
 // BOTH (from one wave).
+//
+// Modes 4 and 5 price an int8 path for the Q8_0 prefill GEMM: waves 0-3 issue
+// 8 v_mfma_i32_32x32x32_i8 per iteration (one MFMA spans exactly one 32-wide
+// Q8_0 block of K).  Mode 4 runs them alone.  Mode 5 gives each one the
+// per-block rescale such a kernel cannot avoid: the block's int32 sums differ
+// in scale per output (weight row n, token t), so each of a lane's 16 sums
+// takes a convert, the product of the two block scales and a fused
+// multiply-add into an fp32 accumulator (48 vector instructions per MFMA).
 extern "C" __global__ void __launch_bounds__(512)
     er_probe_mfma_valu(uint32_t mode, uint32_t iters, uint32_t never, uint32_t *__restrict__ sink) {
     const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t role = wave < 4u ? (mode == 1u ? 2u : mode == 3u ? 3u : 1u) : (mode == 2u ? 2u : 0u);
-    pb_f32x16 acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) acc[j][q] = 0.0f;
-    pb_bf16x8 a, b;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        a[q] = (__bf16)(float)(tid + q);
-        b[q] = (__bf16)(float)(3 * q);
-    }
+    const uint32_t role = wave < 4u ? (mode == 1u ? 2u : mode == 3u ? 3u : mode >= 4u ? mode : 1u)
+                                    : (mode == 2u ? 2u : 0u);
+    // every role keeps its accumulators inside its own branch, so no role
+    // holds another's registers
     float y[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) y[k] = (float)(tid + k);
     const float m = 1.0001f, c = 0.5f;
-    if (role == 1u) {
-        for (uint32_t it = 0; it < iters; ++it)
+    float s = 0.0f;
+    if (role == 1u || role == 3u) {
+        pb_f32x16 acc[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[j][q] = 0.0f;
+        pb_bf16x8 a, b;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            a[q] = (__bf16)(float)(tid + q);
+            b[q] = (__bf16)(float)(3 * q);
+        }
+        if (role == 1u) {
+            for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+        } else {
+            for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) y[k] = __builtin_fmaf(y[k], m, c);
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) s += acc[j][q];
     } else if (role == 2u) {
         for (uint32_t it = 0; it < iters; ++it)
 #pragma unroll
             for (int r = 0; r < 8; ++r)
 #pragma unroll
                 for (int k = 0; k < 8; ++k) y[k] = __builtin_fmaf(y[k], m, c);
-    } else if (role == 3u) {
-        for (uint32_t it = 0; it < iters; ++it)
+    } else if (role >= 4u) {
+        const pb_i32x4 ia = {(int)(tid * 0x01030507u), (int)(tid ^ 0x7f3a1c05u), 0x05f3a1c7, (int)tid};
+        const pb_i32x4 ib = {0x11223344, (int)(tid * 0x9e3779b1u), 0x7c0d5a13, 0x2468ace0};
+        if (role == 4u) {
+            pb_i32x16 iacc[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+            for (int j = 0; j < 8; ++j)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) y[k] = __builtin_fmaf(y[k], m, c);
-            }
+                for (int q = 0; q < 16; ++q) iacc[j][q] = 0;
+            for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) iacc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ia, ib, iacc[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) s += (float)iacc[j][q];
+        } else {
+            // per-token block scales in registers (a kernel would read them
+            // from LDS); one weight-block scale per accumulator, changing
+            // every iteration like the block index does
+            pb_f32x16 acc[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[j][q] = 0.0f;
+            float sx[16], sw[8];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) sx[q] = 1.0f + (float)(tid + q) * 1e-6f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sw[j] = 1.0f + (float)(tid * 8u + j) * 1e-7f;
+            const pb_i32x16 zero = {};
+            pb_i32x4 ja = ia;
+            // software-pipelined as a kernel would run it: the next block's
+            // MFMA is issued before the previous block's sums are rescaled,
+            // into other registers, so the two overlap
+            pb_i32x16 r = __builtin_amdgcn_mfma_i32_32x32x32_i8(ja, ib, zero, 0, 0, 0);
+            for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    // an opaque operand, so each product is issued (not one
+                    // hoisted out of the loop for all)
+                    asm volatile("" : "+v"(ja));
+                    const pb_i32x16 rn = __builtin_amdgcn_mfma_i32_32x32x32_i8(ja, ib, zero, 0, 0, 0);
+                    sw[j] *= m;
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) acc[j][q] = __builtin_fmaf((float)r[q], sw[j] * sx[q], acc[j][q]);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 49, 0);
+                    r = rn;
+                }
+#pragma unroll
+            for (int q = 0; q < 16; ++q) s += (float)r[q];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) s += acc[j][q];
+        }
     }
-    float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) s += y[k];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) s += acc[j][q];
     const uint32_t v = __builtin_bit_cast(uint32_t, s);
     if (v == never) sink[blockIdx.x * 512u + tid] = v;
 }
