@@ -135,6 +135,7 @@ template <int LPR, int NS, int R, int EPI, class RowAt>
 ER_DEV void gemv_q4k_i8_core(const uint8_t *const (&rowp)[R], float *const (&yrow)[R], const bool (&rowLive)[R],
                              const float *__restrict__ x, uint32_t K, RowAt rowAt) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    __shared__ float4 chkw[ER_GEMV_WAVES];  // the waves' shares of the launch's checks
     using C = I8Cfg<LPR, NS>;
     constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
     const uint32_t lane = threadIdx.x & 63u;
@@ -158,8 +159,13 @@ ER_DEV void gemv_q4k_i8_core(const uint8_t *const (&rowp)[R], float *const (&yro
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    xl_store<C::XG, NT>(lds, K, xr);
-    xl_store_tail<C::XG, NT>(x, lds, K);
+    XlCheck ck;
+    xl_store<C::XG, NT>(lds, K, xr, &ck);
+    xl_store_tail<C::XG, NT>(x, lds, K, &ck);
+    {  // this wave's share of the launch's checks, gathered by the conversion
+        const float4 sh = xl_check_share(ck);
+        if ((threadIdx.x & 63u) == 0) chkw[threadIdx.x >> 6] = sh;
+    }
     __syncthreads();
 
     const XLimbs X = xl_view(lds, K);
@@ -186,8 +192,9 @@ ER_DEV void gemv_q4k_i8_core(const uint8_t *const (&rowp)[R], float *const (&yro
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    const bool ill = xl_ill(X, 4.0f);
-    if (ill || nf_any_chunk(X.x16, K >> 4)) {
+    bool ill, nfx;
+    xl_check_decide(chkw, ER_GEMV_WAVES, 4.0f, ill, nfx);
+    if (ill || nfx) {
         float sp[R], hits = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sp[r] = 0.0f;
@@ -370,6 +377,7 @@ template <int LPR, int NS, int R>
 ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict__ x,
                          float *__restrict__ y, uint32_t M, uint32_t K) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    __shared__ float4 chkw[ER_GEMV_WAVES];  // the waves' shares of the launch's checks
     using C = I8Cfg<LPR, NS>;
     constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
     x += (size_t)blockIdx.y * K;
@@ -393,8 +401,13 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
             w[j][r] = q8_slot_load(W + (size_t)min(row0 + (uint32_t)r, M - 1u) * rowBytes + (size_t)s * 68u);
     }
     __builtin_amdgcn_sched_barrier(0);
-    xl_store<C::XG, NT>(lds, K, xr);
-    xl_store_tail<C::XG, NT>(x, lds, K);
+    XlCheck ck;
+    xl_store<C::XG, NT>(lds, K, xr, &ck);
+    xl_store_tail<C::XG, NT>(x, lds, K, &ck);
+    {  // this wave's share of the launch's checks, gathered by the conversion
+        const float4 sh = xl_check_share(ck);
+        if ((threadIdx.x & 63u) == 0) chkw[threadIdx.x >> 6] = sh;
+    }
     __syncthreads();
 
     const XLimbs X = xl_view(lds, K);
@@ -416,8 +429,9 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    const bool ill = xl_ill(X, 1.0f);
-    if (ill || nf_any_chunk(X.x16, K >> 4)) {
+    bool ill, nfx;
+    xl_check_decide(chkw, ER_GEMV_WAVES, 1.0f, ill, nfx);
+    if (ill || nfx) {
         float sp[R], hits = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sp[r] = 0.0f;
@@ -466,6 +480,7 @@ ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const
                                     const float *__restrict__ normW, float eps, uint32_t K, RowAt rowAt) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     __shared__ float red[ER_GEMV_WAVES];
+    __shared__ float4 chkw[ER_GEMV_WAVES];  // the waves' shares of the launch's checks
     using C = I8Cfg<LPR, NS>;
     constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -511,7 +526,12 @@ ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const
                 xr[c][q].w = xr[c][q].w * rms * wr[c][q].w;
             }
     }
-    xl_store<C::XG, NT>(lds, K, xr);
+    XlCheck ck;
+    xl_store<C::XG, NT>(lds, K, xr, &ck);
+    {  // this wave's share of the launch's checks, gathered by the conversion
+        const float4 sh = xl_check_share(ck);
+        if ((threadIdx.x & 63u) == 0) chkw[threadIdx.x >> 6] = sh;
+    }
     __syncthreads();
 
     const XLimbs X = xl_view(lds, K);
@@ -533,8 +553,9 @@ ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    const bool ill = xl_ill(X, 1.0f);
-    if (ill || nf_any_chunk(X.x16, C16)) {
+    bool ill, nfx;
+    xl_check_decide(chkw, ER_GEMV_WAVES, 1.0f, ill, nfx);
+    if (ill || nfx) {
         // the staged values: x, or x * rms * normW as the prologue formed them
         // (rms recomputed from the same wave sums, so it is the same value)
         float rms = 1.0f;
@@ -808,6 +829,7 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
                         float *__restrict__ y, uint32_t M, uint32_t K,
                         float *__restrict__ pv = nullptr, uint32_t *__restrict__ pi = nullptr) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    __shared__ float4 chkw[ER_GEMV_WAVES];  // the waves' shares of the launch's checks
     using C = I8Cfg<LPR, NS>;
     constexpr uint32_t NT = 64u * ER_GEMV_WAVES;
     x += (size_t)blockIdx.y * K;
@@ -840,8 +862,13 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    xl_store<C::XG, NT>(lds, K, xr);
-    xl_store_tail<C::XG, NT>(x, lds, K);
+    XlCheck ck;
+    xl_store<C::XG, NT>(lds, K, xr, &ck);
+    xl_store_tail<C::XG, NT>(x, lds, K, &ck);
+    {  // this wave's share of the launch's checks, gathered by the conversion
+        const float4 sh = xl_check_share(ck);
+        if ((threadIdx.x & 63u) == 0) chkw[threadIdx.x >> 6] = sh;
+    }
     __syncthreads();
 
     const XLimbs X = xl_view(lds, K);
@@ -902,8 +929,9 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    const bool ill = xl_ill(X, 4.0f);
-    if (ill || nf_any_chunk(X.x16, K >> 4)) {
+    bool ill, nfx;
+    xl_check_decide(chkw, ER_GEMV_WAVES, 4.0f, ill, nfx);
+    if (ill || nfx) {
         float sp[R], hits = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; ++r) sp[r] = 0.0f;
@@ -1131,7 +1159,8 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
                     uint32_t M, uint32_t K, uint32_t rowsPerWg, float *__restrict__ pv = nullptr,
                     uint32_t *__restrict__ pi = nullptr) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-    __shared__ uint32_t staged;  // staging waves done
+    __shared__ uint32_t staged;               // staging waves done
+    __shared__ float4 chkw[ER_CU_WAVES];      // [staging wave] its share of the launch's checks
     constexpr uint32_t G = 64u / LPR;
     constexpr uint32_t STEP = ER_CU_WAVES * G;  // rows per workgroup step
     constexpr int NPARK = JC > 0 ? (JC + LPR - 1) / LPR : 64 / LPR;
@@ -1213,6 +1242,7 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
             __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's x pieces are in LDS
         }
         __builtin_amdgcn_sched_barrier(0);
+        XlCheck ck;
         if (halfBlocks) {
             for (uint32_t b = si; b < nBlocks; b += STG) {
                 const uint32_t t = 64u * b + lane;  // 8-value half-chunk; lanes 8k..8k+7 hold one 64-group
@@ -1220,7 +1250,7 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
                 float4 xr[2];
 #pragma unroll
                 for (int q = 0; q < 2; ++q) xr[q] = *(const float4 *)(xraw + 8u * tc + 4u * q);
-                xl_store_half(lds, K, xr, t);  // stores only half-chunks t < K / 8
+                xl_store_half(lds, K, xr, t, &ck);  // stores only half-chunks t < K / 8
             }
         } else {
             for (uint32_t b = si; b < nBlocks; b += STG) {
@@ -1229,12 +1259,17 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
                 float4 xr[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) xr[q] = *(const float4 *)(xraw + 16u * tc + 4u * q);
-                xl_store_chunk(lds, K, xr, t);  // stores only chunks t < K / 16
+                xl_store_chunk(lds, K, xr, t, &ck);  // stores only chunks t < K / 16
             }
         }
-        // publish this wave's limb stores: a release fence on LDS alone (it waits
-        // for the LDS stores, lgkmcnt(0), not for the weight loads in flight,
-        // which a release on every address space would drain first)
+        {  // this staging wave's share of the launch's checks, gathered by the conversion
+            const float4 sh = xl_check_share(ck);
+            if (lane == 0) chkw[si] = sh;
+        }
+        // publish this wave's limb stores and check share: a release fence on
+        // LDS alone (it waits for the LDS stores, lgkmcnt(0), not for the
+        // weight loads in flight, which a release on every address space would
+        // drain first)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         if (lane == 0) __hip_atomic_fetch_add(&staged, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if constexpr (!EARLY) prologue();
@@ -1302,7 +1337,8 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) step(i0, u, true);
-    const bool ill = xl_ill(X, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f);
+    bool ill, nfx;
+    xl_check_decide(chkw, (int)STG, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f, ill, nfx);
     if (ill) {
         // x the limbs do not carry precisely enough: every row of this lane
         // group again, in fp32 over every position from the raw weights, the
@@ -1318,7 +1354,7 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
 #pragma unroll
             for (int q = 0; q < NPARK; ++q) res[q] = (li == st % LPR && (uint32_t)q == st / LPR) ? v : res[q];
         }
-    } else if (nf_any_chunk(X.x16, K >> 4)) {
+    } else if (nfx) {
         // each lane redoes its own parked rows over every chunk; raw x is in LDS
         float sp[NPARK], hits = 0.0f;
 #pragma unroll
@@ -1390,6 +1426,7 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     constexpr uint32_t LPR = 64u / PAR;  // lanes per row slice
     __shared__ float part[ER_CU_WAVES][PAR * J];  // [wave][local row PAR j + g]
+    __shared__ float4 chk[ER_CU_WAVES];           // [wave] its slice's checks: e, r, non-finite
     __shared__ float tv[TOP1 ? PAR * J : 1];      // top-1: the workgroup's row values
     static_assert(PAR == 2 || PAR == 4 || PAR == 8, "2, 4 or 8 rows per step");
     static_assert(J >= 1 && J <= (int)LPR && J <= ER_CUK_MAX_STEPS, "row sums parked one per lane of a slice");
@@ -1412,6 +1449,7 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
     };
     const size_t rowBytes = F::row_bytes(K);
     float res = 0.0f;
+    float4 share = float4{0.0f, 0.0f, 0.0f, 0.0f};  // this wave's share of the launch's checks
     if (s0 < S) {
         const uint32_t s = s0 + li;
         const uint32_t sc = min(s, s1 - 1u);
@@ -1442,14 +1480,16 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
         // convert the slice (pieces past it are not stored: index K / VPL).
         // Every pass runs: a pass under a branch had its x loads sunk behind
         // the weight loads, and the conversion then waited for those too.
+        XlCheck ck;
 #pragma unroll
         for (int p = 0; p < NPASS; ++p) {
             const uint32_t hc = h0 + 64u * p + lane;
             if constexpr (VPL == 16)
-                xl_store_chunk(lds, K, xr[p], hc < h1 ? hc : K >> 4);
+                xl_store_chunk(lds, K, xr[p], hc < h1 ? hc : K >> 4, &ck);
             else
-                xl_store_half(lds, K, xr[p], hc < h1 ? hc : K >> 3);
+                xl_store_half(lds, K, xr[p], hc < h1 ? hc : K >> 3, &ck);
         }
+        share = xl_check_share(ck);
         // the wave reads back only what it stored; its LDS accesses run in order
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_sched_barrier(0);
@@ -1468,10 +1508,11 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
         }
     }
     if (li < (uint32_t)J) part[wave][PAR * li + g] = res;
-    __syncthreads();  // every wave's partials, limbs, chunk sums and scales are in LDS
+    if (lane == 0) chk[wave] = share;
+    __syncthreads();  // every wave's partials and check shares, limbs, chunk sums and scales are in LDS
     const XLimbs X = xl_view(lds, K);
-    const bool ill = xl_ill(X, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f);
-    const bool nf = !ill && nf_any_chunk(X.x16, K >> 4);
+    bool ill, nf;
+    xl_check_decide(chk, ER_CU_WAVES, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f, ill, nf);
     // lane group (wave, g) finishes steps wave, wave + 8, ..., row g
 #pragma unroll 1
     for (uint32_t st = wave; st < (uint32_t)J; st += ER_CU_WAVES) {

@@ -14,11 +14,12 @@
 // non-finite value has no limbs), so after its rows are computed each kernel
 // checks whether its x held a non-finite value and, only then, replaces every
 // row value by the sum above, evaluated from the raw weight bytes with the
-// reference's dequantisation.  The check is a wave-wide scan of the staged
-// fp32 chunk sums x16 (a sum of 16 values is non-finite exactly when one of
-// them is, or when finite values overflow it; the slow path finds the values
-// themselves, so an overflow alone changes nothing).  It runs after the
-// weight loads are consumed and costs K/1024 LDS reads per lane.
+// reference's dequantisation.  The check looks at the fp32 chunk sums (a sum
+// of 16 values is non-finite exactly when one of them is, or when finite
+// values overflow it; the slow path finds the values themselves, so an
+// overflow alone changes nothing): the x conversion notes a non-finite chunk
+// sum as it forms each one (XlCheck, er_xlimbs.h), so the decision at the end
+// of the launch reads one share per wave instead of scanning x again.
 #pragma once
 
 #include "er_common.h"
@@ -65,38 +66,6 @@ ER_DEV float weight_at(const uint8_t *row, uint32_t k) {
     if constexpr (FMT == ER_FMT_Q8_0) return q8_0_weight_at(row, k);
     else if constexpr (FMT == ER_FMT_Q4_K) return q4k_weight_at(row, k);
     else return q6k_weight_at(row, k);
-}
-
-// Wave-uniform: does any of the C16 chunk sums hold a non-finite value?
-// Up to 256 chunks (K <= 4096) one read per lane per 64 chunks.  Longer rows
-// (x16 16-byte aligned, C16 % 4 == 0) read up to four 16-byte pieces per lane
-// per 1024 chunks, all issued before one wait: one value per read waited ~100
-// cycles per 64 chunks, ~1 us at K = 14336.  (The 16-byte form measured
-// ~0.3 us slower on rows of 1024 weights, so short rows keep the first.)
-ER_DEV bool nf_any_chunk(const float *x16, uint32_t C16) {
-    const uint32_t ln = lane_id();
-    bool f = false;
-    if (C16 <= 256u) {
-#pragma unroll 1
-        for (uint32_t c = ln; c < C16; c += 64u) f |= !__builtin_isfinite(x16[c]);
-        return __builtin_amdgcn_ballot_w64(f) != 0;
-    }
-    const float4 *v = (const float4 *)__builtin_assume_aligned(x16, 16);
-    const uint32_t n4 = C16 >> 2;
-#pragma unroll 1
-    for (uint32_t b = 0; b < n4; b += 256u) {
-        float4 q[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t i = b + 64u * u + ln;
-            q[u] = i < n4 ? v[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            f |= !(__builtin_isfinite(q[u].x) && __builtin_isfinite(q[u].y) && __builtin_isfinite(q[u].z) &&
-                   __builtin_isfinite(q[u].w));
-    }
-    return __builtin_amdgcn_ballot_w64(f) != 0;
 }
 
 // Wave-uniform: does any of the K values (K % 4 == 0, 16-byte aligned) hold a

@@ -55,7 +55,7 @@ ER_DEV uint32_t xl_gswz(uint32_t G) { return G ^ ((G >> 3) & 3u); }
 ER_DEV uint32_t xl_lds_bytes(uint32_t K) { return ER_XL_PLANES * K + (K / 16u) * 4u + (K / 64u) * 8u; }
 
 // 2^-24: the launch takes the fp32 path when its limbs' error energy exceeds
-// this fraction of the energy they carry well (xl_ill)
+// this fraction of the energy they carry well (xl_ill_rule)
 #define ER_XL_EPS2 5.9604645e-08f
 
 struct XLimbs {
@@ -76,41 +76,41 @@ ER_DEV XLimbs xl_view(const uint32_t *lds, uint32_t K) {
     return v;
 }
 
-// Wave-uniform: does the staged x call for the fp32 path (the conditioning
-// rule above; f the format's factor)?  Every wave computes it from the same
-// LDS values in the same order, so all agree.
-// Each lane sums groups lane, lane + 64, ... in that order; beyond 64 groups
-// the reads of four of them are issued before one wait (groups past the last
-// are skipped and add exact zeros), as in nf_any_chunk.
-ER_DEV bool xl_ill(const XLimbs &X, float f) {
+// The conditioning rule on its two sums: e adds s_g^2 over the groups that
+// carry energy outside their maximum's lanes, r adds that energy.
+ER_DEV bool xl_ill_rule(float e, float r, float f) { return f * (64.0f / 12.0f) * e > ER_XL_EPS2 * r; }
+
+// The launch's end-of-launch checks, gathered while x is converted: each lane
+// adds, over the chunks it converts, the conditioning sums of xl_ill_rule
+// (e: s_g^2 of each group with energy outside its maximum's lanes, r: that
+// energy; a group counts once, at its first chunk) and whether a chunk sum is
+// non-finite.  xl_check_share reduces a wave's lanes; xl_check_decide adds the
+// waves' shares in wave order.  Every workgroup of a launch converts the same
+// chunks in the same lanes, so all reach the same decisions.
+struct XlCheck {
     float e = 0.0f, r = 0.0f;
-    const uint32_t S = X.K >> 6, ln = lane_id();
-    if (S <= 64u) {
-        if (ln < S) {
-            const float rg = X.rest64[ln], sg = X.sg64[ln];
-            e = __builtin_fmaf(rg > 0.0f ? sg : 0.0f, sg, e);
-            r += rg;
-        }
-    } else {
-#pragma unroll 1
-        for (uint32_t b = 0; b < S; b += 256u) {
-            float rg[4], sg[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t gi = b + 64u * u + ln;
-                rg[u] = gi < S ? X.rest64[gi] : 0.0f;
-                sg[u] = gi < S ? X.sg64[gi] : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                e = __builtin_fmaf(rg[u] > 0.0f ? sg[u] : 0.0f, sg[u], e);
-                r += rg[u];
-            }
-        }
+    bool nf = false;
+};
+
+// Wave-uniform: this wave's share {e, r, 1 if a chunk sum was non-finite, 0}.
+ER_DEV float4 xl_check_share(const XlCheck &c) {
+    return float4{group_sum<64>(c.e), group_sum<64>(c.r), __builtin_amdgcn_ballot_w64(c.nf) != 0 ? 1.0f : 0.0f,
+                  0.0f};
+}
+
+// The decisions from n wave shares (f: the format's factor of xl_ill_rule):
+// ill -- the fp32 path for every row; nf -- the non-finite path (only when
+// not ill).
+ER_DEV void xl_check_decide(const float4 *share, int n, float f, bool &ill, bool &nf) {
+    float e = 0.0f, r = 0.0f, bad = 0.0f;
+    for (int w = 0; w < n; ++w) {
+        const float4 c = share[w];
+        e += c.x;
+        r += c.y;
+        bad += c.z;
     }
-    e = group_sum<64>(e);
-    r = group_sum<64>(r);
-    return f * (64.0f / 12.0f) * e > ER_XL_EPS2 * r;
+    ill = xl_ill_rule(e, r, f);
+    nf = !ill && bad > 0.0f;
 }
 
 // The group's energy outside its maximum's lanes, from this lane's values
@@ -176,7 +176,7 @@ ER_DEV void xl_scale(float mx, float *sg, float *inv) {
 // Converts one 16-value chunk (index tRaw, values in xr) into LDS.  The 4
 // chunks of a 64-group are held by 4 consecutive lanes, which exchange their
 // maxima; every lane of the wave must call this together.
-ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uint32_t tRaw) {
+ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uint32_t tRaw, XlCheck *ck = nullptr) {
     const uint32_t C16 = K >> 4;
     float v[16];
 #pragma unroll
@@ -226,6 +226,12 @@ ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uin
         lb[1][d] = d1 ^ 0x80808080u;
         lb[2][d] = d2 ^ 0x80808080u;
     }
+    if (ck) {
+        const bool st = tRaw < C16, first = st && (tRaw & 3u) == 0;
+        ck->e = __builtin_fmaf(first && rest > 0.0f ? sg : 0.0f, sg, ck->e);
+        ck->r += first ? rest : 0.0f;
+        ck->nf |= st && !__builtin_isfinite(sm);
+    }
     // chunks past the end are clamped copies with a different group max: never stored
     if (tRaw < C16) {
         uint8_t *planes = (uint8_t *)lds;
@@ -249,7 +255,7 @@ ER_DEV void xl_store_chunk(uint32_t *lds, uint32_t K, const float4 (&xr)[4], uin
 // xl_store_chunk.  The 8 half-chunks of a 64-group are held by 8 consecutive
 // lanes, which exchange their maxima (and pairs their half sums); every lane
 // of the wave must call this together.
-ER_DEV void xl_store_half(uint32_t *lds, uint32_t K, const float4 (&xr)[2], uint32_t hRaw) {
+ER_DEV void xl_store_half(uint32_t *lds, uint32_t K, const float4 (&xr)[2], uint32_t hRaw, XlCheck *ck = nullptr) {
     const uint32_t C8 = K >> 3;
     const float v[8] = {xr[0].x, xr[0].y, xr[0].z, xr[0].w, xr[1].x, xr[1].y, xr[1].z, xr[1].w};
     float mx = 0.0f, sh = 0.0f;
@@ -284,6 +290,12 @@ ER_DEV void xl_store_half(uint32_t *lds, uint32_t K, const float4 (&xr)[2], uint
         lb[1][d] = d1 ^ 0x80808080u;
         lb[2][d] = d2 ^ 0x80808080u;
     }
+    if (ck) {
+        const bool st = hRaw < C8, first = st && (hRaw & 7u) == 0;
+        ck->e = __builtin_fmaf(first && rest > 0.0f ? sg : 0.0f, sg, ck->e);
+        ck->r += first ? rest : 0.0f;
+        ck->nf |= st && (hRaw & 1u) == 0 && !__builtin_isfinite(sm);
+    }
     if (hRaw < C8) {
         uint8_t *planes = (uint8_t *)lds;
         float *x16 = (float *)(lds + (ER_XL_PLANES * K) / 4u);
@@ -302,22 +314,22 @@ ER_DEV void xl_store_half(uint32_t *lds, uint32_t K, const float4 (&xr)[2], uint
 
 // Stores the XG register-held chunks of this thread.
 template <int XG, int NT>
-ER_DEV void xl_store(uint32_t *lds, uint32_t K, const float4 (&xr)[XG][4]) {
+ER_DEV void xl_store(uint32_t *lds, uint32_t K, const float4 (&xr)[XG][4], XlCheck *ck = nullptr) {
 #pragma unroll
-    for (int c = 0; c < XG; ++c) xl_store_chunk(lds, K, xr[c], threadIdx.x + (uint32_t)NT * c);
+    for (int c = 0; c < XG; ++c) xl_store_chunk(lds, K, xr[c], threadIdx.x + (uint32_t)NT * c, ck);
 }
 
 // Chunks with index >= XG*NT (K beyond the register-staged part): loaded and
 // stored after the weight loads are in flight.
 template <int XG, int NT>
-ER_DEV void xl_store_tail(const float *__restrict__ x, uint32_t *lds, uint32_t K) {
+ER_DEV void xl_store_tail(const float *__restrict__ x, uint32_t *lds, uint32_t K, XlCheck *ck = nullptr) {
     const uint32_t C16 = K >> 4;
     for (uint32_t base = (uint32_t)NT * XG; base < C16; base += NT) {
         float4 xr[4];
         const uint32_t t = min(base + threadIdx.x, C16 - 1u);
 #pragma unroll
         for (int q = 0; q < 4; ++q) xr[q] = ((const float4 *)(x + 16u * t))[q];
-        xl_store_chunk(lds, K, xr, base + threadIdx.x);
+        xl_store_chunk(lds, K, xr, base + threadIdx.x, ck);
     }
 }
 
