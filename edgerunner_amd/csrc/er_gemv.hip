@@ -167,6 +167,10 @@ ER_DEV void gemv_q4k_i8_core(const uint8_t *const (&rowp)[R], float *const (&yro
         if ((threadIdx.x & 63u) == 0) chkw[threadIdx.x >> 6] = sh;
     }
     __syncthreads();
+    // the launch's check decisions, read while the first weights are in flight
+    bool ill, nfx;
+    xl_check_decide(chkw, ER_GEMV_WAVES, 4.0f, ill, nfx);
+    __builtin_amdgcn_sched_barrier(0);
 
     const XLimbs X = xl_view(lds, K);
     const uint32_t M0F = vreg_const(0x0f0f0f0fu);
@@ -192,8 +196,6 @@ ER_DEV void gemv_q4k_i8_core(const uint8_t *const (&rowp)[R], float *const (&yro
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    bool ill, nfx;
-    xl_check_decide(chkw, ER_GEMV_WAVES, 4.0f, ill, nfx);
     if (ill || nfx) {
         float sp[R], hits = 0.0f;
 #pragma unroll
@@ -409,6 +411,10 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
         if ((threadIdx.x & 63u) == 0) chkw[threadIdx.x >> 6] = sh;
     }
     __syncthreads();
+    // the launch's check decisions, read while the first weights are in flight
+    bool ill, nfx;
+    xl_check_decide(chkw, ER_GEMV_WAVES, 1.0f, ill, nfx);
+    __builtin_amdgcn_sched_barrier(0);
 
     const XLimbs X = xl_view(lds, K);
     float acc[R];
@@ -429,8 +435,6 @@ ER_DEV void gemv_q8_0_i8(const uint8_t *__restrict__ W, const float *__restrict_
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    bool ill, nfx;
-    xl_check_decide(chkw, ER_GEMV_WAVES, 1.0f, ill, nfx);
     if (ill || nfx) {
         float sp[R], hits = 0.0f;
 #pragma unroll
@@ -533,6 +537,10 @@ ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const
         if ((threadIdx.x & 63u) == 0) chkw[threadIdx.x >> 6] = sh;
     }
     __syncthreads();
+    // the launch's check decisions, read while the first weights are in flight
+    bool ill, nfx;
+    xl_check_decide(chkw, ER_GEMV_WAVES, 1.0f, ill, nfx);
+    __builtin_amdgcn_sched_barrier(0);
 
     const XLimbs X = xl_view(lds, K);
     float acc[R];
@@ -553,8 +561,6 @@ ER_DEV void gemv_q8_0_i8_fused_core(const uint8_t *const (&rowp)[R], void *const
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    bool ill, nfx;
-    xl_check_decide(chkw, ER_GEMV_WAVES, 1.0f, ill, nfx);
     if (ill || nfx) {
         // the staged values: x, or x * rms * normW as the prologue formed them
         // (rms recomputed from the same wave sums, so it is the same value)
@@ -870,6 +876,10 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
         if ((threadIdx.x & 63u) == 0) chkw[threadIdx.x >> 6] = sh;
     }
     __syncthreads();
+    // the launch's check decisions, read while the first weights are in flight
+    bool ill, nfx;
+    xl_check_decide(chkw, ER_GEMV_WAVES, 4.0f, ill, nfx);
+    __builtin_amdgcn_sched_barrier(0);
 
     const XLimbs X = xl_view(lds, K);
     const uint32_t M0F = vreg_const(0x0f0f0f0fu), M30 = vreg_const(0x30303030u);
@@ -929,8 +939,6 @@ ER_DEV void gemv_q6k_i8(const uint8_t *__restrict__ W, const float *__restrict__
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    bool ill, nfx;
-    xl_check_decide(chkw, ER_GEMV_WAVES, 4.0f, ill, nfx);
     if (ill || nfx) {
         float sp[R], hits = 0.0f;
 #pragma unroll
@@ -1337,6 +1345,8 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) step(i0, u, true);
+    // the launch's check decisions from the staging waves' shares (read here,
+    // not before the first dot: there they measured 1-2% slower on the heads)
     bool ill, nfx;
     xl_check_decide(chkw, (int)STG, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f, ill, nfx);
     if (ill) {
