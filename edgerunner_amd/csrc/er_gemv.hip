@@ -1476,6 +1476,15 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
 #pragma unroll
             for (int q = 0; q < VPL / 4; ++q) xr[p][q] = *(const float4 *)(x + VPL * hc + 4u * q);
         }
+        // 2-row steps (the longest x slices, two passes per wave): every
+        // wave's x requests leave the CU before any weight request.  The CU
+        // returns data in request order, so a wave issuing its x after the
+        // weights of the waves before it waited behind their HBM reads.
+        // (Waves with no slice take the matching barrier below: every wave
+        // passes exactly one.)  With 4 and 8 rows per step the barrier
+        // measured slower at most step counts, so those kernels go without.
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (PAR == 2) __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         typename F::Wt wb[D];
         auto issue = [&](uint32_t j, int b) {
@@ -1516,6 +1525,8 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
             acc = group_sum<LPR>(acc);
             res = li == (uint32_t)j ? acc : res;
         }
+    } else if constexpr (PAR == 2) {
+        __builtin_amdgcn_s_barrier();  // the x barrier above, for a wave with no slice
     }
     if (li < (uint32_t)J) part[wave][PAR * li + g] = res;
     if (lane == 0) chk[wave] = share;
