@@ -1343,12 +1343,20 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
             for (int u = 0; u < UNR; ++u) step(i0, u, false);
         }
     }
+    // the launch's check decisions from the staging waves' shares, taken after
+    // the next-to-last step of the last body, so the LDS reads run while the
+    // last unit's weights are still arriving (before the first dot they
+    // measured 1-2% slower on the heads; after the last step, ~2% slower)
+    bool ill = false, nfx = false;
+    constexpr int UCK = UNR >= 2 ? UNR - 2 : 0;
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) step(i0, u, true);
-    // the launch's check decisions from the staging waves' shares (read here,
-    // not before the first dot: there they measured 1-2% slower on the heads)
-    bool ill, nfx;
-    xl_check_decide(chkw, (int)STG, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f, ill, nfx);
+    for (int u = 0; u < UNR; ++u) {
+        step(i0, u, true);
+        if (u == UCK) {
+            xl_check_decide(chkw, (int)STG, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f, ill, nfx);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
     if (ill) {
         // x the limbs do not carry precisely enough: every row of this lane
         // group again, in fp32 over every position from the raw weights, the
