@@ -2220,6 +2220,21 @@ ER_CUK_TOP1_ENTRY(4, 13) ER_CUK_TOP1_ENTRY(4, 14) ER_CUK_TOP1_ENTRY(4, 15) ER_CU
     }
 ER_I8_MULTI_CONFIGS(ER_I8_MULTI_ENTRY)
 
+// The multi-matrix kernels with one row computation per lane group
+// (ER_I8_MULTI1_CONFIGS; same names and arguments as above).
+#define ER_I8_MULTI1_ENTRY(LPR, NS, R)                                                         \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q4k_multi_l##LPR##_n##NS##_r##R(Q4Multi mm, const float *__restrict__ x,       \
+                                                uint32_t K) {                                 \
+        gemv_q4k_i8_multi<LPR, NS, R>(mm, x, K);                                              \
+    }                                                                                          \
+    extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                            \
+        er_gemv_q8_0_multi_l##LPR##_n##NS##_r##R(Q8Multi mm, const float *__restrict__ x,      \
+                                                 uint32_t K) {                                \
+        gemv_q8_0_i8_multi<LPR, NS, R>(mm, x, K);                                             \
+    }
+ER_I8_MULTI1_CONFIGS(ER_I8_MULTI1_ENTRY)
+
 #define ER_GEMV_ENTRY(fmt, impl, rows, lpr, xg, tag)                                       \
     extern "C" __global__ void __launch_bounds__(ER_GEMV_THREADS)                        \
         er_gemv_##fmt##_l##lpr##_##tag(const uint8_t *__restrict__ W,                     \

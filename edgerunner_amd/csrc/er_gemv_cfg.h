@@ -28,6 +28,14 @@
     ER_I8_MULTI_CONFIGS_L(X, 64) ER_I8_MULTI_CONFIGS_L(X, 32) ER_I8_MULTI_CONFIGS_L(X, 16) \
     ER_I8_MULTI_CONFIGS_L(X, 4)
 
+// One row computation per lane group, for the multi-matrix kernels whose rows
+// stand alone (Q4_K dual / triple, fused Q8_0 QKV; not the paired GeGLU and
+// gate/up + SiLU): the most workgroups for a latency-bound launch.
+#define ER_I8_MULTI1_CONFIGS_L(X, LPR) X(LPR, 1, 1) X(LPR, 2, 1) X(LPR, 3, 1) X(LPR, 4, 1)
+#define ER_I8_MULTI1_CONFIGS(X) \
+    ER_I8_MULTI1_CONFIGS_L(X, 64) ER_I8_MULTI1_CONFIGS_L(X, 32) ER_I8_MULTI1_CONFIGS_L(X, 16) \
+    ER_I8_MULTI1_CONFIGS_L(X, 4)
+
 // CU-resident Q4_K / Q8_0 / Q6_K kernels (family 3): X(LPR, NS, MAXJ), one 8-wave
 // workgroup per CU-sized share of the rows, unrolled kernels for 1..MAXJ row
 // steps per wave, and for MAXJ == 8 a rolled one for up to ER_CU_MAX_ROLLED.

@@ -177,6 +177,11 @@ constexpr uint32_t cu_lds_bytes(uint32_t K) { return xl_lds_bytes(K) + 4u * K; }
 constexpr I8Cfg kI8MultiCfg[] = {ER_I8_MULTI_CONFIGS(ER_I8_ROW)};
 #undef ER_I8_ROW
 constexpr int kI8MultiCount = (int)(sizeof(kI8MultiCfg) / sizeof(kI8MultiCfg[0]));
+// ... and the one-row forms of the unpaired multi-matrix kernels.
+#define ER_I8_ROW(LPR, NS, R) {LPR, NS, R},
+constexpr I8Cfg kI8Multi1Cfg[] = {ER_I8_MULTI1_CONFIGS(ER_I8_ROW)};
+#undef ER_I8_ROW
+constexpr int kI8Multi1Count = (int)(sizeof(kI8Multi1Cfg) / sizeof(kI8Multi1Cfg[0]));
 
 // Kernel argument block of er_gemv_q4k_multi_* (matches Q4Multi in er_gemv.hip).
 struct Q4MultiArgs {
@@ -218,9 +223,12 @@ struct er_hip_ctx {
     hipFunction_t fnQ4KGeglu[kI8MultiCount] = {};
     hipFunction_t fnQ8Multi[kI8MultiCount] = {};
     hipFunction_t fnQ8Silu[kI8MultiCount] = {};
+    hipFunction_t fnQ4KMulti1[kI8Multi1Count] = {};  // one row computation per lane group
+    hipFunction_t fnQ8Multi1[kI8Multi1Count] = {};
     int cu_count = 0;
     int i8_override = -1;  // ER_HIP_GEMV_CONFIG=lpr:ns:r (benchmark sweeps only)
     int multi_override = -1;  // ER_HIP_GEMV_MULTI_CONFIG=lpr:ns:r for the multi-matrix kernels (tests, sweeps)
+    int multi1_override = -1;  // the same with r = 1: the one-row forms (their unpaired kinds only)
     int cu_mode = -1;      // ER_HIP_GEMV_CU: 0 never, 1 whenever it applies, unset: by shape
     int cuk_mode = -1;     // ER_HIP_GEMV_CUK: 0 never, 2 every K <= 16384, unset: K > 8192 (comparisons)
     int gemm_variant = 0;  // ER_HIP_GEMM_VARIANT=1: non-pipelined GEMM, =2: 256-thread pipelined,
@@ -307,51 +315,108 @@ void pick_lanes(uint32_t S, uint32_t M, uint32_t maxN, int cu, uint32_t &L, uint
     }
 }
 
-// Picks the integer-dot configuration for a row of S 64-weight slots and M
-// rows: the lane split (LPR, NS) of pick_lanes, then the most rows per lane
-// group that still gives every CU two workgroups.  Returns -1 when no
-// configuration covers S.
-int pick_i8(uint32_t S, uint32_t M, int cu) {
+// Rows per lane group for one token's launch of the integer-dot kernels: the
+// most workgroups that fit one per CU, or, when even the fewest do not fit,
+// the fewest; equal counts go to fewer rows per lane group.  At these sizes a
+// launch is latency-bound, and a second, partial round of workgroups cost
+// more than the rounds' extra parallelism gave: Q4_K 5120-8192 x 1024 and
+// 3072-3584 x 2048 ran 17-18% faster at 2 rows than at 1 (256 against 320-512
+// workgroups), 12288-16384 x 1024 and 8192 x 2048 10-14% faster at 4 rows
+// than at 1 or 2.  Several tokens keep the earlier rule: the most rows per
+// lane group that still give every CU two workgroups.
+struct I8Cand {
+    int idx;         // index into its configuration table
+    uint32_t r;      // rows per lane group
+    uint64_t wgs;    // workgroups for one token
+};
+template <size_t N>
+int pick_rows(const I8Cand (&c)[N], int n, int cu, bool oneToken) {
+    int best = -1;
+    if (oneToken) {
+        int fewest = -1;
+        for (int k = 0; k < n; ++k) {
+            if (c[k].wgs <= (uint64_t)cu &&
+                (best < 0 || c[k].wgs > c[best].wgs || (c[k].wgs == c[best].wgs && c[k].r < c[best].r)))
+                best = k;
+            if (fewest < 0 || c[k].wgs < c[fewest].wgs || (c[k].wgs == c[fewest].wgs && c[k].r > c[fewest].r))
+                fewest = k;
+        }
+        return best >= 0 ? best : fewest;
+    }
+    for (int k = 0; k < n; ++k)  // the most rows with two workgroups per CU, else the fewest rows
+        if (c[k].wgs >= 2u * (uint64_t)cu && (best < 0 || c[k].r > c[best].r)) best = k;
+    if (best < 0)
+        for (int k = 0; k < n; ++k)
+            if (best < 0 || c[k].r < c[best].r) best = k;
+    return best;
+}
+
+// Picks the integer-dot configuration for a row of S 64-weight slots, M rows
+// and `tokens` tokens: the lane split (LPR, NS) of pick_lanes, then the rows
+// per lane group of pick_rows.  Returns -1 when no configuration covers S.
+int pick_i8(uint32_t S, uint32_t M, int cu, uint32_t tokens) {
     uint32_t bestL = 0, bestN = 0;
     pick_lanes(S, M, 8, cu, bestL, bestN);
     if (!bestL) return -1;
     const uint32_t G = 64u / bestL;
-    int pick = -1;
-    for (uint32_t R : {4u, 2u, 1u}) {
-        for (int i = 0; i < kI8Count; ++i) {
-            if (kI8Cfg[i].lpr != bestL || kI8Cfg[i].ns != bestN || kI8Cfg[i].r != R) continue;
-            const uint64_t wgs = ((uint64_t)M + ER_GEMV_WAVES * G * R - 1) / (ER_GEMV_WAVES * G * R);
-            if (wgs >= 2u * (uint64_t)cu || R == 1u) return i;
-            if (pick < 0) pick = i;
-        }
+    I8Cand c[8];
+    int n = 0;
+    for (int i = 0; i < kI8Count && n < 8; ++i) {
+        if (kI8Cfg[i].lpr != bestL || kI8Cfg[i].ns != bestN) continue;
+        const uint32_t rows = ER_GEMV_WAVES * G * kI8Cfg[i].r;
+        c[n++] = I8Cand{i, kI8Cfg[i].r, ((uint64_t)M + rows - 1) / rows};
     }
-    return pick;
+    const int k = n ? pick_rows(c, n, cu, tokens <= 1u) : -1;
+    return k < 0 ? -1 : c[k].idx;
 }
 
 // Multi-matrix / GeGLU configuration for S slots and Mt total row
-// computations: as pick_i8, over kI8MultiCfg (R in {4, 2}).
-int pick_i8_multi(uint32_t S, uint32_t Mt, int cu) {
+// computations: as pick_i8, over kI8MultiCfg (R in {4, 2}) and, when the
+// kernel's rows stand alone (r1Ok), the one-row forms kI8Multi1Cfg.  Sets
+// ci (kI8MultiCfg) or ci1 (kI8Multi1Cfg); both -1 when nothing covers S.
+struct MultiPick {
+    int ci = -1, ci1 = -1;
+};
+MultiPick pick_i8_multi(uint32_t S, uint32_t Mt, int cu, bool r1Ok, uint32_t tokens) {
+    MultiPick p;
     uint32_t bestL = 0, bestN = 0;
     pick_lanes(S, Mt, 4, cu, bestL, bestN);
-    if (!bestL) return -1;
+    if (!bestL) return p;
     const uint32_t G = 64u / bestL;
-    int fallback = -1;
-    for (uint32_t R : {4u, 2u}) {
-        for (int i = 0; i < kI8MultiCount; ++i) {
-            if (kI8MultiCfg[i].lpr != bestL || kI8MultiCfg[i].ns != bestN || kI8MultiCfg[i].r != R) continue;
-            const uint64_t wgs = ((uint64_t)Mt + ER_GEMV_WAVES * G * R - 1) / (ER_GEMV_WAVES * G * R);
-            if (wgs >= 2u * (uint64_t)cu) return i;
-            fallback = i;  // the last match is R = 2: most workgroups
-        }
+    I8Cand c[8];
+    bool one[8];
+    int n = 0;
+    for (int i = 0; i < kI8MultiCount && n < 8; ++i) {
+        if (kI8MultiCfg[i].lpr != bestL || kI8MultiCfg[i].ns != bestN) continue;
+        const uint32_t rows = ER_GEMV_WAVES * G * kI8MultiCfg[i].r;
+        one[n] = false;
+        c[n++] = I8Cand{i, kI8MultiCfg[i].r, ((uint64_t)Mt + rows - 1) / rows};
     }
-    return fallback;
+    // several tokens: R in {4, 2} only, as before
+    for (int i = 0; r1Ok && tokens <= 1u && i < kI8Multi1Count && n < 8; ++i) {
+        if (kI8Multi1Cfg[i].lpr != bestL || kI8Multi1Cfg[i].ns != bestN) continue;
+        const uint32_t rows = ER_GEMV_WAVES * G;
+        one[n] = true;
+        c[n++] = I8Cand{i, 1u, ((uint64_t)Mt + rows - 1) / rows};
+    }
+    const int k = n ? pick_rows(c, n, cu, tokens <= 1u) : -1;
+    if (k >= 0) (one[k] ? p.ci1 : p.ci) = c[k].idx;
+    return p;
 }
 
 // pick_i8_multi, or the context's forced configuration when it covers S slots.
-int pick_multi(const er_hip_ctx *ctx, uint32_t S, uint32_t Mt) {
-    const int o = ctx->multi_override;
-    if (o >= 0 && (uint32_t)kI8MultiCfg[o].lpr * kI8MultiCfg[o].ns >= S) return o;
-    return pick_i8_multi(S, Mt, ctx->cu_count);
+MultiPick pick_multi(const er_hip_ctx *ctx, uint32_t S, uint32_t Mt, bool r1Ok, uint32_t tokens) {
+    MultiPick p;
+    const int o = ctx->multi_override, o1 = ctx->multi1_override;
+    if (o >= 0 && (uint32_t)kI8MultiCfg[o].lpr * kI8MultiCfg[o].ns >= S) {
+        p.ci = o;
+        return p;
+    }
+    if (r1Ok && o1 >= 0 && (uint32_t)kI8Multi1Cfg[o1].lpr * kI8Multi1Cfg[o1].ns >= S) {
+        p.ci1 = o1;
+        return p;
+    }
+    return pick_i8_multi(S, Mt, ctx->cu_count, r1Ok, tokens);
 }
 
 // CU-resident configuration for S slots from cfg[0..count): the fewest idle
@@ -562,7 +627,7 @@ er_status encode_gemv(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
                          grid, dim3(64u * ER_CU_WAVES, 1, 1), cu_lds_bytes(K), stream, cargs);
     }
     if ((f != Fmt::Q8_0 || q8Aligned) && K <= kI8MaxK && ctx->gemv_fp32 == 0) {
-        int ci = pick_i8(K / 64u, M, ctx->cu_count);
+        int ci = pick_i8(K / 64u, M, ctx->cu_count, batch);
         if (ctx->i8_override >= 0 && (uint32_t)kI8Cfg[ctx->i8_override].lpr *
                                              kI8Cfg[ctx->i8_override].ns >= K / 64u)
             ci = ctx->i8_override;
@@ -757,7 +822,7 @@ er_status launch_q6k_top1(er_hip_ctx *ctx, er_stream stream, er_buffer W, er_buf
                        dim3(64u * ER_CU_WAVES, 1, 1), ldsTop1, stream, args);
         if (st != ER_OK) return st;
     } else if (M > 0) {
-        int ci = pick_i8(K / 64u, M, ctx->cu_count);
+        int ci = pick_i8(K / 64u, M, ctx->cu_count, 1u);
         if (ctx->i8_override >= 0 && (uint32_t)kI8Cfg[ctx->i8_override].lpr *
                                              kI8Cfg[ctx->i8_override].ns >= K / 64u)
             ci = ctx->i8_override;
@@ -996,15 +1061,15 @@ er_status encode_q4k_multi(er_hip_ctx *ctx, er_stream stream, const er_buffer *W
     if (Mt > 0xffffffffull) return fail(ER_ERR_INVALID_MATRIX_SHAPE, "Q4_K multi: too many rows");
     st = bind_device(ctx);
     if (st != ER_OK) return st;
-    const int ci = K <= kI8MaxK ? pick_multi(ctx, K / 64u, (uint32_t)Mt) : -1;
-    if (ci < 0) {
+    const MultiPick mp = K <= kI8MaxK ? pick_multi(ctx, K / 64u, (uint32_t)Mt, true, 1u) : MultiPick{};
+    if (mp.ci < 0 && mp.ci1 < 0) {
         for (int i = 0; i < count; ++i) {
             st = encode_gemv(ctx, stream, Fmt::Q4_K, Ws[i], x, ys[i], 1, Ms[i], K);
             if (st != ER_OK) return st;
         }
         return ER_OK;
     }
-    const I8Cfg &c = kI8MultiCfg[ci];
+    const I8Cfg &c = mp.ci >= 0 ? kI8MultiCfg[mp.ci] : kI8Multi1Cfg[mp.ci1];
     Q4MultiArgs a{};
     for (int i = 0; i < 3; ++i) {
         const int j = i < count ? i : 0;
@@ -1016,8 +1081,8 @@ er_status encode_q4k_multi(er_hip_ctx *ctx, er_stream stream, const er_buffer *W
     const uint32_t lds = xl_lds_bytes(K);
     void *args[] = {&a, &x.data, &K};
     dim3 grid((uint32_t)((Mt + rowsPerBlock - 1) / rowsPerBlock), 1, 1);
-    return launch_fn(ctx->fnQ4KMulti[ci], "er_gemv_q4k_multi", grid, dim3(kGemvThreads, 1, 1), lds,
-                     stream, args);
+    return launch_fn(mp.ci >= 0 ? ctx->fnQ4KMulti[mp.ci] : ctx->fnQ4KMulti1[mp.ci1], "er_gemv_q4k_multi", grid,
+                     dim3(kGemvThreads, 1, 1), lds, stream, args);
 }
 
 er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_buffer Wu, er_buffer x,
@@ -1028,7 +1093,7 @@ er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_b
     if (st != ER_OK) return st;
     st = check_ctx(ctx);
     if (st != ER_OK || M == 0) return st;
-    const int ci = K <= kI8MaxK && ctx->gemv_fp32 == 0 ? pick_multi(ctx, K / 64u, 2u * M) : -1;
+    const int ci = K <= kI8MaxK && ctx->gemv_fp32 == 0 ? pick_multi(ctx, K / 64u, 2u * M, false, 1u).ci : -1;
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     if (ci < 0) {
@@ -1118,8 +1183,8 @@ er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     const uint32_t S = K / 64u;
-    const int ci = anyK ? -1 : pick_multi(ctx, S, (uint32_t)(f.silu ? 2u * Mt : Mt));
-    if (ci < 0) {
+    const MultiPick mp = anyK ? MultiPick{} : pick_multi(ctx, S, (uint32_t)(f.silu ? 2u * Mt : Mt), !f.silu, tokens);
+    if (mp.ci < 0 && mp.ci1 < 0) {
         Q8MultiArgs a{};
         for (int m = 0; m < 3; ++m) {
             const int j = m < f.count ? m : 0;
@@ -1138,7 +1203,8 @@ er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &
         return launch(ctx, f.silu ? K_GEMV_Q8_0_ANY_SILU : K_GEMV_Q8_0_ANY_MULTI, grid, dim3(kGemvThreads, 1, 1), 0,
                       stream, args);
     }
-    const I8Cfg &c = kI8MultiCfg[ci];
+    const int ci = mp.ci;  // the paired gate/up + SiLU kernel has no one-row form (r1Ok false above)
+    const I8Cfg &c = ci >= 0 ? kI8MultiCfg[ci] : kI8Multi1Cfg[mp.ci1];
     const uint32_t lds = xl_lds_bytes(K);
     const float *normW = (const float *)f.normW.data;
     float eps = f.eps;
@@ -1165,8 +1231,8 @@ er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &
     const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
     void *args[] = {&a, &x.data, &K};
     dim3 grid((uint32_t)((Mt + rowsPerBlock - 1) / rowsPerBlock), tokens, 1);
-    return launch_fn(ctx->fnQ8Multi[ci], "er_gemv_q8_0_multi", grid, dim3(kGemvThreads, 1, 1), lds, stream,
-                     args);
+    return launch_fn(ci >= 0 ? ctx->fnQ8Multi[ci] : ctx->fnQ8Multi1[mp.ci1], "er_gemv_q8_0_multi", grid,
+                     dim3(kGemvThreads, 1, 1), lds, stream, args);
 }
 
 er_status encode_dequant(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer blocks,
@@ -1366,6 +1432,21 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
             }
         }
     }
+    for (int i = 0; i < kI8Multi1Count; ++i) {
+        char name[64];
+        static const char *const kinds[2] = {"q4k_multi", "q8_0_multi"};
+        hipFunction_t *const slots[2] = {&ctx->fnQ4KMulti1[i], &ctx->fnQ8Multi1[i]};
+        for (int kind = 0; kind < 2; ++kind) {
+            std::snprintf(name, sizeof(name), "er_gemv_%s_l%u_n%u_r%u", kinds[kind], (unsigned)kI8Multi1Cfg[i].lpr,
+                          (unsigned)kI8Multi1Cfg[i].ns, (unsigned)kI8Multi1Cfg[i].r);
+            e = hipModuleGetFunction(slots[kind], ctx->module, name);
+            if (e != hipSuccess) {
+                (void)hipModuleUnload(ctx->module);
+                delete ctx;
+                return fail(ER_ERR_FUNCTION_NOT_FOUND, "functionNotFound(%s): %s", name, hipGetErrorString(e));
+            }
+        }
+    }
     if (const char *gv = std::getenv("ER_HIP_GEMM_VARIANT")) ctx->gemm_variant = std::atoi(gv);
     if (const char *fv = std::getenv("ER_HIP_GEMV_FP32")) ctx->gemv_fp32 = std::atoi(fv);
     if (const char *gt = std::getenv("ER_HIP_GEMM_TILE")) {
@@ -1382,6 +1463,10 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
         if (std::sscanf(mv, "%u:%u:%u", &l, &n, &r) == 3)
             for (int i = 0; i < kI8MultiCount; ++i)
                 if (kI8MultiCfg[i].lpr == l && kI8MultiCfg[i].ns == n && kI8MultiCfg[i].r == r) ctx->multi_override = i;
+        if (std::sscanf(mv, "%u:%u:%u", &l, &n, &r) == 3)
+            for (int i = 0; i < kI8Multi1Count; ++i)
+                if (kI8Multi1Cfg[i].lpr == l && kI8Multi1Cfg[i].ns == n && kI8Multi1Cfg[i].r == r)
+                    ctx->multi1_override = i;
     }
     if (const char *ov = std::getenv("ER_HIP_GEMV_CONFIG")) {
         unsigned l = 0, n = 0, r = 0;

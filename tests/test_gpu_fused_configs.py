@@ -2,7 +2,8 @@
 ER_HIP_GEMV_MULTI_CONFIG=lpr:ns:r in a context of its own, on a row length
 that makes some lanes use all NS slots: the Q4_K triple projection and dual
 GeGLU, and the Q8_0 RMSNorm + gate/up + SiLU, against the CPU oracle at the
-parity bar (relative L2 <= 1e-3)."""
+parity bar (relative L2 <= 1e-3); and every one-row form (r = 1) of the
+unpaired kernels: the Q4_K triple and the Q8_0 RMSNorm + QKV."""
 import os
 
 import numpy as np
@@ -75,5 +76,55 @@ def test_forced_multi_config(lpr, ns, r):
             g = ref.gemv("q8_0", Wg, n, inter, K, threads=ref.max_threads())
             u = ref.gemv("q8_0", Wu, n, inter, K, threads=ref.max_threads())
             assert rel_l2(got[t], ref.silu(g) * u) < TOL, ("q8 gate-up-silu", lpr, ns, r, K, t)
+    finally:
+        ctx.close()
+
+
+# One-row forms of the unpaired multi-matrix kernels (the Q4_K dual / triple
+# and the fused Q8_0 QKV), forced the same way with r = 1.
+CONFIGS1 = [(l, n) for l in (64, 32, 16, 4) for n in (1, 2, 3, 4) if row_length(l, n) is not None]
+
+
+@pytest.mark.parametrize("lpr,ns", CONFIGS1)
+def test_forced_one_row_multi_config(lpr, ns):
+    K = row_length(lpr, ns)
+    old = os.environ.get("ER_HIP_GEMV_MULTI_CONFIG")
+    os.environ["ER_HIP_GEMV_MULTI_CONFIG"] = f"{lpr}:{ns}:1"
+    try:
+        ctx = Context(int(os.environ.get("ER_DEVICE", "0")))
+    finally:
+        if old is None:
+            os.environ.pop("ER_HIP_GEMV_MULTI_CONFIG", None)
+        else:
+            os.environ["ER_HIP_GEMV_MULTI_CONFIG"] = old
+    try:
+        gemv, fk = GEMVKernel(ctx), FusedQ8Kernel(ctx)
+        tag = lpr * 100 + ns * 10 + 1
+        x = synth.normal_f32(synth.seed(92, tag), K)
+        rows = [203, 77, 130]
+        Ws = [synth.q4_k(synth.seed(93, 3 * tag + i), m, K) for i, m in enumerate(rows)]
+        ys = gemv.executeQ4KWeightsMulti(Ws, x, rows, K)
+        for W, m, y in zip(Ws, rows, ys):
+            assert rel_l2(y, ref.gemv("q4_k", W, x, m, K, threads=ref.max_threads())) < TOL, ("triple", lpr, ns, K)
+
+        qd, kvd = 203, 77
+        Wq, Wk, Wv = (synth.q8_0(synth.seed(98, 3 * tag + i), m, K) for i, m in enumerate((qd, kvd, kvd)))
+        nw = (0.5 + synth.normal_f32(synth.seed(97, tag), K) ** 2 / 4).astype(np.float32)
+        bufs = [ctx.upload(a) for a in (Wq, Wk, Wv, x, nw)]
+        oq, ok, ov = ctx.alloc(4 * qd), ctx.alloc(4 * kvd), ctx.alloc(2 * kvd)
+        try:
+            fk.encodeFusedQKV(None, bufs[0], bufs[1], bufs[2], bufs[3], oq, ok, ov, bufs[4], qd, kvd, K, 1, EPS)
+            ctx.synchronize()
+            q, k = oq.download(np.float32), ok.download(np.float32)
+            v = ov.download(np.float16).astype(np.float32)
+        finally:
+            for b in bufs + [oq, ok, ov]:
+                b.free()
+        n = ref.rmsnorm(x, nw, EPS)
+        for got, W, m, half in ((q, Wq, qd, False), (k, Wk, kvd, False), (v, Wv, kvd, True)):
+            e = ref.gemv("q8_0", W, n, m, K, threads=ref.max_threads())
+            if half:
+                e = e.astype(np.float16).astype(np.float32)
+            assert rel_l2(got, e) < TOL, ("q8 qkv", lpr, ns, K, m)
     finally:
         ctx.close()
