@@ -315,48 +315,47 @@ void pick_lanes(uint32_t S, uint32_t M, uint32_t maxN, int cu, uint32_t &L, uint
     }
 }
 
-// Rows per lane group for one token's launch of the integer-dot kernels: the
-// most workgroups that fit one per CU, or, when even the fewest do not fit,
-// the fewest; equal counts go to fewer rows per lane group.  At these sizes a
-// launch is latency-bound, and a second, partial round of workgroups cost
-// more than the rounds' extra parallelism gave: Q4_K 5120-8192 x 1024 and
-// 3072-3584 x 2048 ran 17-18% faster at 2 rows than at 1 (256 against 320-512
-// workgroups), 12288-16384 x 1024 and 8192 x 2048 10-14% faster at 4 rows
-// than at 1 or 2.  Several tokens keep the earlier rule: the most rows per
-// lane group that still give every CU two workgroups.
+// Rows per lane group R for a launch of the integer-dot kernels, counting the
+// workgroups of all its tokens: the most workgroups that fit one per CU, or,
+// when even the fewest do not fit, the fewest; equal counts go to fewer rows
+// per lane group.  At these sizes a launch is latency-bound, and a second,
+// partial round of workgroups cost more than the rounds' extra parallelism
+// gave.  Same-box A/B against the earlier rule (the most rows per lane group
+// that still give every CU two workgroups per token, else R = 1): one token,
+// Q4_K 5120-8192 x 1024 and 3072-3584 x 2048 17-18% faster at 2 rows,
+// 12288-16384 x 1024 and 8192 x 2048 10-14% faster at 4 rows; 2-8 tokens of
+// 1024-4096 x 1024, 10-28% faster.
 struct I8Cand {
-    int idx;         // index into its configuration table
-    uint32_t r;      // rows per lane group
-    uint64_t wgs;    // workgroups for one token
+    int idx;       // index into its configuration table
+    uint32_t r;    // rows per lane group
+    uint64_t wgs;  // workgroups, all tokens
 };
 template <size_t N>
-int pick_rows(const I8Cand (&c)[N], int n, int cu, bool oneToken) {
-    int best = -1;
-    if (oneToken) {
-        int fewest = -1;
-        for (int k = 0; k < n; ++k) {
-            if (c[k].wgs <= (uint64_t)cu &&
-                (best < 0 || c[k].wgs > c[best].wgs || (c[k].wgs == c[best].wgs && c[k].r < c[best].r)))
-                best = k;
-            if (fewest < 0 || c[k].wgs < c[fewest].wgs || (c[k].wgs == c[fewest].wgs && c[k].r > c[fewest].r))
-                fewest = k;
-        }
-        return best >= 0 ? best : fewest;
+int pick_rows(const I8Cand (&c)[N], int n, int cu) {
+    int best = -1, fewest = -1;
+    for (int k = 0; k < n; ++k) {
+        if (c[k].wgs <= (uint64_t)cu &&
+            (best < 0 || c[k].wgs > c[best].wgs || (c[k].wgs == c[best].wgs && c[k].r < c[best].r)))
+            best = k;
+        if (fewest < 0 || c[k].wgs < c[fewest].wgs || (c[k].wgs == c[fewest].wgs && c[k].r > c[fewest].r))
+            fewest = k;
     }
-    for (int k = 0; k < n; ++k)  // the most rows with two workgroups per CU, else the fewest rows
-        if (c[k].wgs >= 2u * (uint64_t)cu && (best < 0 || c[k].r > c[best].r)) best = k;
-    if (best < 0)
-        for (int k = 0; k < n; ++k)
-            if (best < 0 || c[k].r < c[best].r) best = k;
-    return best;
+    return best >= 0 ? best : fewest;
+}
+
+// Rows of all tokens, for pick_lanes (its workgroup counts are proportional to
+// the rows), saturated to 32 bits.
+uint32_t all_rows(uint32_t M, uint32_t tokens) {
+    return (uint32_t)std::min<uint64_t>((uint64_t)M * std::max<uint32_t>(tokens, 1u), 0xffffffffull);
 }
 
 // Picks the integer-dot configuration for a row of S 64-weight slots, M rows
-// and `tokens` tokens: the lane split (LPR, NS) of pick_lanes, then the rows
-// per lane group of pick_rows.  Returns -1 when no configuration covers S.
+// and `tokens` tokens: the lane split (LPR, NS) of pick_lanes over the rows of
+// all tokens, then the rows per lane group of pick_rows.  Returns -1 when no
+// configuration covers S.
 int pick_i8(uint32_t S, uint32_t M, int cu, uint32_t tokens) {
     uint32_t bestL = 0, bestN = 0;
-    pick_lanes(S, M, 8, cu, bestL, bestN);
+    pick_lanes(S, all_rows(M, tokens), 8, cu, bestL, bestN);
     if (!bestL) return -1;
     const uint32_t G = 64u / bestL;
     I8Cand c[8];
@@ -364,15 +363,15 @@ int pick_i8(uint32_t S, uint32_t M, int cu, uint32_t tokens) {
     for (int i = 0; i < kI8Count && n < 8; ++i) {
         if (kI8Cfg[i].lpr != bestL || kI8Cfg[i].ns != bestN) continue;
         const uint32_t rows = ER_GEMV_WAVES * G * kI8Cfg[i].r;
-        c[n++] = I8Cand{i, kI8Cfg[i].r, ((uint64_t)M + rows - 1) / rows};
+        c[n++] = I8Cand{i, kI8Cfg[i].r, ((uint64_t)M + rows - 1) / rows * std::max<uint32_t>(tokens, 1u)};
     }
-    const int k = n ? pick_rows(c, n, cu, tokens <= 1u) : -1;
+    const int k = n ? pick_rows(c, n, cu) : -1;
     return k < 0 ? -1 : c[k].idx;
 }
 
-// Multi-matrix / GeGLU configuration for S slots and Mt total row
-// computations: as pick_i8, over kI8MultiCfg (R in {4, 2}) and, when the
-// kernel's rows stand alone (r1Ok), the one-row forms kI8Multi1Cfg.  Sets
+// Multi-matrix / GeGLU configuration for S slots, Mt total row computations
+// and `tokens` tokens: as pick_i8, over kI8MultiCfg (R in {4, 2}) and, when
+// the kernel's rows stand alone (r1Ok), the one-row forms kI8Multi1Cfg.  Sets
 // ci (kI8MultiCfg) or ci1 (kI8Multi1Cfg); both -1 when nothing covers S.
 struct MultiPick {
     int ci = -1, ci1 = -1;
@@ -380,9 +379,9 @@ struct MultiPick {
 MultiPick pick_i8_multi(uint32_t S, uint32_t Mt, int cu, bool r1Ok, uint32_t tokens) {
     MultiPick p;
     uint32_t bestL = 0, bestN = 0;
-    pick_lanes(S, Mt, 4, cu, bestL, bestN);
+    pick_lanes(S, all_rows(Mt, tokens), 4, cu, bestL, bestN);
     if (!bestL) return p;
-    const uint32_t G = 64u / bestL;
+    const uint32_t G = 64u / bestL, T = std::max<uint32_t>(tokens, 1u);
     I8Cand c[8];
     bool one[8];
     int n = 0;
@@ -390,16 +389,15 @@ MultiPick pick_i8_multi(uint32_t S, uint32_t Mt, int cu, bool r1Ok, uint32_t tok
         if (kI8MultiCfg[i].lpr != bestL || kI8MultiCfg[i].ns != bestN) continue;
         const uint32_t rows = ER_GEMV_WAVES * G * kI8MultiCfg[i].r;
         one[n] = false;
-        c[n++] = I8Cand{i, kI8MultiCfg[i].r, ((uint64_t)Mt + rows - 1) / rows};
+        c[n++] = I8Cand{i, kI8MultiCfg[i].r, ((uint64_t)Mt + rows - 1) / rows * T};
     }
-    // several tokens: R in {4, 2} only, as before
-    for (int i = 0; r1Ok && tokens <= 1u && i < kI8Multi1Count && n < 8; ++i) {
+    for (int i = 0; r1Ok && i < kI8Multi1Count && n < 8; ++i) {
         if (kI8Multi1Cfg[i].lpr != bestL || kI8Multi1Cfg[i].ns != bestN) continue;
         const uint32_t rows = ER_GEMV_WAVES * G;
         one[n] = true;
-        c[n++] = I8Cand{i, 1u, ((uint64_t)Mt + rows - 1) / rows};
+        c[n++] = I8Cand{i, 1u, ((uint64_t)Mt + rows - 1) / rows * T};
     }
-    const int k = n ? pick_rows(c, n, cu, tokens <= 1u) : -1;
+    const int k = n ? pick_rows(c, n, cu) : -1;
     if (k >= 0) (one[k] ? p.ci1 : p.ci) = c[k].idx;
     return p;
 }
