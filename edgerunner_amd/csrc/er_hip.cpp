@@ -523,6 +523,15 @@ struct CuPlan {
     int slot = 0;            // steps - 1, or ER_CU_MAX_STEPS for the rolled kernel
     uint32_t rowsPerWg = 0;  // step rows x steps
 };
+// Steps per workgroup for `need` steps of rows per CU and kernels of at most
+// maxSteps: the need split evenly over the fewest workgroups that hold it, so
+// every CU gets the same number of workgroups (28672 x 4096 Q4_K: 14 steps as
+// 2 x 7, 512 workgroups, instead of 8 + 6 as 448, of which 64 CUs got one).
+uint32_t even_steps(uint32_t need, uint32_t maxSteps) {
+    const uint32_t parts = (need + maxSteps - 1u) / maxSteps;
+    return std::max<uint32_t>(1u, (need + parts - 1u) / parts);
+}
+
 bool plan_cu(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batch, CuPlan &p) {
     if (K % 256u != 0 || K > kCuMaxK || ctx->gemv_fp32 != 0 || ctx->i8_override >= 0 || ctx->cu_mode == 0 ||
         (uint64_t)cu_lds_bytes(K) + 1024u > ctx->info.lds_per_workgroup || batch == 0)
@@ -540,10 +549,10 @@ bool plan_cu(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batc
                                        : (needed1 <= c.maxJ && (needed1 >= 3u || K > 8192u));
     if (!use) return false;
     // unrolled kernels up to maxJ steps, the rolled one up to ER_CU_MAX_ROLLED,
-    // more workgroups beyond
+    // more workgroups beyond (a CU's steps split evenly over them)
     const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
     const uint32_t maxSteps = rolled ? ER_CU_MAX_ROLLED : c.maxJ;
-    const uint32_t steps = std::min<uint32_t>(maxSteps, ((M + perToken - 1u) / perToken + step - 1u) / step);
+    const uint32_t steps = even_steps(((M + perToken - 1u) / perToken + step - 1u) / step, maxSteps);
     p.ci = ci;
     p.rowsPerWg = step * steps;
     p.slot = steps <= ER_CU_MAX_STEPS ? (int)steps - 1 : ER_CU_MAX_STEPS;
@@ -583,8 +592,8 @@ bool plan_cuk(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t bat
                        : (ctx->cuk_mode != 2 && (S < 64u || (S == 64u && (f != Fmt::Q4_K || rows1 < 8u)))))
         return false;
     const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
-    const uint32_t rows = (M + perToken - 1u) / perToken;  // per workgroup, one token
-    p.j = (int)std::min<uint32_t>(maxJ, std::max<uint32_t>(1u, (rows + par - 1u) / par));
+    const uint32_t rows = (M + perToken - 1u) / perToken;  // per CU, one token
+    p.j = (int)even_steps(std::max<uint32_t>(1u, (rows + par - 1u) / par), maxJ);
     p.rowsPerWg = par * (uint32_t)p.j;
     return true;
 }
