@@ -544,14 +544,19 @@ bool plan_cu(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batc
     const uint32_t cu = (uint32_t)ctx->cu_count;
     const uint32_t needed1 = ((M + cu - 1u) / cu + step - 1u) / step;  // steps per CU, one token
     const bool rolled = c.maxJ == ER_CU_MAX_STEPS;
+    // Q4_K / Q8_0 by default: the unrolled kernels at any share of 3 steps or
+    // more, beyond maxJ as several workgroups per CU (their rolled loop measured
+    // no faster than the lane-group kernels; split evenly, the unrolled ones
+    // took Q8_0 20480 / 28672 x 4096 from 18.3 / 23.5 to 16.5 / 22.1 us)
     const bool use = ctx->cu_mode == 1 ? (rolled || needed1 <= c.maxJ)
                      : f == Fmt::Q6_K  ? (needed1 >= 3u && (rolled || needed1 <= c.maxJ))
-                                       : (needed1 <= c.maxJ && (needed1 >= 3u || K > 8192u));
+                                       : (needed1 >= 3u || K > 8192u);
     if (!use) return false;
-    // unrolled kernels up to maxJ steps, the rolled one up to ER_CU_MAX_ROLLED,
-    // more workgroups beyond (a CU's steps split evenly over them)
+    // unrolled kernels up to maxJ steps, the rolled one (Q6_K, or any format
+    // when the family is forced) up to ER_CU_MAX_ROLLED, more workgroups
+    // beyond (a CU's steps split evenly over them)
     const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
-    const uint32_t maxSteps = rolled ? ER_CU_MAX_ROLLED : c.maxJ;
+    const uint32_t maxSteps = rolled && (f == Fmt::Q6_K || ctx->cu_mode == 1) ? ER_CU_MAX_ROLLED : c.maxJ;
     const uint32_t steps = even_steps(((M + perToken - 1u) / perToken + step - 1u) / step, maxSteps);
     p.ci = ci;
     p.rowsPerWg = step * steps;
