@@ -18,7 +18,10 @@ timed call reads weights that >= 768 MB of other reads have pushed out of the
 distinct bytes one such cycle reads.
 
 Also reported in `results`: the other BASELINE GEMV shapes (Q8_0 3072x1024 and
-14336x4096, Q4_K 4096x14336, Q6_K 151936x1024 and 128256x4096).
+14336x4096, Q4_K 4096x14336, Q6_K 151936x1024 and 128256x4096), the Q6_K
+top-1 heads, the Q8_0 row quantizer, the dequantisation of the 14336x4096
+matrix in each format, the prefill GEMMs, the GGUF upload, the decode chain
+and the ceilings.
 
 The cpu_baseline leg times the CPU oracle (a C restatement of the reference's
 Swift CPU dequant+dot loop, oracle/er_oracle.c) on a bounded sample of the
@@ -70,6 +73,14 @@ TOP1_WORKLOADS = [
 QUANT_WORKLOADS = [
     ("q8_0_quantize_512x4096", 512, 4096, 4),
     ("q8_0_quantize_8192x4096", 8192, 4096, 4),
+]
+
+# Dequantisation to fp32 of the headline matrix in each format: (name, fmt,
+# M, K, BASELINE config index of the format's synthetic weights)
+DEQUANT_WORKLOADS = [
+    ("q8_0_dequant_14336x4096", "q8_0", 14336, 4096, 1),
+    ("q4_k_dequant_14336x4096", "q4_k", 14336, 4096, 2),
+    ("q6_k_dequant_14336x4096", "q6_k", 14336, 4096, 3),
 ]
 
 # (name, fmt, T tokens, N, K, BASELINE config index)
@@ -212,6 +223,41 @@ def bench_quant(ctx, rows: int, K: int, cfg: int, steps: int, warmup: int) -> di
     return {"rows": rows, "K": K, **rotation_fields(copies, src.nbytes, steps), "bytes_per_call": nbytes,
             "us_per_call": avg_us,
             "GBps": nbytes / (avg_us * 1e-6) / 1e9,
+            "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
+DEQUANT_KERNELS = {"q8_0": "DequantQ8_0Kernel", "q4_k": "DequantQ4KMKernel", "q6_k": "DequantQ6KKernel"}
+
+
+def dequant_bytes(fmt: str, M: int, K: int) -> int:
+    """Least HBM traffic of one dequantisation: the blocks read once, fp32 written once."""
+    return weight_bytes(fmt, M, K) + 4 * M * K
+
+
+def bench_dequant(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: int) -> dict:
+    """Dequantisation of an M x K matrix to fp32 (er_hip_dequant_*), rotating
+    block copies (>= 768 MB, so every call reads HBM), in a HIP graph.  Bytes
+    per call: the blocks read + 4 per weight written."""
+    import edgerunner_amd
+    import edgerunner_amd.synth as synth
+
+    kern = getattr(edgerunner_amd, DEQUANT_KERNELS[fmt])(ctx)
+    W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
+    count = M * K // BLOCK[fmt][1]
+    copies = max(2, -(-ROTATE_BYTES // W.nbytes))
+    stream = ctx.stream()
+    wbufs = [ctx.upload(W, stream) for _ in range(copies)]
+    out = ctx.alloc(4 * M * K)
+    for i in range(warmup):
+        kern.encode(stream, wbufs[i % copies], count, out)
+    stream.synchronize()
+    avg_us = rotation_time_us(ctx, stream, lambda i: kern.encode(stream, wbufs[i % copies], count, out), steps, copies)
+    nbytes = dequant_bytes(fmt, M, K)
+    for b in wbufs + [out]:
+        b.free()
+    stream.destroy()
+    return {"fmt": fmt, "M": M, "K": K, **rotation_fields(copies, W.nbytes, steps), "bytes_per_call": nbytes,
+            "us_per_call": avg_us, "GBps": nbytes / (avg_us * 1e-6) / 1e9,
             "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
@@ -719,11 +765,11 @@ def load_traffic(name: str):
 COPY_CAL_BYTES = 64 << 20
 
 
-def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None, chain_steps: int = 0) -> None:
+def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None, chain_steps: int = 0, dq_todo=()) -> None:
     """Counter-collection driver (run under `rocprofv3 --pmc ...`): three
     device-to-device copies of COPY_CAL_BYTES (the calibration kernel of known
     traffic), then for each GEMV workload (rotating weights) and each GEMM
-    workload in `gemm_todo`: one empty kernel (er_probe_empty) that marks
+    workload in `gemm_todo` and dequantisation in `dq_todo`: one empty kernel (er_probe_empty) that marks
     where the workload's dispatches begin, then its `steps` calls; with
     chain_steps, the same for that many eager steps of the fused decode chain.  The workload names
     and step counts go to `order_file` (one `name steps` line each), which
@@ -760,6 +806,23 @@ def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None, chain_steps: int
             b.free()
         xb.free()
         yb.free()
+    for name, fmt, M, K, cfg in dq_todo:
+        import edgerunner_amd
+        kern = getattr(edgerunner_amd, DEQUANT_KERNELS[fmt])(ctx)
+        W = synth.weights(fmt, synth.seed(cfg, 0), M, K, **DSCALE[fmt])
+        count = M * K // BLOCK[fmt][1]
+        copies = max(2, -(-ROTATE_BYTES // W.nbytes))
+        wbufs = [ctx.upload(W, stream) for _ in range(copies)]
+        out = ctx.alloc(4 * M * K)
+        stream.synchronize()
+        separator()
+        for i in range(steps):
+            kern.encode(stream, wbufs[i % copies], count, out)
+        stream.synchronize()
+        order.append((name, steps))
+        log(f"probe {name}: {steps} calls")
+        for b in wbufs + [out]:
+            b.free()
     if gemm_todo:
         from edgerunner_amd import QuantGEMMKernel
         gemm = QuantGEMMKernel(ctx)
@@ -906,6 +969,7 @@ def summarize(root: Path) -> str:
         out.append("|---|---|---|---|")
         alg = {w[0]: algorithmic_bytes(w[1], w[2], w[3]) for w in GEMV_WORKLOADS}
         alg.update({w[0]: gemm_min_bytes(w[1], w[2], w[3], w[4]) for w in GEMM_WORKLOADS})
+        alg.update({w[0]: dequant_bytes(w[1], w[2], w[3]) for w in DEQUANT_WORKLOADS})
         from edgerunner_amd.chain import ChainSpec
         alg["decode_chain_fused_eager"] = ChainSpec().weight_bytes()
         for name, v in per_workload.items():
@@ -967,8 +1031,10 @@ def main() -> int:
     if args.probe:
         gemm_todo = [w for w in GEMM_WORKLOADS if args.workloads not in ("all", "headline")
                      and w[0] in args.workloads.split(",")]
+        dq_todo = [w for w in DEQUANT_WORKLOADS if args.workloads not in ("all", "headline")
+                   and w[0] in args.workloads.split(",")]
         chain_steps = 3 if "decode_chain" in args.workloads.split(",") else 0
-        probe(ctx, todo, args.steps, gemm_todo, args.probe_order, chain_steps)
+        probe(ctx, todo, args.steps, gemm_todo, args.probe_order, chain_steps, dq_todo)
         return 0
     results = {}
     for name, fmt, M, K, cfg in todo:
@@ -993,6 +1059,16 @@ def main() -> int:
             continue
         log(f"{name}: running")
         r = bench_quant(ctx, rows, K, cfg, max(20, args.steps // 2), min(args.warmup, 5))
+        results[name] = r
+        log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
+            f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s)")
+
+    for name, fmt, M, K, cfg in DEQUANT_WORKLOADS:
+        if args.workloads not in ("all",) and name not in args.workloads.split(","):
+            continue
+        log(f"{name}: running")
+        r = bench_dequant(ctx, fmt, M, K, cfg, max(20, args.steps // 4), min(args.warmup, 5))
+        r["traffic_bytes"] = load_traffic(name)
         results[name] = r
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
             f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s)")
