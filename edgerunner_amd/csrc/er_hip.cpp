@@ -324,7 +324,7 @@ void pick_lanes(uint32_t S, uint32_t M, uint32_t maxN, int cu, uint32_t &L, uint
 // that still give every CU two workgroups per token, else R = 1): one token,
 // Q4_K 5120-8192 x 1024 and 3072-3584 x 2048 17-18% faster at 2 rows,
 // 12288-16384 x 1024 and 8192 x 2048 10-14% faster at 4 rows; 2-8 tokens of
-// 1024-4096 x 1024, 10-28% faster.
+// 2048-4096 x 1024, 11-18% faster.
 struct I8Cand {
     int idx;       // index into its configuration table
     uint32_t r;    // rows per lane group
@@ -343,19 +343,15 @@ int pick_rows(const I8Cand (&c)[N], int n, int cu) {
     return best >= 0 ? best : fewest;
 }
 
-// Rows of all tokens, for pick_lanes (its workgroup counts are proportional to
-// the rows), saturated to 32 bits.
-uint32_t all_rows(uint32_t M, uint32_t tokens) {
-    return (uint32_t)std::min<uint64_t>((uint64_t)M * std::max<uint32_t>(tokens, 1u), 0xffffffffull);
-}
-
 // Picks the integer-dot configuration for a row of S 64-weight slots, M rows
-// and `tokens` tokens: the lane split (LPR, NS) of pick_lanes over the rows of
-// all tokens, then the rows per lane group of pick_rows.  Returns -1 when no
-// configuration covers S.
+// and `tokens` tokens: the lane split (LPR, NS) of pick_lanes for one token's
+// rows -- so a row's arithmetic (its slots per lane and lane reduction) is the
+// same for batched and per-token calls -- then the rows per lane group of
+// pick_rows over all tokens' workgroups.  Returns -1 when no configuration
+// covers S.
 int pick_i8(uint32_t S, uint32_t M, int cu, uint32_t tokens) {
     uint32_t bestL = 0, bestN = 0;
-    pick_lanes(S, all_rows(M, tokens), 8, cu, bestL, bestN);
+    pick_lanes(S, M, 8, cu, bestL, bestN);
     if (!bestL) return -1;
     const uint32_t G = 64u / bestL;
     I8Cand c[8];
@@ -370,7 +366,8 @@ int pick_i8(uint32_t S, uint32_t M, int cu, uint32_t tokens) {
 }
 
 // Multi-matrix / GeGLU configuration for S slots, Mt total row computations
-// and `tokens` tokens: as pick_i8, over kI8MultiCfg (R in {4, 2}) and, when
+// and `tokens` tokens: as pick_i8 (lane split from one token's rows), over
+// kI8MultiCfg (R in {4, 2}) and, when
 // the kernel's rows stand alone (r1Ok), the one-row forms kI8Multi1Cfg.  Sets
 // ci (kI8MultiCfg) or ci1 (kI8Multi1Cfg); both -1 when nothing covers S.
 struct MultiPick {
@@ -379,7 +376,7 @@ struct MultiPick {
 MultiPick pick_i8_multi(uint32_t S, uint32_t Mt, int cu, bool r1Ok, uint32_t tokens) {
     MultiPick p;
     uint32_t bestL = 0, bestN = 0;
-    pick_lanes(S, all_rows(Mt, tokens), 4, cu, bestL, bestN);
+    pick_lanes(S, Mt, 4, cu, bestL, bestN);
     if (!bestL) return p;
     const uint32_t G = 64u / bestL, T = std::max<uint32_t>(tokens, 1u);
     I8Cand c[8];

@@ -142,8 +142,10 @@ def test_one_hot_returns_dequantised_column_exactly(gemv, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["q8_0", "q4_k", "q6_k"])
-def test_batched_equals_per_token(gemv, fmt):
-    M, K, T = 300, 1024, 5
+@pytest.mark.parametrize("M,K,T", [(300, 1024, 5), (3072, 1024, 4), (2048, 1024, 8), (4096, 1024, 2)])
+def test_batched_equals_per_token(gemv, fmt, M, K, T):
+    """Batched rows equal per-token rows bit for bit, also at shapes where the
+    batch changes the number of rows each lane group computes."""
     W = synth.weights(fmt, synth.seed(33, 0), M, K, **DSCALE[fmt])
     x = synth.normal_f32(synth.seed(33, 1), T * K)
     yb = getattr(gemv, EXEC_B[fmt])(W, x, T, M, K).reshape(T, M)
