@@ -503,14 +503,16 @@ er_status validate_gemv(Fmt f, er_buffer W, er_buffer x, er_buffer y, uint32_t b
 }
 
 // CU-resident family (er_gemv.hip gemv_cu) for one call: rows of K % 256 == 0
-// up to kCuMaxK with a configuration covering K / 64 slots.  Taken when a CU's
-// share of one token's rows is 3..ER_CU_MAX_STEPS row steps, or, for Q4_K /
-// Q8_0 rows longer than 8192 weights (whose per-workgroup x staging the
-// lane-group family repeats ~512 times), any share up to the unrolled steps.
-// Q6_K takes the rolled kernel beyond ER_CU_MAX_STEPS steps (the lane-group
-// Q6_K kernel waits for its weight loads before converting x); for Q4_K /
-// Q8_0 the rolled loop measured no faster than the lane-group family and runs
-// only when ER_HIP_GEMV_CU=1 forces the family.  The choice of configuration
+// up to kCuMaxK with a configuration covering K / 64 slots.  Q4_K / Q8_0 take
+// it when a CU's share of one token's rows is 3 row steps or more (Q4_K rows
+// longer than 8192 weights, whose per-workgroup x staging the lane-group
+// family repeats ~512 times, at any share; these reach this plan only when the
+// K-sliced kernels are switched off), beyond the unrolled kernels' steps as
+// several workgroups per CU with the steps split evenly; their rolled loop
+// measured no faster than the lane-group family and runs only when
+// ER_HIP_GEMV_CU=1 forces the family.  Q6_K takes it at 3 steps or more, the
+// rolled kernel beyond ER_CU_MAX_STEPS steps (the lane-group Q6_K kernel
+// waits for its weight loads before converting x).  The choice of configuration
 // and family depends on M and K only, so a batched call, its per-token calls
 // and the Q6_K top-1 over the same matrix run the same per-row arithmetic;
 // the batch only changes the row partition (about one workgroup per CU over
