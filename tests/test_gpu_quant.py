@@ -42,6 +42,32 @@ def test_destination_row_base_keeps_other_rows(quant):
     assert np.array_equal(got[: base * bpr * 34], before[: base * bpr * 34])
 
 
+@pytest.mark.parametrize("offset,base,rows,bpr", [(0, 0, 37, 24), (2, 0, 37, 24), (16, 0, 37, 24),
+                                                  (0, 2, 37, 4), (0, 1, 37, 4), (34, 1, 40, 8),
+                                                  (0, 0, 3, 3), (16, 2, 130, 32)])
+def test_destination_alignments(ctx, quant, offset, base, rows, bpr):
+    """Destinations whose first written block is 16-byte aligned or not (a
+    byte offset into the buffer, a destination row base), with block counts
+    that are not multiples of a wave's 8 blocks or a workgroup's 64: every
+    written byte matches the oracle, every other byte is kept."""
+    src = synth.normal_f32(synth.seed(50, 30 + offset + base), rows * bpr * 32)
+    n = offset + (base + rows) * bpr * 34 + 40
+    before = synth.q8_0(synth.seed(50, 31), (n + 33) // 34, 32)[:n].copy()
+    sb, db = ctx.upload(src), ctx.upload(before)
+    try:
+        quant.encode(None, sb, db.view(offset), rows, bpr * 32, base, bpr)
+        ctx.synchronize()
+        got = db.download(np.uint8)
+    finally:
+        sb.free()
+        db.free()
+    exp = before.copy()
+    region = exp[offset:offset + (base + rows) * bpr * 34]
+    exp[offset:offset + (base + rows) * bpr * 34] = ref.quantize_q8_0_rows(src, rows, bpr * 32, base, bpr,
+                                                                            dst=region.copy())
+    assert np.array_equal(got, exp)
+
+
 def test_unaligned_source_uses_scalar_kernel(ctx, quant):
     rows, bpr = 9, 4
     src = synth.normal_f32(synth.seed(50, 22), rows * bpr * 32 + 1)
