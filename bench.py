@@ -20,8 +20,9 @@ distinct bytes one such cycle reads.
 Also reported in `results`: the other BASELINE GEMV shapes (Q8_0 3072x1024 and
 14336x4096, Q4_K 4096x14336, Q6_K 151936x1024 and 128256x4096), the Q6_K
 top-1 heads, the Q8_0 row quantizer, the dequantisation of the 14336x4096
-matrix in each format, the prefill GEMMs, the GGUF upload, the decode chain
-and the ceilings.
+matrix in each format, the fused projections at Llama-3-8B shapes (Q4_K
+triple / dual / dual GeGLU, Q8_0 RMSNorm + QKV and RMSNorm + gate-up-SiLU),
+the prefill GEMMs, the GGUF upload, the decode chain and the ceilings.
 
 The cpu_baseline leg times the CPU oracle (a C restatement of the reference's
 Swift CPU dequant+dot loop, oracle/er_oracle.c) on a bounded sample of the
@@ -81,6 +82,19 @@ DEQUANT_WORKLOADS = [
     ("q8_0_dequant_14336x4096", "q8_0", 14336, 4096, 1),
     ("q4_k_dequant_14336x4096", "q4_k", 14336, 4096, 2),
     ("q6_k_dequant_14336x4096", "q6_k", 14336, 4096, 3),
+]
+
+# Fused projections at Llama-3-8B shapes (hidden 4096, q 4096, kv 1024, FFN
+# 14336; the BASELINE GEMV shapes): (name, kind, fmt, rows of each matrix, K,
+# BASELINE config index of the format's synthetic weights).  Kinds: the Q4_K
+# triple / dual / dual GeGLU entries, and the Q8_0 RMSNorm + QKV (fp16 V) and
+# RMSNorm + gate-up-SiLU pipelines, one token each.
+FUSED_WORKLOADS = [
+    ("q4_k_triple_4096+1024+1024x4096", "triple", "q4_k", (4096, 1024, 1024), 4096, 2),
+    ("q4_k_dual_2x14336x4096", "dual", "q4_k", (14336, 14336), 4096, 2),
+    ("q4_k_dual_geglu_2x14336x4096", "geglu", "q4_k", (14336, 14336), 4096, 2),
+    ("q8_0_fused_qkv_4096+1024+1024x4096", "qkv", "q8_0", (4096, 1024, 1024), 4096, 1),
+    ("q8_0_fused_gate_up_silu_2x14336x4096", "silu", "q8_0", (14336, 14336), 4096, 1),
 ]
 
 # (name, fmt, T tokens, N, K, BASELINE config index)
@@ -259,6 +273,64 @@ def bench_dequant(ctx, fmt: str, M: int, K: int, cfg: int, steps: int, warmup: i
     return {"fmt": fmt, "M": M, "K": K, **rotation_fields(copies, W.nbytes, steps), "bytes_per_call": nbytes,
             "us_per_call": avg_us, "GBps": nbytes / (avg_us * 1e-6) / 1e9,
             "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
+def fused_bytes(kind: str, fmt: str, rows, K: int) -> int:
+    """Least HBM traffic of one fused call: every matrix once, x once (and
+    the RMSNorm weight), the outputs once (fp16 V for the Q8_0 QKV; one
+    activated vector for GeGLU / SiLU)."""
+    w = sum(weight_bytes(fmt, M, K) for M in rows)
+    if kind in ("triple", "dual"):
+        out = 4 * sum(rows)
+    elif kind in ("geglu", "silu"):
+        out = 4 * rows[0]
+    else:  # qkv
+        out = 4 * (rows[0] + rows[1]) + 2 * rows[2]
+    return w + 4 * K + out + (4 * K if fmt == "q8_0" else 0)
+
+
+def bench_fused(ctx, kind: str, fmt: str, rows, K: int, cfg: int, steps: int, warmup: int) -> dict:
+    """One fused projection call (one x read for all its matrices) over
+    rotating sets of its matrices (>= 768 MB), in a HIP graph."""
+    import edgerunner_amd.synth as synth
+    from edgerunner_amd import FusedQ8Kernel, GEMVKernel
+
+    gemv, fq = GEMVKernel(ctx), FusedQ8Kernel(ctx)
+    Ws = [synth.weights(fmt, synth.seed(cfg, 10 + i), M, K, **DSCALE[fmt]) for i, M in enumerate(rows)]
+    set_bytes = sum(W.nbytes for W in Ws)
+    copies = max(2, -(-ROTATE_BYTES // set_bytes))
+    stream = ctx.stream()
+    sets = [[ctx.upload(W, stream) for W in Ws] for _ in range(copies)]
+    xb = ctx.upload(synth.normal_f32(synth.seed(cfg, 1), K), stream)
+    norm = ctx.upload((1.0 + 0.1 * synth.normal_f32(synth.seed(cfg, 2), K)).astype(np.float32), stream)
+    ys = [ctx.alloc(4 * M) for M in rows]
+    eps = 1e-5
+
+    def enc(i):
+        w = sets[i % copies]
+        if kind == "triple":
+            gemv.encodeQ4KWeightsTriple(stream, *w, xb, *ys, *rows, K)
+        elif kind == "dual":
+            gemv.encodeQ4KWeightsDual(stream, *w, xb, *ys, rows[0], K)
+        elif kind == "geglu":
+            gemv.encodeQ4KWeightsDualGeGLU(stream, *w, xb, ys[0], rows[0], K)
+        elif kind == "qkv":
+            fq.encodeFusedQKV(stream, *w, xb, *ys, norm, rows[0], rows[1], K, 1, eps)
+        else:  # silu
+            fq.encodeFusedGateUpSilu(stream, *w, xb, ys[0], norm, rows[0], K, 1, eps)
+
+    for i in range(warmup):
+        enc(i)
+    stream.synchronize()
+    avg_us = rotation_time_us(ctx, stream, enc, steps, copies)
+    finite = bool(np.all(np.isfinite(ys[0].download(np.float32, stream=stream))))
+    nbytes = fused_bytes(kind, fmt, rows, K)
+    for b in [b for w in sets for b in w] + [xb, norm] + ys:
+        b.free()
+    stream.destroy()
+    return {"kind": kind, "fmt": fmt, "rows": list(rows), "K": K, **rotation_fields(copies, set_bytes, steps),
+            "bytes_per_call": nbytes, "us_per_call": avg_us, "GBps": nbytes / (avg_us * 1e-6) / 1e9,
+            "frac_of_hbm_peak": nbytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS, "y_finite": finite}
 
 
 def bench_gguf_upload(ctx, gib: float, reps: int = 3) -> dict:
@@ -1068,6 +1140,16 @@ def main() -> int:
             continue
         log(f"{name}: running")
         r = bench_dequant(ctx, fmt, M, K, cfg, max(20, args.steps // 4), min(args.warmup, 5))
+        r["traffic_bytes"] = load_traffic(name)
+        results[name] = r
+        log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "
+            f"({100 * r['frac_of_hbm_peak']:.1f}% of 8 TB/s)")
+
+    for name, kind, fmt, rows, K, cfg in FUSED_WORKLOADS:
+        if args.workloads not in ("all",) and name not in args.workloads.split(","):
+            continue
+        log(f"{name}: running")
+        r = bench_fused(ctx, kind, fmt, rows, K, cfg, max(20, args.steps // 4), min(args.warmup, 5))
         r["traffic_bytes"] = load_traffic(name)
         results[name] = r
         log(f"{name}: {r['us_per_call']:.2f} us/call, {r['GBps']:.0f} GB/s "

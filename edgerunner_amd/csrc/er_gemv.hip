@@ -1438,9 +1438,11 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
 // 4).  Quads of 4 consecutive rows stay in one workgroup: with PAR = 2 the
 // steps pair up, step j taking rows ((j / 2) * gridDim.x + blockIdx.x) * 4 +
 // 2 (j % 2) + g, and J is even.  The row values are the plain kernel's.
-template <class F, int PAR, int J, bool TOP1 = false>
-ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
-                     uint32_t M, uint32_t K, float *__restrict__ pv = nullptr, uint32_t *__restrict__ pi = nullptr) {
+// Rows: where row r's bytes are and where its value goes (CukOne: one
+// matrix; CukMulti: up to three matrices of one row length, concatenated).
+template <class F, int PAR, int J, bool TOP1, class Rows>
+ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_t M, uint32_t K,
+                          float *__restrict__ pv, uint32_t *__restrict__ pi) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     constexpr uint32_t LPR = 64u / PAR;  // lanes per row slice
     __shared__ float part[ER_CU_WAVES][PAR * J];  // [wave][local row PAR j + g]
@@ -1455,7 +1457,6 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
     constexpr int VPL = PAR == 8 ? 8 : 16;  // values per lane per pass
     constexpr int NPASS = PAR == 2 ? 2 : 1;
     x += (size_t)blockIdx.y * K;
-    y += (size_t)blockIdx.y * M;
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t g = lane / LPR, li = lane % LPR;
     const uint32_t S = K >> 6;
@@ -1465,7 +1466,6 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
         return (TOP1 && PAR == 2) ? ((j >> 1) * gridDim.x + blockIdx.x) * 4u + 2u * (j & 1u) + gg
                                   : (j * gridDim.x + blockIdx.x) * (uint32_t)PAR + gg;
     };
-    const size_t rowBytes = F::row_bytes(K);
     float res = 0.0f;
     float4 share = float4{0.0f, 0.0f, 0.0f, 0.0f};  // this wave's share of the launch's checks
     if (s0 < S) {
@@ -1497,7 +1497,7 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
         typename F::Wt wb[D];
         auto issue = [&](uint32_t j, int b) {
             const uint32_t row = min(rowAt(j, g), M - 1u);
-            wb[b] = F::load(W + (size_t)row * rowBytes, sc);
+            wb[b] = F::load(rows.row(row), sc);
         };
 #pragma unroll
         for (int v = 0; v < D; ++v) {
@@ -1555,7 +1555,7 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
             // the group's lanes splitting the 16-value chunks
             const uint32_t rc = min(row, M - 1u);
             float sp1[1] = {0.0f}, h = 0.0f;
-            nf_terms<1>([&](int, uint32_t k) { return weight_at<F::FMT>(W + (size_t)rc * rowBytes, k); },
+            nf_terms<1>([&](int, uint32_t k) { return weight_at<F::FMT>(rows.row(rc), k); },
                         [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, li, LPR, sp1, h, ill);
             const float fv = group_sum<LPR>(sp1[0]);
             h = group_sum<LPR>(h);
@@ -1564,13 +1564,50 @@ ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x,
         if constexpr (TOP1) {
             if (li == 0) tv[lr] = v;
         } else {
-            if (li == 0 && row < M) y[row] = v;
+            if (li == 0 && row < M) rows.store(row, v);
         }
     }
     if constexpr (TOP1) {
         __syncthreads();
         top1_partial(tv, PAR * J / 4u, M, [&](uint32_t l) { return rowAt(l / PAR, l % PAR); }, pv, pi);
     }
+}
+
+struct CukOne {
+    const uint8_t *W;
+    float *y;
+    size_t rowBytes;
+    __device__ __forceinline__ const uint8_t *row(uint32_t r) const { return W + (size_t)r * rowBytes; }
+    __device__ __forceinline__ void store(uint32_t r, float v) const { y[r] = v; }
+};
+
+// Rows [0, M0) of W[0], then M1 of W[1], then M2 of W[2]; each row's value
+// is the one the matrix's own K-sliced launch gives it.
+struct CukMulti {
+    const Q4Multi &mm;
+    size_t rowBytes;
+    __device__ __forceinline__ uint32_t seg(uint32_t r, uint32_t &l) const {
+        const uint32_t m1 = mm.M[0], m2 = m1 + mm.M[1];
+        l = r < m1 ? r : (r < m2 ? r - m1 : r - m2);
+        return r < m1 ? 0u : (r < m2 ? 1u : 2u);
+    }
+    __device__ __forceinline__ const uint8_t *row(uint32_t r) const {
+        uint32_t l;
+        const uint32_t m = seg(r, l);
+        return (m == 0u ? mm.W[0] : (m == 1u ? mm.W[1] : mm.W[2])) + (size_t)l * rowBytes;
+    }
+    __device__ __forceinline__ void store(uint32_t r, float v) const {
+        uint32_t l;
+        const uint32_t m = seg(r, l);
+        (m == 0u ? mm.y[0] : (m == 1u ? mm.y[1] : mm.y[2]))[l] = v;
+    }
+};
+
+template <class F, int PAR, int J, bool TOP1 = false>
+ER_DEV void gemv_cuk(const uint8_t *__restrict__ W, const float *__restrict__ x, float *__restrict__ y,
+                     uint32_t M, uint32_t K, float *__restrict__ pv = nullptr, uint32_t *__restrict__ pi = nullptr) {
+    const CukOne rows{W, y + (size_t)blockIdx.y * M, F::row_bytes(K)};
+    gemv_cuk_rows<F, PAR, J, TOP1>(rows, x, M, K, pv, pi);
 }
 
 // ===========================================================================
@@ -2171,6 +2208,25 @@ ER_CUK_ENTRIES8(q4k, CuQ4K, 8)
 ER_CUK_ENTRIES16(q8_0, CuQ8, 2)
 ER_CUK_ENTRIES16(q8_0, CuQ8, 4)
 ER_CUK_ENTRIES8(q8_0, CuQ8, 8)
+// The Q4_K dual / triple over the K-sliced kernels: er_gemv_q4k_multi_cuk<PAR>_j<J>
+// (mm, x, K), rows of the matrices concatenated, one token.
+#define ER_CUK_MULTI_ENTRY(PAR, J)                                                          \
+    extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                                 \
+        er_gemv_q4k_multi_cuk##PAR##_j##J(Q4Multi mm, const float *__restrict__ x, uint32_t K) {     \
+        const CukMulti rows{mm, CuQ4K::row_bytes(K)};                                               \
+        gemv_cuk_rows<CuQ4K, PAR, J, false>(rows, x, mm.M[0] + mm.M[1] + mm.M[2], K, nullptr, nullptr); \
+    }
+#define ER_CUK_MULTI8(PAR)                                                                                   \
+    ER_CUK_MULTI_ENTRY(PAR, 1) ER_CUK_MULTI_ENTRY(PAR, 2) ER_CUK_MULTI_ENTRY(PAR, 3)             \
+    ER_CUK_MULTI_ENTRY(PAR, 4) ER_CUK_MULTI_ENTRY(PAR, 5) ER_CUK_MULTI_ENTRY(PAR, 6)             \
+    ER_CUK_MULTI_ENTRY(PAR, 7) ER_CUK_MULTI_ENTRY(PAR, 8)
+#define ER_CUK_MULTI16(PAR)                                                                                  \
+    ER_CUK_MULTI8(PAR) ER_CUK_MULTI_ENTRY(PAR, 9) ER_CUK_MULTI_ENTRY(PAR, 10)                        \
+    ER_CUK_MULTI_ENTRY(PAR, 11) ER_CUK_MULTI_ENTRY(PAR, 12) ER_CUK_MULTI_ENTRY(PAR, 13)          \
+    ER_CUK_MULTI_ENTRY(PAR, 14) ER_CUK_MULTI_ENTRY(PAR, 15) ER_CUK_MULTI_ENTRY(PAR, 16)
+ER_CUK_MULTI16(2)
+ER_CUK_MULTI16(4)
+ER_CUK_MULTI8(8)
 // Q6_K: rows of more than 64 slots (2 and 4 rows per step), and the top-1
 // forms (er_gemv_q6k_top1_cuk<PAR>_j<J>: (W, x, pv, pi, M, K), even J for PAR 2)
 ER_CUK_ENTRIES16(q6k, CuQ6K, 2)

@@ -216,6 +216,7 @@ struct er_hip_ctx {
     hipFunction_t fnQ6KCu[kCuCountQ6K][ER_CU_MAX_STEPS + 1] = {};
     hipFunction_t fnQ6KTop1Cu[kCuCountQ6K][ER_CU_MAX_STEPS + 1] = {};
     hipFunction_t fnQ4KCuk[3][ER_CUK_MAX_STEPS] = {};  // [2, 4, 8 rows per step][row steps - 1]
+    hipFunction_t fnQ4KCukMulti[3][ER_CUK_MAX_STEPS] = {};  // the dual / triple over them
     hipFunction_t fnQ8Cuk[3][ER_CUK_MAX_STEPS] = {};
     hipFunction_t fnQ6KCuk[2][ER_CUK_MAX_STEPS] = {};      // [2, 4 rows per step][row steps - 1]
     hipFunction_t fnQ6KTop1Cuk[2][ER_CUK_MAX_STEPS] = {};  // even steps only for 2 rows per step
@@ -1057,7 +1058,9 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
 }
 
 // Fused Q4_K projections: validation of each weight as encodeQ4KWeights, then
-// one multi-matrix launch (fp32 fallback: one GEMV per matrix).
+// one launch over all the matrices' rows -- the K-sliced kernels for large
+// totals, else the multi-matrix lane-group kernels (fp32 fallback: one GEMV
+// per matrix).
 er_status encode_q4k_multi(er_hip_ctx *ctx, er_stream stream, const er_buffer *Ws, er_buffer x,
                            const er_buffer *ys, const uint32_t *Ms, int count, uint32_t K) {
     for (int i = 0; i < count; ++i) {
@@ -1072,6 +1075,36 @@ er_status encode_q4k_multi(er_hip_ctx *ctx, er_stream stream, const er_buffer *W
     if (Mt > 0xffffffffull) return fail(ER_ERR_INVALID_MATRIX_SHAPE, "Q4_K multi: too many rows");
     st = bind_device(ctx);
     if (st != ER_OK) return st;
+    Q4MultiArgs a{};
+    for (int i = 0; i < 3; ++i) {
+        const int j = i < count ? i : 0;
+        a.W[i] = Ws[j].data;
+        a.y[i] = ys[j].data;
+        a.M[i] = i < count ? Ms[i] : 0u;
+    }
+    // From 24 rows per CU, and where each wave's slice of K fills at least 7/8
+    // of its row slice's lanes (K = 4096, 7680, 8192, 14336, 16384 ...), when
+    // one matrix of all the rows would take the K-sliced kernels, the matrices
+    // run there as one launch over their concatenated rows (each row's value
+    // is the one a K-sliced call gives it, a function of K alone); with
+    // ER_HIP_GEMV_CUK=2 wherever that plan takes them; never when a
+    // multi-matrix configuration is forced.  Same-box A/B against the
+    // multi-matrix kernels, medians of 4 (us): K = 4096: 2 x 14336 rows 18.62
+    // -> 17.38, 4096 + 2 x 1024 6.97 -> 6.54, 2 x 4096 7.50 -> 7.28, but 2 x
+    // 2048 4.81 -> 5.19 and 1536 + 2 x 512 4.34 -> 4.87; K = 8192: 2 x 3100
+    // 11.11 -> 10.55; K = 14336: 2 x 3100 20.49 -> 17.43; K = 7680: 5120 + 2 x
+    // 1024 11.09 -> 10.79; K = 5120 (10 of 16 lanes): the same rows 8.88 -> 10.28.
+    const uint32_t rowsPerCu = (uint32_t)((Mt + (uint64_t)ctx->cu_count - 1u) / (uint64_t)ctx->cu_count);
+    const uint32_t S = K / 64u, sliceLanes = S <= 64u ? 8u : (S <= 128u ? 16u : 32u);
+    const bool fullSlices = 8u * ((S + 7u) / 8u) >= 7u * sliceLanes;
+    CukPlan kp;
+    if (ctx->multi_override < 0 && ctx->multi1_override < 0 &&
+        ((rowsPerCu >= 24u && fullSlices) || ctx->cuk_mode == 2) && plan_cuk(ctx, Fmt::Q4_K, (uint32_t)Mt, K, 1u, kp)) {
+        void *kargs[] = {&a, &x.data, &K};
+        dim3 grid((uint32_t)((Mt + kp.rowsPerWg - 1u) / kp.rowsPerWg), 1, 1);
+        return launch_fn(ctx->fnQ4KCukMulti[kp.pi][kp.j - 1], "er_gemv_q4k_multi_cuk", grid,
+                         dim3(64u * ER_CU_WAVES, 1, 1), xl_lds_bytes(K), stream, kargs);
+    }
     const MultiPick mp = K <= kI8MaxK ? pick_multi(ctx, K / 64u, (uint32_t)Mt, true, 1u) : MultiPick{};
     if (mp.ci < 0 && mp.ci1 < 0) {
         for (int i = 0; i < count; ++i) {
@@ -1081,13 +1114,6 @@ er_status encode_q4k_multi(er_hip_ctx *ctx, er_stream stream, const er_buffer *W
         return ER_OK;
     }
     const I8Cfg &c = mp.ci >= 0 ? kI8MultiCfg[mp.ci] : kI8Multi1Cfg[mp.ci1];
-    Q4MultiArgs a{};
-    for (int i = 0; i < 3; ++i) {
-        const int j = i < count ? i : 0;
-        a.W[i] = Ws[j].data;
-        a.y[i] = ys[j].data;
-        a.M[i] = i < count ? Ms[i] : 0u;
-    }
     const uint32_t rowsPerBlock = ER_GEMV_WAVES * (64u / c.lpr) * c.r;
     const uint32_t lds = xl_lds_bytes(K);
     void *args[] = {&a, &x.data, &K};
@@ -1407,15 +1433,17 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
     }
     for (int pi = 0; pi < 3; ++pi)
         for (int j = 1; j <= (pi == 2 ? 8 : ER_CUK_MAX_STEPS); ++j)
-            for (int kind = 0; kind < 4; ++kind) {
-                // q4k, q8_0 (2, 4, 8 rows per step); q6k and its top-1 (2, 4;
-                // the top-1 with 2 rows per step at even step counts)
-                if (kind >= 2 && (pi == 2 || (kind == 3 && pi == 0 && j % 2 != 0))) continue;
-                static const char *const kinds[4] = {"q4k", "q8_0", "q6k", "q6k_top1"};
+            for (int kind = 0; kind < 5; ++kind) {
+                // q4k, q8_0, the Q4_K dual / triple (2, 4, 8 rows per step);
+                // q6k and its top-1 (2, 4; the top-1 with 2 rows per step at
+                // even step counts)
+                if ((kind == 2 || kind == 3) && (pi == 2 || (kind == 3 && pi == 0 && j % 2 != 0))) continue;
+                static const char *const kinds[5] = {"q4k", "q8_0", "q6k", "q6k_top1", "q4k_multi"};
                 hipFunction_t *const slot = kind == 0   ? &ctx->fnQ4KCuk[pi][j - 1]
                                             : kind == 1 ? &ctx->fnQ8Cuk[pi][j - 1]
                                             : kind == 2 ? &ctx->fnQ6KCuk[pi][j - 1]
-                                                        : &ctx->fnQ6KTop1Cuk[pi][j - 1];
+                                            : kind == 3 ? &ctx->fnQ6KTop1Cuk[pi][j - 1]
+                                                        : &ctx->fnQ4KCukMulti[pi][j - 1];
                 char name[64];
                 std::snprintf(name, sizeof(name), "er_gemv_%s_cuk%d_j%d", kinds[kind], 2 << pi, j);
                 e = hipModuleGetFunction(slot, ctx->module, name);

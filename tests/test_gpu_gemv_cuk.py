@@ -8,7 +8,8 @@ mid-wave and a wave with no slice (K = 8448: 20 slots per wave, 132 slots);
 exact one-hot columns at the slice boundaries; the same row bit for bit
 whatever the row partition or the batch; non-finite and heavy-tailed x; the
 Q6_K top-1 on the same kernels equal to the selection rule over the plain
-call's logits."""
+call's logits; the Q4_K dual / triple over the same kernels equal to the
+single-matrix calls."""
 import os
 
 import numpy as np
@@ -250,3 +251,29 @@ def test_q6k_top1_ties_and_nan(gemv):
     assert gemv.executeQ6KWeightsTop1(Wt.reshape(-1), x, M, K) == min(a, hi)
     xn = np.full(K, np.nan, np.float32)
     assert gemv.executeQ6KWeightsTop1(W.reshape(-1), xn, M, K) == 0
+
+
+# (rows of each matrix -- the dual's two are of one height --, K, whether the
+# default plan takes the K-sliced kernels for the total rows: from 24 rows per
+# CU, with slices filling 7/8 of their lanes): steps that straddle two
+# matrices (3201 with 8 rows per step, 700 + 130 and 5001 with 4, 9 with 2),
+# every PAR, K = 16384
+@pytest.mark.parametrize("rows,K,default_cuk", [((4096, 1024, 1024), 4096, True), ((3201, 3201), 4096, True),
+                                                ((5001, 1000, 1000), 7680, True), ((3100, 3100), 8192, True),
+                                                ((5001, 1000, 1000), 5120, False),
+                                                ((700, 130, 130), 5120, False), ((300, 300), 8192, False),
+                                                ((9, 9), 16384, False), ((40, 17, 5), 1024, False)])
+def test_q4k_multi_over_k_sliced(gemv, cuk_everywhere, rows, K, default_cuk):
+    """Q4_K dual / triple where the total rows take the K-sliced kernels (one
+    launch over the concatenated rows): every row equal bit for bit to a
+    K-sliced call of its own matrix (a row's value depends on K alone) and
+    within the parity bar of the oracle.  With ER_HIP_GEMV_CUK=2 the shapes
+    below 24 rows per CU and the short-row one take them too."""
+    Ws = [synth.q4_k(synth.seed(52, i), m, K) for i, m in enumerate(rows)]
+    x = synth.normal_f32(synth.seed(52, 9), K)
+    singles = [cuk_everywhere.executeQ4KWeights(W, x, m, K) for W, m in zip(Ws, rows)]
+    for kern in ((gemv, cuk_everywhere) if default_cuk else (cuk_everywhere,)):
+        ys = kern.executeQ4KWeightsMulti(Ws, x, list(rows), K)
+        for W, m, y, s in zip(Ws, rows, ys, singles):
+            assert np.array_equal(y, s)
+            assert rel_l2(y, ref.gemv("q4_k", W, x, m, K)) < TOL
