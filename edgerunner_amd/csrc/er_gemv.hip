@@ -1439,7 +1439,14 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
 // steps pair up, step j taking rows ((j / 2) * gridDim.x + blockIdx.x) * 4 +
 // 2 (j % 2) + g, and J is even.  The row values are the plain kernel's.
 // Rows: where row r's bytes are and where its value goes (CukOne: one
-// matrix; CukMulti: up to three matrices of one row length, concatenated).
+// matrix; CukMulti: up to three matrices of one row length, concatenated;
+// CukQ8Multi / CukQ8Pairs: the fused Q8_0 projections).  Rows::NORM: x enters
+// as x * w (rows.normW, when set) and each row value is multiplied by the
+// launch's RMSNorm factor 1 / sqrt(mean(x^2) + eps), formed after the end
+// barrier from the waves' sums of x^2 over their slices, added in wave order.
+// Rows::PAIRS: rows 2i, 2i + 1 are a gate row and its up row (PAR is even, so
+// a pair never straddles a step); the even row's lane group stores
+// Rows::act(gate) * up.
 template <class F, int PAR, int J, bool TOP1, class Rows>
 ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_t M, uint32_t K,
                           float *__restrict__ pv, uint32_t *__restrict__ pi) {
@@ -1448,6 +1455,7 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
     __shared__ float part[ER_CU_WAVES][PAR * J];  // [wave][local row PAR j + g]
     __shared__ float4 chk[ER_CU_WAVES];           // [wave] its slice's checks: e, r, non-finite
     __shared__ float tv[TOP1 ? PAR * J : 1];      // top-1: the workgroup's row values
+    __shared__ float ssw[Rows::NORM ? ER_CU_WAVES : 1];  // RMSNorm: [wave] sum of x^2 over its slice
     static_assert(PAR == 2 || PAR == 4 || PAR == 8, "2, 4 or 8 rows per step");
     static_assert(J >= 1 && J <= (int)LPR && J <= ER_CUK_MAX_STEPS, "row sums parked one per lane of a slice");
     static_assert(!TOP1 || PAR > 2 || J % 2 == 0, "top-1 quads pair the steps of 2-row slices");
@@ -1468,6 +1476,7 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
     };
     float res = 0.0f;
     float4 share = float4{0.0f, 0.0f, 0.0f, 0.0f};  // this wave's share of the launch's checks
+    float ssq = 0.0f;                               // RMSNorm: this wave's sum of x^2
     if (s0 < S) {
         const uint32_t s = s0 + li;
         const uint32_t sc = min(s, s1 - 1u);
@@ -1483,6 +1492,17 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
             const uint32_t hc = min(h0 + 64u * p + lane, h1 - 1u);
 #pragma unroll
             for (int q = 0; q < VPL / 4; ++q) xr[p][q] = *(const float4 *)(x + VPL * hc + 4u * q);
+        }
+        float4 nw[Rows::NORM ? NPASS : 1][VPL / 4];  // the norm weights of the same pieces
+        if constexpr (Rows::NORM) {
+            if (rows.normW) {
+#pragma unroll
+                for (int p = 0; p < NPASS; ++p) {
+                    const uint32_t hc = min(h0 + 64u * p + lane, h1 - 1u);
+#pragma unroll
+                    for (int q = 0; q < VPL / 4; ++q) nw[p][q] = *(const float4 *)(rows.normW + VPL * hc + 4u * q);
+                }
+            }
         }
         // 2-row steps (the longest x slices, two passes per wave): every
         // wave's x requests leave the CU before any weight request.  The CU
@@ -1507,6 +1527,24 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
         // convert the slice (pieces past it are not stored: index K / VPL).
         // Every pass runs: a pass under a branch had its x loads sunk behind
         // the weight loads, and the conversion then waited for those too.
+        if constexpr (Rows::NORM) {
+            if (rows.normW) {
+                // sum of x^2 over the slice's pieces (each once: clamped copies
+                // past the slice are not counted), then x * w
+#pragma unroll
+                for (int p = 0; p < NPASS; ++p) {
+                    const bool own = h0 + 64u * p + lane < h1;
+#pragma unroll
+                    for (int q = 0; q < VPL / 4; ++q) {
+                        float4 &v = xr[p][q];
+                        const float4 w = nw[p][q];
+                        const float sq = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                        ssq += own ? sq : 0.0f;
+                        v = float4{v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w};
+                    }
+                }
+            }
+        }
         XlCheck ck;
 #pragma unroll
         for (int p = 0; p < NPASS; ++p) {
@@ -1538,10 +1576,23 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
     }
     if (li < (uint32_t)J) part[wave][PAR * li + g] = res;
     if (lane == 0) chk[wave] = share;
+    if constexpr (Rows::NORM) {
+        ssq = group_sum<64>(ssq);
+        if (lane == 0) ssw[wave] = ssq;
+    }
     __syncthreads();  // every wave's partials and check shares, limbs, chunk sums and scales are in LDS
     const XLimbs X = xl_view(lds, K);
     bool ill, nf;
     xl_check_decide(chk, ER_CU_WAVES, F::FMT == ER_FMT_Q8_0 ? 1.0f : 4.0f, ill, nf);
+    float rms = 1.0f;  // RMSNorm factor (Rows::NORM with a norm weight)
+    if constexpr (Rows::NORM) {
+        if (rows.normW) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int w = 0; w < ER_CU_WAVES; ++w) ss += ssw[w];
+            rms = 1.0f / __builtin_sqrtf(ss / (float)K + rows.eps);
+        }
+    }
     // lane group (wave, g) finishes steps wave, wave + 8, ..., row g
 #pragma unroll 1
     for (uint32_t st = wave; st < (uint32_t)J; st += ER_CU_WAVES) {
@@ -1550,19 +1601,28 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < ER_CU_WAVES; ++w) v += part[w][lr];
+        if constexpr (Rows::NORM) v *= rms;
         if (ill || nf) {
             // fp32 from the raw weights (every term, or the non-finite ones),
-            // the group's lanes splitting the 16-value chunks
+            // the group's lanes splitting the 16-value chunks; x as staged
+            // (x * rms * w under RMSNorm)
             const uint32_t rc = min(row, M - 1u);
             float sp1[1] = {0.0f}, h = 0.0f;
             nf_terms<1>([&](int, uint32_t k) { return weight_at<F::FMT>(rows.row(rc), k); },
-                        [&](uint32_t k) { return x[k]; }, X.x16, K >> 4, li, LPR, sp1, h, ill);
+                        [&](uint32_t k) {
+                            if constexpr (Rows::NORM) return rows.normW ? x[k] * rms * rows.normW[k] : x[k];
+                            else return x[k];
+                        },
+                        X.x16, K >> 4, li, LPR, sp1, h, ill);
             const float fv = group_sum<LPR>(sp1[0]);
             h = group_sum<LPR>(h);
             v = (ill || h > 0.0f) ? fv : v;
         }
         if constexpr (TOP1) {
             if (li == 0) tv[lr] = v;
+        } else if constexpr (Rows::PAIRS) {
+            const float up = __shfl_down(v, LPR);  // the up row: lane group g + 1
+            if ((g & 1u) == 0u && li == 0 && row < M) rows.store(row, Rows::act(v) * up);
         } else {
             if (li == 0 && row < M) rows.store(row, v);
         }
@@ -1574,6 +1634,7 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
 }
 
 struct CukOne {
+    static constexpr bool NORM = false, PAIRS = false;
     const uint8_t *W;
     float *y;
     size_t rowBytes;
@@ -1581,26 +1642,114 @@ struct CukOne {
     __device__ __forceinline__ void store(uint32_t r, float v) const { y[r] = v; }
 };
 
+// One of three values by index, taken as values (a conditional on the
+// members themselves selects their addresses and puts the row source in
+// memory: per-lane loads of the pointers, or scratch).
+template <class T>
+__device__ __forceinline__ T pick3(uint32_t m, T a, T b, T c) {
+    T v = a;
+    v = m == 1u ? b : v;
+    v = m == 2u ? c : v;
+    return v;
+}
+
 // Rows [0, M0) of W[0], then M1 of W[1], then M2 of W[2]; each row's value
-// is the one the matrix's own K-sliced launch gives it.
+// is the one the matrix's own K-sliced launch gives it.  Pointers and row
+// counts are held as values (uniform: scalar registers).
 struct CukMulti {
-    const Q4Multi &mm;
+    static constexpr bool NORM = false, PAIRS = false;
+    const uint8_t *W0, *W1, *W2;
+    float *y0, *y1, *y2;
+    uint32_t m1, m2;  // M0, M0 + M1
     size_t rowBytes;
+    __device__ __forceinline__ CukMulti(const Q4Multi &mm, size_t rb)
+        : W0(mm.W[0]), W1(mm.W[1]), W2(mm.W[2]), y0(mm.y[0]), y1(mm.y[1]), y2(mm.y[2]), m1(mm.M[0]),
+          m2(mm.M[0] + mm.M[1]), rowBytes(rb) {}
     __device__ __forceinline__ uint32_t seg(uint32_t r, uint32_t &l) const {
-        const uint32_t m1 = mm.M[0], m2 = m1 + mm.M[1];
         l = r < m1 ? r : (r < m2 ? r - m1 : r - m2);
         return r < m1 ? 0u : (r < m2 ? 1u : 2u);
     }
     __device__ __forceinline__ const uint8_t *row(uint32_t r) const {
         uint32_t l;
         const uint32_t m = seg(r, l);
-        return (m == 0u ? mm.W[0] : (m == 1u ? mm.W[1] : mm.W[2])) + (size_t)l * rowBytes;
+        return pick3(m, W0, W1, W2) + (size_t)l * rowBytes;
     }
     __device__ __forceinline__ void store(uint32_t r, float v) const {
         uint32_t l;
         const uint32_t m = seg(r, l);
-        (m == 0u ? mm.y[0] : (m == 1u ? mm.y[1] : mm.y[2]))[l] = v;
+        pick3(m, y0, y1, y2)[l] = v;
     }
+};
+
+// The fused Q8_0 rows (Q8Multi): matrices concatenated as CukMulti; token t =
+// blockIdx.y writes row l of matrix m at y[m] + t M[m] + l, fp16 when bit m of
+// halfMask is set, adding res[m][t M[m] + l] when res[m] is set.
+struct CukQ8Multi {
+    static constexpr bool NORM = true, PAIRS = false;
+    const uint8_t *W0, *W1, *W2;
+    void *y0, *y1, *y2;
+    const float *r0, *r1, *r2;
+    uint32_t M0, M1, M2, halfMask;
+    size_t rowBytes;
+    const float *normW;
+    float eps;
+    __device__ __forceinline__ CukQ8Multi(const Q8Multi &mm, size_t rb)
+        : W0(mm.W[0]), W1(mm.W[1]), W2(mm.W[2]), y0(mm.y[0]), y1(mm.y[1]), y2(mm.y[2]), r0(mm.res[0]),
+          r1(mm.res[1]), r2(mm.res[2]), M0(mm.M[0]), M1(mm.M[1]), M2(mm.M[2]), halfMask(mm.halfMask), rowBytes(rb),
+          normW(mm.normW), eps(mm.eps) {}
+    __device__ __forceinline__ uint32_t seg(uint32_t r, uint32_t &l) const {
+        const uint32_t m2 = M0 + M1;
+        l = r < M0 ? r : (r < m2 ? r - M0 : r - m2);
+        return r < M0 ? 0u : (r < m2 ? 1u : 2u);
+    }
+    __device__ __forceinline__ const uint8_t *row(uint32_t r) const {
+        uint32_t l;
+        const uint32_t m = seg(r, l);
+        return pick3(m, W0, W1, W2) + (size_t)l * rowBytes;
+    }
+    __device__ __forceinline__ void store(uint32_t r, float v) const {
+        uint32_t l;
+        const uint32_t m = seg(r, l);
+        const size_t out = (size_t)blockIdx.y * pick3(m, M0, M1, M2) + l;
+        const float *rp = pick3(m, r0, r1, r2);
+        void *yp = pick3(m, y0, y1, y2);
+        const float o = rp ? v + rp[out] : v;
+        if ((halfMask >> m) & 1u)
+            ((_Float16 *)yp)[out] = (_Float16)o;
+        else
+            ((float *)yp)[out] = o;
+    }
+};
+
+// Gate/up pairs: row 2i is gate row i, 2i + 1 up row i; token t writes
+// y[t M + i].  CukQ8Pairs: the fused Q8_0 SiLU (RMSNorm, silu);
+// CukGegluPairs: the Q4_K dual GeGLU (gelu_tanh, no norm).
+struct CukQ8Pairs {
+    static constexpr bool NORM = true, PAIRS = true;
+    __device__ __forceinline__ static float act(float g) { return silu(g); }
+    const uint8_t *Wg, *Wu;
+    float *y;
+    size_t rowBytes;
+    const float *normW;
+    float eps;
+    uint32_t M;
+    __device__ __forceinline__ const uint8_t *row(uint32_t r) const {
+        return pick3((r & 1u), Wg, Wu, Wu) + (size_t)(r >> 1) * rowBytes;
+    }
+    __device__ __forceinline__ void store(uint32_t r, float v) const { y[(size_t)blockIdx.y * M + (r >> 1)] = v; }
+};
+
+struct CukGegluPairs {
+    static constexpr bool NORM = false, PAIRS = true;
+    __device__ __forceinline__ static float act(float g) { return gelu_tanh(g); }
+    const uint8_t *Wg, *Wu;
+    float *y;
+    size_t rowBytes;
+    uint32_t M;
+    __device__ __forceinline__ const uint8_t *row(uint32_t r) const {
+        return pick3((r & 1u), Wg, Wu, Wu) + (size_t)(r >> 1) * rowBytes;
+    }
+    __device__ __forceinline__ void store(uint32_t r, float v) const { y[(size_t)blockIdx.y * M + (r >> 1)] = v; }
 };
 
 template <class F, int PAR, int J, bool TOP1 = false>
@@ -2209,12 +2358,20 @@ ER_CUK_ENTRIES16(q8_0, CuQ8, 2)
 ER_CUK_ENTRIES16(q8_0, CuQ8, 4)
 ER_CUK_ENTRIES8(q8_0, CuQ8, 8)
 // The Q4_K dual / triple over the K-sliced kernels: er_gemv_q4k_multi_cuk<PAR>_j<J>
-// (mm, x, K), rows of the matrices concatenated, one token.
+// (mm, x, K), rows of the matrices concatenated, one token; and the dual GeGLU,
+// er_gemv_q4k_geglu_cuk<PAR>_j<J> (Wg, Wu, x, y, M, K; 2M rows).
 #define ER_CUK_MULTI_ENTRY(PAR, J)                                                          \
     extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                                 \
         er_gemv_q4k_multi_cuk##PAR##_j##J(Q4Multi mm, const float *__restrict__ x, uint32_t K) {     \
-        const CukMulti rows{mm, CuQ4K::row_bytes(K)};                                               \
+        const CukMulti rows(mm, CuQ4K::row_bytes(K));                                               \
         gemv_cuk_rows<CuQ4K, PAR, J, false>(rows, x, mm.M[0] + mm.M[1] + mm.M[2], K, nullptr, nullptr); \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                                 \
+        er_gemv_q4k_geglu_cuk##PAR##_j##J(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu, \
+                                          const float *__restrict__ x, float *__restrict__ y, uint32_t M, \
+                                          uint32_t K) {                                            \
+        const CukGegluPairs rows{Wg, Wu, y, CuQ4K::row_bytes(K), M};                                \
+        gemv_cuk_rows<CuQ4K, PAR, J, false>(rows, x, 2u * M, K, nullptr, nullptr);                  \
     }
 #define ER_CUK_MULTI8(PAR)                                                                                   \
     ER_CUK_MULTI_ENTRY(PAR, 1) ER_CUK_MULTI_ENTRY(PAR, 2) ER_CUK_MULTI_ENTRY(PAR, 3)             \
@@ -2227,6 +2384,32 @@ ER_CUK_ENTRIES8(q8_0, CuQ8, 8)
 ER_CUK_MULTI16(2)
 ER_CUK_MULTI16(4)
 ER_CUK_MULTI8(8)
+// The fused Q8_0 projections over the K-sliced kernels: er_gemv_q8_0_multi_cuk<PAR>_j<J>
+// (mm, x, K) and er_gemv_q8_0_silu_cuk<PAR>_j<J> (Wg, Wu, x, y, normW, eps, M, K;
+// 2M rows), grid (ceil(rows / (PAR J)), tokens).
+#define ER_CUK_Q8F_ENTRY(PAR, J)                                                                              \
+    extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                                           \
+        er_gemv_q8_0_multi_cuk##PAR##_j##J(Q8Multi mm, const float *__restrict__ x, uint32_t K) {              \
+        const CukQ8Multi rows(mm, CuQ8::row_bytes(K));                                      \
+        gemv_cuk_rows<CuQ8, PAR, J, false>(rows, x, mm.M[0] + mm.M[1] + mm.M[2], K, nullptr, nullptr);        \
+    }                                                                                                          \
+    extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                                           \
+        er_gemv_q8_0_silu_cuk##PAR##_j##J(const uint8_t *__restrict__ Wg, const uint8_t *__restrict__ Wu,      \
+                                          const float *__restrict__ x, float *__restrict__ y,                 \
+                                          const float *__restrict__ normW, float eps, uint32_t M, uint32_t K) { \
+        const CukQ8Pairs rows{Wg, Wu, y, CuQ8::row_bytes(K), normW, eps, M};                                  \
+        gemv_cuk_rows<CuQ8, PAR, J, false>(rows, x, 2u * M, K, nullptr, nullptr);                             \
+    }
+#define ER_CUK_Q8F8(PAR)                                                                                     \
+    ER_CUK_Q8F_ENTRY(PAR, 1) ER_CUK_Q8F_ENTRY(PAR, 2) ER_CUK_Q8F_ENTRY(PAR, 3) ER_CUK_Q8F_ENTRY(PAR, 4)       \
+    ER_CUK_Q8F_ENTRY(PAR, 5) ER_CUK_Q8F_ENTRY(PAR, 6) ER_CUK_Q8F_ENTRY(PAR, 7) ER_CUK_Q8F_ENTRY(PAR, 8)
+#define ER_CUK_Q8F16(PAR)                                                                                    \
+    ER_CUK_Q8F8(PAR) ER_CUK_Q8F_ENTRY(PAR, 9) ER_CUK_Q8F_ENTRY(PAR, 10) ER_CUK_Q8F_ENTRY(PAR, 11)            \
+    ER_CUK_Q8F_ENTRY(PAR, 12) ER_CUK_Q8F_ENTRY(PAR, 13) ER_CUK_Q8F_ENTRY(PAR, 14) ER_CUK_Q8F_ENTRY(PAR, 15)  \
+    ER_CUK_Q8F_ENTRY(PAR, 16)
+ER_CUK_Q8F16(2)
+ER_CUK_Q8F16(4)
+ER_CUK_Q8F8(8)
 // Q6_K: rows of more than 64 slots (2 and 4 rows per step), and the top-1
 // forms (er_gemv_q6k_top1_cuk<PAR>_j<J>: (W, x, pv, pi, M, K), even J for PAR 2)
 ER_CUK_ENTRIES16(q6k, CuQ6K, 2)

@@ -217,6 +217,9 @@ struct er_hip_ctx {
     hipFunction_t fnQ6KTop1Cu[kCuCountQ6K][ER_CU_MAX_STEPS + 1] = {};
     hipFunction_t fnQ4KCuk[3][ER_CUK_MAX_STEPS] = {};  // [2, 4, 8 rows per step][row steps - 1]
     hipFunction_t fnQ4KCukMulti[3][ER_CUK_MAX_STEPS] = {};  // the dual / triple over them
+    hipFunction_t fnQ4KCukGeglu[3][ER_CUK_MAX_STEPS] = {};  // the dual GeGLU over them
+    hipFunction_t fnQ8CukMulti[3][ER_CUK_MAX_STEPS] = {};   // the fused Q8_0 rows over them
+    hipFunction_t fnQ8CukSilu[3][ER_CUK_MAX_STEPS] = {};    // the fused Q8_0 gate/up + SiLU
     hipFunction_t fnQ8Cuk[3][ER_CUK_MAX_STEPS] = {};
     hipFunction_t fnQ6KCuk[2][ER_CUK_MAX_STEPS] = {};      // [2, 4 rows per step][row steps - 1]
     hipFunction_t fnQ6KTop1Cuk[2][ER_CUK_MAX_STEPS] = {};  // even steps only for 2 rows per step
@@ -585,7 +588,8 @@ struct CukPlan {
     int j = 0;               // row steps per lane group
     uint32_t rowsPerWg = 0;  // PAR j
 };
-bool plan_cuk(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batch, CukPlan &p) {
+bool plan_cuk(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batch, CukPlan &p,
+              bool rows64 = false) {
     if (K % 256u != 0 || K > 16384u || ctx->gemv_fp32 != 0 || ctx->i8_override >= 0 ||
         ctx->cu_mode >= 0 || ctx->cuk_mode == 0 || batch == 0 ||
         (uint64_t)xl_lds_bytes(K) + 1024u > ctx->info.lds_per_workgroup)
@@ -594,7 +598,7 @@ bool plan_cuk(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t bat
     p.pi = S <= 64u ? 2 : (S <= 128u ? 1 : 0);
     const uint32_t par = 2u << p.pi, maxJ = p.pi == 2 ? 8u : (uint32_t)ER_CUK_MAX_STEPS;
     if (f == Fmt::Q6_K ? (S <= 64u || rows1 > par * maxJ)
-                       : (ctx->cuk_mode != 2 && (S < 64u || (S == 64u && (f != Fmt::Q4_K || rows1 < 8u)))))
+                       : (ctx->cuk_mode != 2 && (S < 64u || (S == 64u && !rows64 && (f != Fmt::Q4_K || rows1 < 8u)))))
         return false;
     const uint32_t perToken = std::max<uint32_t>(1u, cu / batch);
     const uint32_t rows = (M + perToken - 1u) / perToken;  // per CU, one token
@@ -1057,6 +1061,31 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
     return launch(ctx, k, grid, dim3(256, 1, 1), lds, stream, args);
 }
 
+// Whether fused projections of Mt rows (one token's) of K weights run on the
+// K-sliced kernels: where each wave's slice of K fills at least 7/8 of its row
+// slice's lanes (K = 4096, 7680, 8192, 14336, 16384 ...), from 12 rows per CU
+// at K = 4096 and 8 beyond; or wherever ER_HIP_GEMV_CUK=2 lets them; never
+// when a multi-matrix configuration is forced.  Depends on the rows and K
+// alone, so batched and per-token calls run the same arithmetic.  Same-box,
+// one token, us, multi-matrix kernels -> K-sliced: K = 4096: Q4_K 2 x 1024
+// rows 3.72 -> 4.08 and Q8_0 gate/up + SiLU 2 x 1024 4.69 -> 4.97 (8 rows per
+// CU); Q4_K 2 x 1536 4.48 -> 4.40, 2 x 2048 4.80 -> 4.67, 2 x 2560 6.86 ->
+// 5.18, Q8_0 QKV 2048 + 2 x 512 6.80 -> 5.66, 4096 + 2 x 512 9.85 -> 7.23,
+// gate/up + SiLU 2 x 2048 6.94 -> 6.28; K = 8192: Q4_K 2 x 1024 4.91 -> 4.88,
+// 2 x 2048 8.13 -> 6.31, Q8_0 QKV 2048 + 2 x 512 10.64 -> 7.90; K = 14336:
+// Q4_K 2 x 1024 9.14 -> 6.95, gate/up + SiLU 2 x 1024 13.05 -> 10.13.  A
+// slice filling 10 of 16 lanes (K = 5120) lost: 5120 + 2 x 1024 rows 8.88 ->
+// 10.28 (before the row sources held their pointers as values).
+// min4096: the rows per CU needed at K = 4096 (24 for the Q4_K GeGLU, whose
+// paired multi-matrix kernel held 2 x 1536 rows at 4.32 against 4.63 us).
+bool fused_on_cuk(const er_hip_ctx *ctx, uint64_t Mt, uint32_t K, uint32_t min4096 = 12u) {
+    if (ctx->multi_override >= 0 || ctx->multi1_override >= 0) return false;
+    if (ctx->cuk_mode == 2) return true;
+    const uint64_t rowsPerCu = (Mt + (uint64_t)ctx->cu_count - 1u) / (uint64_t)ctx->cu_count;
+    const uint32_t S = K / 64u, sliceLanes = S <= 64u ? 8u : (S <= 128u ? 16u : 32u);
+    return rowsPerCu >= (S <= 64u ? min4096 : 8u) && 8u * ((S + 7u) / 8u) >= 7u * sliceLanes;
+}
+
 // Fused Q4_K projections: validation of each weight as encodeQ4KWeights, then
 // one launch over all the matrices' rows -- the K-sliced kernels for large
 // totals, else the multi-matrix lane-group kernels (fp32 fallback: one GEMV
@@ -1082,24 +1111,14 @@ er_status encode_q4k_multi(er_hip_ctx *ctx, er_stream stream, const er_buffer *W
         a.y[i] = ys[j].data;
         a.M[i] = i < count ? Ms[i] : 0u;
     }
-    // From 24 rows per CU, and where each wave's slice of K fills at least 7/8
-    // of its row slice's lanes (K = 4096, 7680, 8192, 14336, 16384 ...), when
-    // one matrix of all the rows would take the K-sliced kernels, the matrices
-    // run there as one launch over their concatenated rows (each row's value
-    // is the one a K-sliced call gives it, a function of K alone); with
-    // ER_HIP_GEMV_CUK=2 wherever that plan takes them; never when a
-    // multi-matrix configuration is forced.  Same-box A/B against the
-    // multi-matrix kernels, medians of 4 (us): K = 4096: 2 x 14336 rows 18.62
-    // -> 17.38, 4096 + 2 x 1024 6.97 -> 6.54, 2 x 4096 7.50 -> 7.28, but 2 x
-    // 2048 4.81 -> 5.19 and 1536 + 2 x 512 4.34 -> 4.87; K = 8192: 2 x 3100
-    // 11.11 -> 10.55; K = 14336: 2 x 3100 20.49 -> 17.43; K = 7680: 5120 + 2 x
-    // 1024 11.09 -> 10.79; K = 5120 (10 of 16 lanes): the same rows 8.88 -> 10.28.
-    const uint32_t rowsPerCu = (uint32_t)((Mt + (uint64_t)ctx->cu_count - 1u) / (uint64_t)ctx->cu_count);
-    const uint32_t S = K / 64u, sliceLanes = S <= 64u ? 8u : (S <= 128u ? 16u : 32u);
-    const bool fullSlices = 8u * ((S + 7u) / 8u) >= 7u * sliceLanes;
+    // Large totals (fused_on_cuk), where one matrix of all the rows would take
+    // the K-sliced kernels: the matrices run there as one launch over their
+    // concatenated rows, each row's value the one a K-sliced call gives it (a
+    // function of K alone).  Same-box A/B against the multi-matrix kernels,
+    // medians of 4 (us): 2 x 14336 x 4096 19.81 -> 16.09, 4096 + 2 x 1024 rows
+    // x 4096 6.98 -> 5.42, 2 x 4096 x 4096 7.47 -> 6.23.
     CukPlan kp;
-    if (ctx->multi_override < 0 && ctx->multi1_override < 0 &&
-        ((rowsPerCu >= 24u && fullSlices) || ctx->cuk_mode == 2) && plan_cuk(ctx, Fmt::Q4_K, (uint32_t)Mt, K, 1u, kp)) {
+    if (fused_on_cuk(ctx, Mt, K) && plan_cuk(ctx, Fmt::Q4_K, (uint32_t)Mt, K, 1u, kp)) {
         void *kargs[] = {&a, &x.data, &K};
         dim3 grid((uint32_t)((Mt + kp.rowsPerWg - 1u) / kp.rowsPerWg), 1, 1);
         return launch_fn(ctx->fnQ4KCukMulti[kp.pi][kp.j - 1], "er_gemv_q4k_multi_cuk", grid,
@@ -1133,6 +1152,18 @@ er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_b
     const int ci = K <= kI8MaxK && ctx->gemv_fp32 == 0 ? pick_multi(ctx, K / 64u, 2u * M, false, 1u).ci : -1;
     st = bind_device(ctx);
     if (st != ER_OK) return st;
+    // large totals: the K-sliced kernels over the 2M gate/up rows, interleaved
+    // (fused_on_cuk; at K = 4096 from 24 rows per CU).  Same-box A/B, medians
+    // of 4 (us): 2 x 14336 x 4096 18.51 -> 15.38, 2 x 3000 x 4096 6.26 -> 5.58,
+    // 2 x 1100 x 14336 12.13 -> 7.55; 2 x 1536 x 4096 4.32 -> 4.63 (kept).
+    CukPlan kp;
+    if (M < 0x80000000u && fused_on_cuk(ctx, 2u * (uint64_t)M, K, 24u) &&
+        plan_cuk(ctx, Fmt::Q4_K, 2u * M, K, 1u, kp)) {
+        void *kargs[] = {&Wg.data, &Wu.data, &x.data, &y.data, &M, &K};
+        dim3 grid((2u * M + kp.rowsPerWg - 1u) / kp.rowsPerWg, 1, 1);
+        return launch_fn(ctx->fnQ4KCukGeglu[kp.pi][kp.j - 1], "er_gemv_q4k_geglu_cuk", grid,
+                         dim3(64u * ER_CU_WAVES, 1, 1), xl_lds_bytes(K), stream, kargs);
+    }
     if (ci < 0) {
         // rows longer than the integer-dot kernels cover: fp32 pair kernel,
         // x from global memory
@@ -1220,6 +1251,40 @@ er_status encode_q8_fused(er_hip_ctx *ctx, er_stream stream, const Q8FusedSpec &
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     const uint32_t S = K / 64u;
+    // Large totals: the K-sliced kernels (gate/up pairs as 2M rows), as the
+    // Q4_K dual / triple (fused_on_cuk); Q8_0 takes them here at K = 4096 too.
+    // Same-box A/B against the multi-matrix kernels, one token, medians of 4
+    // (us): QKV 4096 + 2 x 1024 rows x 4096 9.97 -> 7.67, gate/up + SiLU 2 x
+    // 14336 x 4096 28.00 -> 24.27.
+    CukPlan kp;
+    const uint64_t rowsV = f.silu ? 2u * Mt : Mt;
+    if (!anyK && fused_on_cuk(ctx, rowsV, K) && plan_cuk(ctx, Fmt::Q8_0, (uint32_t)rowsV, K, tokens, kp, true)) {
+        const uint32_t lds = xl_lds_bytes(K);
+        dim3 grid((uint32_t)((rowsV + kp.rowsPerWg - 1u) / kp.rowsPerWg), tokens, 1);
+        const float *normW = (const float *)f.normW.data;
+        float eps = f.eps;
+        if (f.silu) {
+            uint32_t M = f.M[0];
+            void *args[] = {(void *)&f.W[0].data, (void *)&f.W[1].data, &x.data, (void *)&f.y[0].data,
+                            &normW, &eps, &M, &K};
+            return launch_fn(ctx->fnQ8CukSilu[kp.pi][kp.j - 1], "er_gemv_q8_0_silu_cuk", grid,
+                             dim3(64u * ER_CU_WAVES, 1, 1), lds, stream, args);
+        }
+        Q8MultiArgs a{};
+        for (int m = 0; m < 3; ++m) {
+            const int j = m < f.count ? m : 0;
+            a.W[m] = f.W[j].data;
+            a.y[m] = f.y[j].data;
+            a.res[m] = m < f.count ? (const float *)f.res[m].data : nullptr;
+            a.M[m] = m < f.count ? f.M[m] : 0u;
+        }
+        a.halfMask = f.halfMask;
+        a.normW = normW;
+        a.eps = eps;
+        void *args[] = {&a, &x.data, &K};
+        return launch_fn(ctx->fnQ8CukMulti[kp.pi][kp.j - 1], "er_gemv_q8_0_multi_cuk", grid,
+                         dim3(64u * ER_CU_WAVES, 1, 1), lds, stream, args);
+    }
     const MultiPick mp = anyK ? MultiPick{} : pick_multi(ctx, S, (uint32_t)(f.silu ? 2u * Mt : Mt), !f.silu, tokens);
     if (mp.ci < 0 && mp.ci1 < 0) {
         Q8MultiArgs a{};
@@ -1433,17 +1498,22 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
     }
     for (int pi = 0; pi < 3; ++pi)
         for (int j = 1; j <= (pi == 2 ? 8 : ER_CUK_MAX_STEPS); ++j)
-            for (int kind = 0; kind < 5; ++kind) {
-                // q4k, q8_0, the Q4_K dual / triple (2, 4, 8 rows per step);
-                // q6k and its top-1 (2, 4; the top-1 with 2 rows per step at
-                // even step counts)
+            for (int kind = 0; kind < 8; ++kind) {
+                // q4k, q8_0, the Q4_K dual / triple and dual GeGLU, the fused
+                // Q8_0 rows and gate/up + SiLU (2, 4, 8 rows per step); q6k
+                // and its top-1 (2, 4; the top-1 with 2 rows per step at even
+                // step counts)
                 if ((kind == 2 || kind == 3) && (pi == 2 || (kind == 3 && pi == 0 && j % 2 != 0))) continue;
-                static const char *const kinds[5] = {"q4k", "q8_0", "q6k", "q6k_top1", "q4k_multi"};
+                static const char *const kinds[8] = {"q4k",       "q8_0",       "q6k",       "q6k_top1",
+                                                     "q4k_multi", "q8_0_multi", "q8_0_silu", "q4k_geglu"};
                 hipFunction_t *const slot = kind == 0   ? &ctx->fnQ4KCuk[pi][j - 1]
                                             : kind == 1 ? &ctx->fnQ8Cuk[pi][j - 1]
                                             : kind == 2 ? &ctx->fnQ6KCuk[pi][j - 1]
                                             : kind == 3 ? &ctx->fnQ6KTop1Cuk[pi][j - 1]
-                                                        : &ctx->fnQ4KCukMulti[pi][j - 1];
+                                            : kind == 4 ? &ctx->fnQ4KCukMulti[pi][j - 1]
+                                            : kind == 5 ? &ctx->fnQ8CukMulti[pi][j - 1]
+                                            : kind == 6 ? &ctx->fnQ8CukSilu[pi][j - 1]
+                                                        : &ctx->fnQ4KCukGeglu[pi][j - 1];
                 char name[64];
                 std::snprintf(name, sizeof(name), "er_gemv_%s_cuk%d_j%d", kinds[kind], 2 << pi, j);
                 e = hipModuleGetFunction(slot, ctx->module, name);

@@ -4,7 +4,9 @@ RMSNorm restated from FusedKernelTests.cpuRMSNorm, the Q8_0 GEMV oracle,
 silu from FusedKernelTests.silu.  Bar: relative L2 <= 1e-3 per output
 (fp16 outputs compared with the fp16 rounding of the oracle), on the
 reference tests' shapes (dim 128, q 64, kv 32, inter 96, 1 and 3 tokens) and
-on Llama-sized ones; batched calls equal per-token calls exactly."""
+on Llama-sized ones (those of 6144 rows or more on the K-sliced kernels);
+batched calls equal per-token calls exactly; every entry forced onto the
+K-sliced kernels at odd shapes."""
 import numpy as np
 import pytest
 
@@ -106,7 +108,8 @@ def test_fused_final_norm_gemv(ctx, fk, rows, dim):
     assert rel_l2(got, oracle_proj(W, x, nw, rows, dim)) < TOL
 
 
-@pytest.mark.parametrize("rows,dim", [(96, 128), (1024, 4096), (4096, 14336), (96, 96), (501, 16416)])
+@pytest.mark.parametrize("rows,dim", [(96, 128), (1024, 4096), (4096, 14336), (96, 96), (501, 16416),
+                                      (6144, 4096)])
 def test_gemv_f16out_and_add(ctx, fk, rows, dim):
     W = q8(rows, dim, 7)
     x = synth.normal_f32(synth.seed(70, 31), dim)
@@ -155,8 +158,9 @@ def test_fused_qkv_turbo_keeps_v_fp32(ctx, fk):
             buf.free()
 
 
-def test_batched_equals_per_token(ctx, fk):
-    dim, qd, kvd, T = 1024, 1024, 256, 4
+# the second shape's 6144 rows take the K-sliced kernels
+@pytest.mark.parametrize("dim,qd,kvd,T", [(1024, 1024, 256, 4), (4096, 4096, 1024, 2)])
+def test_batched_equals_per_token(ctx, fk, dim, qd, kvd, T):
     Wq, Wk, Wv = q8(qd, dim, 11), q8(kvd, dim, 12), q8(kvd, dim, 13)
     x = synth.normal_f32(synth.seed(70, 40), T * dim)
     nw = norm_weight(dim, 3)
@@ -176,6 +180,70 @@ def test_batched_equals_per_token(ctx, fk):
     finally:
         for b in bufs + outs + one:
             b.free()
+
+
+@pytest.fixture(scope="module")
+def fk_cuk2():
+    """A context whose fused Q8_0 calls take the K-sliced kernels wherever K %
+    256 == 0 (ER_HIP_GEMV_CUK=2, read at creation)."""
+    import os
+    from edgerunner_amd import Context
+    old = os.environ.get("ER_HIP_GEMV_CUK")
+    os.environ["ER_HIP_GEMV_CUK"] = "2"
+    try:
+        c = Context(0)
+    finally:
+        if old is None:
+            os.environ.pop("ER_HIP_GEMV_CUK", None)
+        else:
+            os.environ["ER_HIP_GEMV_CUK"] = old
+    yield c, FusedQ8Kernel(c)
+    c.close()
+
+
+# (dim, rows: q / kv for the QKV and final-norm projections, gate/up for the
+# SiLU, T): 8, 4 and 2 rows per step (K = 512, 8192, 14336), steps that
+# straddle q | k | v and gate/up pairs, a wave with a partial slice (14336:
+# 28 of 32 lanes)
+@pytest.mark.parametrize("dim,qd,kvd,T", [(512, 130, 42, 2), (8192, 300, 77, 1), (14336, 70, 21, 2)])
+def test_k_sliced_fused_forms(fk_cuk2, dim, qd, kvd, T):
+    """Every fused Q8_0 entry on the K-sliced kernels (the RMSNorm factor from
+    the waves' sums of x^2, fp16 V, the residual, gate/up pairs): within the
+    parity bar of the oracle."""
+    c, f = fk_cuk2
+    Wq, Wk, Wv = q8(qd, dim, 31), q8(kvd, dim, 32), q8(kvd, dim, 33)
+    x = synth.normal_f32(synth.seed(70, 60 + T), T * dim)
+    nw = norm_weight(dim, 5)
+    res = synth.normal_f32(synth.seed(70, 61), qd)
+    bufs = [c.upload(a) for a in (Wq, Wk, Wv, x, nw, res)]
+    oq, ok, ov = c.alloc(4 * T * qd), c.alloc(4 * T * kvd), c.alloc(2 * T * kvd)
+    os_, on, oh, oa = c.alloc(4 * T * kvd), c.alloc(4 * qd), c.alloc(2 * qd), c.alloc(4 * qd)
+    try:
+        f.encodeFusedQKV(None, bufs[0], bufs[1], bufs[2], bufs[3], oq, ok, ov, bufs[4], qd, kvd, dim, T, EPS)
+        f.encodeFusedGateUpSilu(None, bufs[1], bufs[2], bufs[3], os_, bufs[4], kvd, dim, T, EPS)
+        f.encodeFusedFinalNormGEMV(None, bufs[0], bufs[3], on, bufs[4], qd, dim, EPS)
+        f.encodeGEMVF16Out(None, bufs[0], bufs[3], oh, qd, dim)
+        f.encodeGEMVAdd(None, bufs[0], bufs[3], bufs[5], oa, qd, dim)
+        c.synchronize()
+        q = oq.download(np.float32).reshape(T, qd)
+        k = ok.download(np.float32).reshape(T, kvd)
+        v = ov.download(np.float16).reshape(T, kvd).astype(np.float32)
+        sl = os_.download(np.float32).reshape(T, kvd)
+        n, h, a = on.download(np.float32), oh.download(np.float16).astype(np.float32), oa.download(np.float32)
+    finally:
+        for b in bufs + [oq, ok, ov, os_, on, oh, oa]:
+            b.free()
+    for t in range(T):
+        xt = x[t * dim:(t + 1) * dim]
+        eq, ek, ev = (oracle_proj(W, xt, nw, m, dim) for W, m in ((Wq, qd), (Wk, kvd), (Wv, kvd)))
+        assert rel_l2(q[t], eq) < TOL and rel_l2(k[t], ek) < TOL
+        assert rel_l2(v[t], ev.astype(np.float16).astype(np.float32)) < TOL
+        assert rel_l2(sl[t], ref.silu(ek) * ev) < TOL
+    x0 = x[:dim]
+    assert rel_l2(n, oracle_proj(Wq, x0, nw, qd, dim)) < TOL
+    plain = oracle_proj(Wq, x0, None, qd, dim)
+    assert rel_l2(h, plain.astype(np.float16).astype(np.float32)) < TOL
+    assert rel_l2(a, plain + res) < TOL
 
 
 def test_validation(ctx, fk):

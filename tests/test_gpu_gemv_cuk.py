@@ -254,8 +254,9 @@ def test_q6k_top1_ties_and_nan(gemv):
 
 
 # (rows of each matrix -- the dual's two are of one height --, K, whether the
-# default plan takes the K-sliced kernels for the total rows: from 24 rows per
-# CU, with slices filling 7/8 of their lanes): steps that straddle two
+# default plan takes the K-sliced kernels for the total rows: from 12 rows per
+# CU at K = 4096 and 8 beyond, with slices filling 7/8 of their lanes): steps
+# that straddle two
 # matrices (3201 with 8 rows per step, 700 + 130 and 5001 with 4, 9 with 2),
 # every PAR, K = 16384
 @pytest.mark.parametrize("rows,K,default_cuk", [((4096, 1024, 1024), 4096, True), ((3201, 3201), 4096, True),
@@ -267,8 +268,8 @@ def test_q4k_multi_over_k_sliced(gemv, cuk_everywhere, rows, K, default_cuk):
     """Q4_K dual / triple where the total rows take the K-sliced kernels (one
     launch over the concatenated rows): every row equal bit for bit to a
     K-sliced call of its own matrix (a row's value depends on K alone) and
-    within the parity bar of the oracle.  With ER_HIP_GEMV_CUK=2 the shapes
-    below 24 rows per CU and the short-row one take them too."""
+    within the parity bar of the oracle.  With ER_HIP_GEMV_CUK=2 the smaller
+    totals, the half-filled slices and the short rows take them too."""
     Ws = [synth.q4_k(synth.seed(52, i), m, K) for i, m in enumerate(rows)]
     x = synth.normal_f32(synth.seed(52, 9), K)
     singles = [cuk_everywhere.executeQ4KWeights(W, x, m, K) for W, m in zip(Ws, rows)]
