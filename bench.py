@@ -289,9 +289,10 @@ def fused_bytes(kind: str, fmt: str, rows, K: int) -> int:
     return w + 4 * K + out + (4 * K if fmt == "q8_0" else 0)
 
 
-def bench_fused(ctx, kind: str, fmt: str, rows, K: int, cfg: int, steps: int, warmup: int) -> dict:
-    """One fused projection call (one x read for all its matrices) over
-    rotating sets of its matrices (>= 768 MB), in a HIP graph."""
+def fused_calls(ctx, stream, kind: str, fmt: str, rows, K: int, cfg: int):
+    """Device buffers of one fused workload: rotating sets of its matrices
+    (>= 768 MB), x, the RMSNorm weight and the outputs.  Returns (enc, copies,
+    set_bytes, buffers): enc(i) encodes the call reading set i % copies."""
     import edgerunner_amd.synth as synth
     from edgerunner_amd import FusedQ8Kernel, GEMVKernel
 
@@ -299,7 +300,6 @@ def bench_fused(ctx, kind: str, fmt: str, rows, K: int, cfg: int, steps: int, wa
     Ws = [synth.weights(fmt, synth.seed(cfg, 10 + i), M, K, **DSCALE[fmt]) for i, M in enumerate(rows)]
     set_bytes = sum(W.nbytes for W in Ws)
     copies = max(2, -(-ROTATE_BYTES // set_bytes))
-    stream = ctx.stream()
     sets = [[ctx.upload(W, stream) for W in Ws] for _ in range(copies)]
     xb = ctx.upload(synth.normal_f32(synth.seed(cfg, 1), K), stream)
     norm = ctx.upload((1.0 + 0.1 * synth.normal_f32(synth.seed(cfg, 2), K)).astype(np.float32), stream)
@@ -319,13 +319,21 @@ def bench_fused(ctx, kind: str, fmt: str, rows, K: int, cfg: int, steps: int, wa
         else:  # silu
             fq.encodeFusedGateUpSilu(stream, *w, xb, ys[0], norm, rows[0], K, 1, eps)
 
+    return enc, copies, set_bytes, [b for w in sets for b in w] + [xb, norm] + ys
+
+
+def bench_fused(ctx, kind: str, fmt: str, rows, K: int, cfg: int, steps: int, warmup: int) -> dict:
+    """One fused projection call (one x read for all its matrices) over
+    rotating sets of its matrices (>= 768 MB), in a HIP graph."""
+    stream = ctx.stream()
+    enc, copies, set_bytes, bufs = fused_calls(ctx, stream, kind, fmt, rows, K, cfg)
     for i in range(warmup):
         enc(i)
     stream.synchronize()
     avg_us = rotation_time_us(ctx, stream, enc, steps, copies)
-    finite = bool(np.all(np.isfinite(ys[0].download(np.float32, stream=stream))))
+    finite = bool(np.all(np.isfinite(bufs[-len(rows)].download(np.float32, stream=stream))))
     nbytes = fused_bytes(kind, fmt, rows, K)
-    for b in [b for w in sets for b in w] + [xb, norm] + ys:
+    for b in bufs:
         b.free()
     stream.destroy()
     return {"kind": kind, "fmt": fmt, "rows": list(rows), "K": K, **rotation_fields(copies, set_bytes, steps),
@@ -837,11 +845,13 @@ def load_traffic(name: str):
 COPY_CAL_BYTES = 64 << 20
 
 
-def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None, chain_steps: int = 0, dq_todo=()) -> None:
+def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None, chain_steps: int = 0, dq_todo=(),
+          fu_todo=()) -> None:
     """Counter-collection driver (run under `rocprofv3 --pmc ...`): three
     device-to-device copies of COPY_CAL_BYTES (the calibration kernel of known
     traffic), then for each GEMV workload (rotating weights) and each GEMM
-    workload in `gemm_todo` and dequantisation in `dq_todo`: one empty kernel (er_probe_empty) that marks
+    workload in `gemm_todo`, dequantisation in `dq_todo` and fused projection
+    in `fu_todo`: one empty kernel (er_probe_empty) that marks
     where the workload's dispatches begin, then its `steps` calls; with
     chain_steps, the same for that many eager steps of the fused decode chain.  The workload names
     and step counts go to `order_file` (one `name steps` line each), which
@@ -894,6 +904,17 @@ def probe(ctx, todo, steps: int, gemm_todo=(), order_file=None, chain_steps: int
         order.append((name, steps))
         log(f"probe {name}: {steps} calls")
         for b in wbufs + [out]:
+            b.free()
+    for name, kind, fmt, rows, K, cfg in fu_todo:
+        enc, copies, _, bufs = fused_calls(ctx, stream, kind, fmt, rows, K, cfg)
+        stream.synchronize()
+        separator()
+        for i in range(steps):
+            enc(i)
+        stream.synchronize()
+        order.append((name, steps))
+        log(f"probe {name}: {steps} calls")
+        for b in bufs:
             b.free()
     if gemm_todo:
         from edgerunner_amd import QuantGEMMKernel
@@ -1042,6 +1063,7 @@ def summarize(root: Path) -> str:
         alg = {w[0]: algorithmic_bytes(w[1], w[2], w[3]) for w in GEMV_WORKLOADS}
         alg.update({w[0]: gemm_min_bytes(w[1], w[2], w[3], w[4]) for w in GEMM_WORKLOADS})
         alg.update({w[0]: dequant_bytes(w[1], w[2], w[3]) for w in DEQUANT_WORKLOADS})
+        alg.update({w[0]: fused_bytes(w[1], w[2], w[3], w[4]) for w in FUSED_WORKLOADS})
         from edgerunner_amd.chain import ChainSpec
         alg["decode_chain_fused_eager"] = ChainSpec().weight_bytes()
         for name, v in per_workload.items():
@@ -1105,8 +1127,10 @@ def main() -> int:
                      and w[0] in args.workloads.split(",")]
         dq_todo = [w for w in DEQUANT_WORKLOADS if args.workloads not in ("all", "headline")
                    and w[0] in args.workloads.split(",")]
+        fu_todo = [w for w in FUSED_WORKLOADS if args.workloads not in ("all", "headline")
+                   and w[0] in args.workloads.split(",")]
         chain_steps = 3 if "decode_chain" in args.workloads.split(",") else 0
-        probe(ctx, todo, args.steps, gemm_todo, args.probe_order, chain_steps, dq_todo)
+        probe(ctx, todo, args.steps, gemm_todo, args.probe_order, chain_steps, dq_todo, fu_todo)
         return 0
     results = {}
     for name, fmt, M, K, cfg in todo:
