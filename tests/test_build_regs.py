@@ -6,6 +6,10 @@ ROCm LLVM tools:
     full drains (one such kernel ran at twice the time of its spill-free
     neighbour), and the compiler's choice depends on unroll depth and loads
     in flight, so every configuration is checked;
+  - no kernel has a private (scratch) segment at all: a stack object that is
+    not a spill -- a struct whose fields are chosen through a conditional on
+    the fields themselves, which selects their addresses -- puts every access
+    to it through scratch memory;
   - in the CU-resident kernels whose staging waves issue their first weight
     loads before converting x, the explicit s_waitcnt vmcnt(n) that waits
     for x counts exactly the weight loads issued after the workgroup barrier
@@ -46,7 +50,8 @@ def _kernel_metadata(tmp_path):
         if m:
             name = m.group(1)
             continue
-        m = re.match(r"\s+\.(vgpr_spill_count|sgpr_spill_count|vgpr_count):\s+(\d+)", line)
+        m = re.match(r"\s+\.(vgpr_spill_count|sgpr_spill_count|vgpr_count|private_segment_fixed_size):\s+(\d+)",
+                     line)
         if m and name is not None:
             kernels.setdefault(name, {})[m.group(1)] = int(m.group(2))
     return kernels
@@ -59,6 +64,14 @@ def test_no_kernel_spills(tmp_path):
     spills = {k: v for k, v in kernels.items()
               if v.get("vgpr_spill_count", 0) or v.get("sgpr_spill_count", 0)}
     assert not spills, spills
+
+
+def test_no_private_segment(tmp_path):
+    kernels = _kernel_metadata(tmp_path)
+    assert any(k.startswith("er_gemv_q8_0_silu_cuk") for k in kernels)
+    private = {k: v["private_segment_fixed_size"] for k, v in kernels.items()
+               if v.get("private_segment_fixed_size", 0)}
+    assert not private, private
 
 
 def test_cu_early_weight_loads_match_x_wait(tmp_path):
