@@ -255,6 +255,20 @@ ER_DEV void gemv_q4k_i8(const uint8_t *__restrict__ W, const float *__restrict__
 // projections, q4_k_gemv_dual_f32 / q4_k_gemv_three_f32,
 // Dequant_Q4_K_M.metal:704-803, 1024-1202): rows of A, B, C are concatenated
 // into one row space; a lane group's R rows may cross a matrix boundary.
+// One of three values by index, taken as values.  Indexing a kernel-argument
+// array with a per-lane index (mm.W[m]), or a conditional on struct members
+// themselves (which selects their addresses), makes every lane load the value
+// through the vector memory path -- behind any loads already in flight -- or
+// puts the struct in scratch; the three values here are uniform loads
+// (scalar registers) and the choice a per-lane select.
+template <class T>
+__device__ __forceinline__ T pick3(uint32_t m, T a, T b, T c) {
+    T v = a;
+    v = m == 1u ? b : v;
+    v = m == 2u ? c : v;
+    return v;
+}
+
 struct Q4Multi {
     const uint8_t *W[3];
     float *y[3];
@@ -298,8 +312,8 @@ ER_DEV void gemv_q4k_i8_multi(const Q4Multi &mm, const float *__restrict__ x, ui
                 m = 2;
             }
         }
-        rowp[r] = mm.W[m] + (size_t)v * rowBytes;
-        yrow[r] = mm.y[m] + v;
+        rowp[r] = pick3((uint32_t)m, mm.W[0], mm.W[1], mm.W[2]) + (size_t)v * rowBytes;
+        yrow[r] = pick3((uint32_t)m, mm.y[0], mm.y[1], mm.y[2]) + v;
         live[r] = row0 + (uint32_t)r < Mt;
     }
     gemv_q4k_i8_core<LPR, NS, R, ER_EPI_STORE>(rowp, yrow, live, x, K, rowAt);
@@ -656,11 +670,13 @@ ER_DEV void gemv_q8_0_i8_multi(const Q8Multi &mm, const float *__restrict__ x, u
                 m = 2;
             }
         }
-        const size_t out = (size_t)t * mm.M[m] + v;
-        rowp[r] = mm.W[m] + (size_t)v * rowBytes;
+        const uint32_t mu = (uint32_t)m;
+        const size_t out = (size_t)t * pick3(mu, mm.M[0], mm.M[1], mm.M[2]) + v;
+        rowp[r] = pick3(mu, mm.W[0], mm.W[1], mm.W[2]) + (size_t)v * rowBytes;
         half[r] = (mm.halfMask >> m) & 1u;
-        yrow[r] = (uint8_t *)mm.y[m] + out * (half[r] ? 2u : 4u);
-        res[r] = mm.res[m] ? mm.res[m] + out : nullptr;
+        yrow[r] = (uint8_t *)pick3(mu, mm.y[0], mm.y[1], mm.y[2]) + out * (half[r] ? 2u : 4u);
+        const float *rp = pick3(mu, mm.res[0], mm.res[1], mm.res[2]);
+        res[r] = rp ? rp + out : nullptr;
         live[r] = row0 + (uint32_t)r < Mt;
     }
     gemv_q8_0_i8_fused_core<LPR, NS, R, ER_EPI_Q8_ROWS>(rowp, yrow, live, half, res, x + (size_t)t * K,
@@ -1642,17 +1658,6 @@ struct CukOne {
     __device__ __forceinline__ void store(uint32_t r, float v) const { y[r] = v; }
 };
 
-// One of three values by index, taken as values (a conditional on the
-// members themselves selects their addresses and puts the row source in
-// memory: per-lane loads of the pointers, or scratch).
-template <class T>
-__device__ __forceinline__ T pick3(uint32_t m, T a, T b, T c) {
-    T v = a;
-    v = m == 1u ? b : v;
-    v = m == 2u ? c : v;
-    return v;
-}
-
 // Rows [0, M0) of W[0], then M1 of W[1], then M2 of W[2]; each row's value
 // is the one the matrix's own K-sliced launch gives it.  Pointers and row
 // counts are held as values (uniform: scalar registers).
@@ -2197,12 +2202,14 @@ ER_DEV void gemv_q8_0_any_fused(const Q8Multi &mm, const float *__restrict__ x, 
                 m = 2;
             }
         }
-        const size_t out = (size_t)t * mm.M[m] + v;
-        rowp[r] = mm.W[m] + (size_t)v * rowBytes;
+        const uint32_t mu = (uint32_t)m;
+        const size_t out = (size_t)t * pick3(mu, mm.M[0], mm.M[1], mm.M[2]) + v;
+        rowp[r] = pick3(mu, mm.W[0], mm.W[1], mm.W[2]) + (size_t)v * rowBytes;
         if (EPI == ER_EPI_Q8_SILU) rowp[OR + r] = mm.W[1] + (size_t)v * rowBytes;
         half[r] = EPI == ER_EPI_Q8_ROWS && ((mm.halfMask >> m) & 1u);
-        yrow[r] = (uint8_t *)mm.y[m] + out * (half[r] ? 2u : 4u);
-        res[r] = EPI == ER_EPI_Q8_ROWS && mm.res[m] ? mm.res[m] + out : nullptr;
+        yrow[r] = (uint8_t *)pick3(mu, mm.y[0], mm.y[1], mm.y[2]) + out * (half[r] ? 2u : 4u);
+        const float *rp = pick3(mu, mm.res[0], mm.res[1], mm.res[2]);
+        res[r] = EPI == ER_EPI_Q8_ROWS && rp ? rp + out : nullptr;
         live[r] = row0 + (uint32_t)r < Mt;
     }
     float acc[R];
