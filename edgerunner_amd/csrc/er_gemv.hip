@@ -1475,7 +1475,11 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
     static_assert(PAR == 2 || PAR == 4 || PAR == 8, "2, 4 or 8 rows per step");
     static_assert(J >= 1 && J <= (int)LPR && J <= ER_CUK_MAX_STEPS, "row sums parked one per lane of a slice");
     static_assert(!TOP1 || PAR > 2 || J % 2 == 0, "top-1 quads pair the steps of 2-row slices");
-    constexpr int D = F::UNITS < J ? F::UNITS : J;
+    // units in flight: the format's F::UNITS, or, with 8 rows per step, every
+    // unit of a launch of at most 3 steps (Q8_0, 2 units: the fused QKV of
+    // 4096 + 2 x 1024 rows x 4096 7.67 -> 7.44 us; with 4 rows per step at
+    // K = 8192 7.90 -> 7.97, so those keep 2)
+    constexpr int D = (PAR == 8 && J <= 3) ? J : (F::UNITS < J ? F::UNITS : J);
     // x pieces per wave: 16-value chunks (4 spw <= 4 LPR, 64 per pass), or for
     // 8-lane slices 8-value halves (8 spw <= 64: one pass)
     constexpr int VPL = PAR == 8 ? 8 : 16;  // values per lane per pass
