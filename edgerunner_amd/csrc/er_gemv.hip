@@ -1445,7 +1445,8 @@ ER_DEV void gemv_cu(const uint8_t *__restrict__ W, const float *__restrict__ x, 
 // takes row g of the step and slot spw w + li (lanes past the slice reuse its
 // last slot with weight 0).  Row step j, row g is row (j * gridDim.x +
 // blockIdx.x) * PAR + g; a step's slot dots are summed over the LPR lanes
-// (group_sum) and parked in lane j.  At the end the 8 wave partials of each
+// (group_sum) and parked in lane j (steps LPR + j in a second register).  At
+// the end the 8 wave partials of each
 // row meet in LDS and are added in wave order, so a row's value depends on K
 // alone, not on the row partition or the batch.  J row steps per lane group,
 // F::UNITS in flight.
@@ -1473,7 +1474,7 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
     __shared__ float tv[TOP1 ? PAR * J : 1];      // top-1: the workgroup's row values
     __shared__ float ssw[Rows::NORM ? ER_CU_WAVES : 1];  // RMSNorm: [wave] sum of x^2 over its slice
     static_assert(PAR == 2 || PAR == 4 || PAR == 8, "2, 4 or 8 rows per step");
-    static_assert(J >= 1 && J <= (int)LPR && J <= ER_CUK_MAX_STEPS, "row sums parked one per lane of a slice");
+    static_assert(J >= 1 && J <= 2 * (int)LPR && J <= ER_CUK_MAX_STEPS, "row sums parked two per lane of a slice");
     static_assert(!TOP1 || PAR > 2 || J % 2 == 0, "top-1 quads pair the steps of 2-row slices");
     // units in flight: the format's F::UNITS, or, with 8 rows per step, every
     // unit of a launch of at most 3 steps (Q8_0, 2 units: the fused QKV of
@@ -1494,7 +1495,7 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
         return (TOP1 && PAR == 2) ? ((j >> 1) * gridDim.x + blockIdx.x) * 4u + 2u * (j & 1u) + gg
                                   : (j * gridDim.x + blockIdx.x) * (uint32_t)PAR + gg;
     };
-    float res = 0.0f;
+    float res = 0.0f, res2 = 0.0f;  // step j's row sum parked in lane j (res), step LPR + j's in res2
     float4 share = float4{0.0f, 0.0f, 0.0f, 0.0f};  // this wave's share of the launch's checks
     float ssq = 0.0f;                               // RMSNorm: this wave's sum of x^2
     if (s0 < S) {
@@ -1589,12 +1590,16 @@ ER_DEV void gemv_cuk_rows(const Rows &rows, const float *__restrict__ x, uint32_
             if (j + D < J) issue((uint32_t)(j + D), j % D);
             __builtin_amdgcn_sched_barrier(0);
             acc = group_sum<LPR>(acc);
-            res = li == (uint32_t)j ? acc : res;
+            if ((uint32_t)j < LPR)
+                res = li == (uint32_t)j ? acc : res;
+            else
+                res2 = li == (uint32_t)j - LPR ? acc : res2;
         }
     } else if constexpr (PAR == 2) {
         __builtin_amdgcn_s_barrier();  // the x barrier above, for a wave with no slice
     }
     if (li < (uint32_t)J) part[wave][PAR * li + g] = res;
+    if (LPR + li < (uint32_t)J) part[wave][PAR * (LPR + li) + g] = res2;
     if (lane == 0) chk[wave] = share;
     if constexpr (Rows::NORM) {
         ssq = group_sum<64>(ssq);
@@ -2346,7 +2351,7 @@ ER_CU_CONFIGS_Q8(ER_CU_ENTRY_Q8)
 ER_CU_CONFIGS_Q6K(ER_CU_ENTRY_Q6K)
 
 // K-sliced CU-resident kernels: er_gemv_<fmt>_cuk<PAR>_j<J>, J = 1..ER_CUK_MAX_STEPS
-// row steps of PAR rows per workgroup (J <= 64 / PAR), grid (ceil(M / (PAR J)),
+// row steps of PAR rows per workgroup (J <= 2 * 64 / PAR), grid (ceil(M / (PAR J)),
 // batch), dynamic LDS xl_lds_bytes(K).
 #define ER_CUK_ENTRY(fmt, F, PAR, J)                                                                \
     extern "C" __global__ void __launch_bounds__(64 * ER_CU_WAVES)                                 \
@@ -2364,10 +2369,10 @@ ER_CU_CONFIGS_Q6K(ER_CU_ENTRY_Q6K)
     ER_CUK_ENTRY(fmt, F, PAR, 14) ER_CUK_ENTRY(fmt, F, PAR, 15) ER_CUK_ENTRY(fmt, F, PAR, 16)
 ER_CUK_ENTRIES16(q4k, CuQ4K, 2)
 ER_CUK_ENTRIES16(q4k, CuQ4K, 4)
-ER_CUK_ENTRIES8(q4k, CuQ4K, 8)
+ER_CUK_ENTRIES16(q4k, CuQ4K, 8)
 ER_CUK_ENTRIES16(q8_0, CuQ8, 2)
 ER_CUK_ENTRIES16(q8_0, CuQ8, 4)
-ER_CUK_ENTRIES8(q8_0, CuQ8, 8)
+ER_CUK_ENTRIES16(q8_0, CuQ8, 8)
 // The Q4_K dual / triple over the K-sliced kernels: er_gemv_q4k_multi_cuk<PAR>_j<J>
 // (mm, x, K), rows of the matrices concatenated, one token; and the dual GeGLU,
 // er_gemv_q4k_geglu_cuk<PAR>_j<J> (Wg, Wu, x, y, M, K; 2M rows).
@@ -2394,7 +2399,7 @@ ER_CUK_ENTRIES8(q8_0, CuQ8, 8)
     ER_CUK_MULTI_ENTRY(PAR, 14) ER_CUK_MULTI_ENTRY(PAR, 15) ER_CUK_MULTI_ENTRY(PAR, 16)
 ER_CUK_MULTI16(2)
 ER_CUK_MULTI16(4)
-ER_CUK_MULTI8(8)
+ER_CUK_MULTI16(8)
 // The fused Q8_0 projections over the K-sliced kernels: er_gemv_q8_0_multi_cuk<PAR>_j<J>
 // (mm, x, K) and er_gemv_q8_0_silu_cuk<PAR>_j<J> (Wg, Wu, x, y, normW, eps, M, K;
 // 2M rows), grid (ceil(rows / (PAR J)), tokens).
@@ -2420,7 +2425,7 @@ ER_CUK_MULTI8(8)
     ER_CUK_Q8F_ENTRY(PAR, 16)
 ER_CUK_Q8F16(2)
 ER_CUK_Q8F16(4)
-ER_CUK_Q8F8(8)
+ER_CUK_Q8F16(8)
 // Q6_K: rows of more than 64 slots (2 and 4 rows per step), and the top-1
 // forms (er_gemv_q6k_top1_cuk<PAR>_j<J>: (W, x, pv, pi, M, K), even J for PAR 2)
 ER_CUK_ENTRIES16(q6k, CuQ6K, 2)

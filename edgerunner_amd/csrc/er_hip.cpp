@@ -570,7 +570,7 @@ bool plan_cu(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t batc
 // K-sliced CU-resident kernels (er_gemv.hip gemv_cuk), PAR = 2, 4 or 8 rows per
 // workgroup step as the row has up to 256, 128 or 64 slots (each wave's slice
 // then fills 16 of 32, 9 of 16 ... all lanes of its row slices), up to
-// ER_CUK_MAX_STEPS steps (8 for PAR 8), about one workgroup per CU for one
+// ER_CUK_MAX_STEPS steps, about one workgroup per CU for one
 // token's rows (more beyond).  Taken by default for Q4_K / Q8_0 rows of
 // 4096 < K <= 16384 weights at any M, and for Q4_K rows of K = 4096 when one
 // token's rows give each CU at least 8 (A/B in one process against the
@@ -596,7 +596,7 @@ bool plan_cuk(const er_hip_ctx *ctx, Fmt f, uint32_t M, uint32_t K, uint32_t bat
         return false;
     const uint32_t S = K / 64u, cu = (uint32_t)ctx->cu_count, rows1 = (M + cu - 1u) / cu;
     p.pi = S <= 64u ? 2 : (S <= 128u ? 1 : 0);
-    const uint32_t par = 2u << p.pi, maxJ = p.pi == 2 ? 8u : (uint32_t)ER_CUK_MAX_STEPS;
+    const uint32_t par = 2u << p.pi, maxJ = (uint32_t)ER_CUK_MAX_STEPS;
     if (f == Fmt::Q6_K ? (S <= 64u || rows1 > par * maxJ)
                        : (ctx->cuk_mode != 2 && (S < 64u || (S == 64u && !rows64 && (f != Fmt::Q4_K || rows1 < 8u)))))
         return false;
@@ -1497,7 +1497,7 @@ er_status er_hip_create(int device, er_hip_ctx **out_ctx) {
             }
     }
     for (int pi = 0; pi < 3; ++pi)
-        for (int j = 1; j <= (pi == 2 ? 8 : ER_CUK_MAX_STEPS); ++j)
+        for (int j = 1; j <= ER_CUK_MAX_STEPS; ++j)
             for (int kind = 0; kind < 8; ++kind) {
                 // q4k, q8_0, the Q4_K dual / triple and dual GeGLU, the fused
                 // Q8_0 rows and gate/up + SiLU (2, 4, 8 rows per step); q6k

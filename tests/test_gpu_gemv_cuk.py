@@ -183,7 +183,7 @@ def test_short_rows_every_step_count(cuk_everywhere, whole_rows, fmt, K):
     cus = cuk_everywhere.ctx.compute_units
     par = 8 if K <= 4096 else 4
     x = synth.normal_f32(synth.seed(115, K % 97), K)
-    for j in range(1, (8 if par == 8 else 16) + 1, 3 if par == 4 else 1):
+    for j in range(1, 17, 3 if par == 4 else 1):  # 8 rows per step: every step count 1..16
         M = cus * par * j
         W = synth.weights(fmt, synth.seed(115, 10 * j + K % 7), M, K, **DSCALE[fmt])
         y = getattr(cuk_everywhere, EXEC[fmt])(W, x, M, K)
