@@ -157,9 +157,10 @@ def test_batched_one_token_poisoned(families, fmt, family, M, K, kind):
 
 @pytest.mark.parametrize("kind", ["nan", "pinf", "ninf", "pinf_group", "pm_inf"])
 @pytest.mark.parametrize("mode", ["dual", "triple", "geglu"])
-def test_q4k_multi_nonfinite(gemv, kind, mode):
-    """Dual / triple Q4_K projections sharing x, and the GeGLU pair."""
-    K = 1024
+@pytest.mark.parametrize("K", [1024, 4096])
+def test_q4k_multi_nonfinite(gemv, kind, mode, K):
+    """Dual / triple Q4_K projections sharing x, and the GeGLU pair (K = 4096:
+    on the K-sliced kernels)."""
     geglu = mode == "geglu"
     rows = [2048, 1024, 1024] if mode == "triple" else [3072, 3072]
     Ws = [weights("q4_k", r, K, 10 + i) for i, r in enumerate(rows)]
@@ -178,12 +179,14 @@ def norm_weight(K):
 
 
 @pytest.mark.parametrize("kind", ["nan", "pinf", "ninf", "pm_inf"])
-def test_q8_0_fused_nonfinite(ctx, kind):
+@pytest.mark.parametrize("dim,qd,kvd", [(1024, 1024, 256), (4096, 4096, 1024)])
+def test_q8_0_fused_nonfinite(ctx, kind, dim, qd, kvd):
     """RMSNorm-fused QKV / gate-up-SiLU / final-norm GEMV (a non-finite x makes
     every normalised value NaN in the reference's cpuRMSNorm, so every output
-    is NaN), and the unnormalised f16-out / residual-add GEMVs."""
+    is NaN), and the unnormalised f16-out / residual-add GEMVs (dim 4096: on
+    the K-sliced kernels)."""
     fk = FusedQ8Kernel(ctx)
-    dim, qd, kvd, inter, T = 1024, 1024, 256, 3072, 2
+    inter, T = 3072, 2
     Wq, Wk, Wv = weights("q8_0", qd, dim, 20), weights("q8_0", kvd, dim, 21), weights("q8_0", kvd, dim, 22)
     Wg, Wu = weights("q8_0", inter, dim, 23), weights("q8_0", inter, dim, 24)
     xs = [synth.normal_f32(synth.seed(90, 25), dim), poison(synth.normal_f32(synth.seed(90, 26), dim), kind)]
