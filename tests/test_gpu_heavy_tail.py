@@ -113,8 +113,9 @@ def test_plain_gemv(fam_gemv, fmt, M, K, amp):
 
 
 @pytest.mark.parametrize("amp", AMPS)
-def test_q4k_triple_and_geglu(gemv, amp):
-    K, rows = 2048, (1024, 512, 512)
+@pytest.mark.parametrize("K,rows", [(2048, (1024, 512, 512)),
+                                    (4096, (4096, 3072, 3072))])  # the K-sliced triple and GeGLU
+def test_q4k_triple_and_geglu(gemv, amp, K, rows):
     Ws, x = [], None
     for i, m in enumerate(rows):
         W, x = heavy_case("q4_k", m, K, amp, 3 + i * 0)
@@ -129,10 +130,10 @@ def test_q4k_triple_and_geglu(gemv, amp):
 
 
 @pytest.mark.parametrize("amp", AMPS)
-def test_fused_q8_with_norm(ctx, amp):
+@pytest.mark.parametrize("dim,qd,kvd", [(2048, 1024, 512), (4096, 4096, 1024)])  # second: the K-sliced QKV
+def test_fused_q8_with_norm(ctx, amp, dim, qd, kvd):
     """Fused QKV with RMSNorm: the normalised x keeps the outliers' ratio."""
     fk = FusedQ8Kernel(ctx)
-    dim, qd, kvd = 2048, 1024, 512
     Wq, x = heavy_case("q8_0", qd, dim, amp, 5)
     Wk, _ = heavy_case("q8_0", kvd, dim, amp, 6)
     Wv, _ = heavy_case("q8_0", kvd, dim, amp, 7)
