@@ -268,6 +268,10 @@ __device__ __forceinline__ T pick3(uint32_t m, T a, T b, T c) {
     v = m == 2u ? c : v;
     return v;
 }
+template <class T>
+__device__ __forceinline__ T pick2(bool second, T a, T b) {
+    return second ? b : a;
+}
 
 struct Q4Multi {
     const uint8_t *W[3];
@@ -1748,7 +1752,7 @@ struct CukQ8Pairs {
     float eps;
     uint32_t M;
     __device__ __forceinline__ const uint8_t *row(uint32_t r) const {
-        return pick3((r & 1u), Wg, Wu, Wu) + (size_t)(r >> 1) * rowBytes;
+        return pick2((r & 1u) != 0u, Wg, Wu) + (size_t)(r >> 1) * rowBytes;
     }
     __device__ __forceinline__ void store(uint32_t r, float v) const { y[(size_t)blockIdx.y * M + (r >> 1)] = v; }
 };
@@ -1761,7 +1765,7 @@ struct CukGegluPairs {
     size_t rowBytes;
     uint32_t M;
     __device__ __forceinline__ const uint8_t *row(uint32_t r) const {
-        return pick3((r & 1u), Wg, Wu, Wu) + (size_t)(r >> 1) * rowBytes;
+        return pick2((r & 1u) != 0u, Wg, Wu) + (size_t)(r >> 1) * rowBytes;
     }
     __device__ __forceinline__ void store(uint32_t r, float v) const { y[(size_t)blockIdx.y * M + (r >> 1)] = v; }
 };
