@@ -1076,8 +1076,9 @@ er_status encode_gemm(er_hip_ctx *ctx, er_stream stream, Fmt f, er_buffer W, er_
 // Q4_K 2 x 1024 9.14 -> 6.95, gate/up + SiLU 2 x 1024 13.05 -> 10.13.  A
 // slice filling 10 of 16 lanes (K = 5120) lost: 5120 + 2 x 1024 rows 8.88 ->
 // 10.28 (before the row sources held their pointers as values).
-// min4096: the rows per CU needed at K = 4096 (24 for the Q4_K GeGLU, whose
-// paired multi-matrix kernel held 2 x 1536 rows at 4.32 against 4.63 us).
+// min4096: the rows per CU needed at K = 4096 (20 for the Q4_K GeGLU, whose
+// paired multi-matrix kernel held 2 x 1536 and 2 x 2048 rows at 4.32 / 4.38
+// against 4.63 / 4.90 us, and lost 2 x 2560 at 6.22 against 5.32).
 bool fused_on_cuk(const er_hip_ctx *ctx, uint64_t Mt, uint32_t K, uint32_t min4096 = 12u) {
     if (ctx->multi_override >= 0 || ctx->multi1_override >= 0) return false;
     if (ctx->cuk_mode == 2) return true;
@@ -1153,11 +1154,12 @@ er_status encode_q4k_geglu(er_hip_ctx *ctx, er_stream stream, er_buffer Wg, er_b
     st = bind_device(ctx);
     if (st != ER_OK) return st;
     // large totals: the K-sliced kernels over the 2M gate/up rows, interleaved
-    // (fused_on_cuk; at K = 4096 from 24 rows per CU).  Same-box A/B, medians
+    // (fused_on_cuk; at K = 4096 from 20 rows per CU).  Same-box A/B, medians
     // of 4 (us): 2 x 14336 x 4096 18.51 -> 15.38, 2 x 3000 x 4096 6.26 -> 5.58,
-    // 2 x 1100 x 14336 12.13 -> 7.55; 2 x 1536 x 4096 4.32 -> 4.63 (kept).
+    // 2 x 2560 x 4096 6.22 -> 5.32, 2 x 1100 x 14336 12.13 -> 7.55; 2 x 2048 x
+    // 4096 4.38 -> 4.90 and 2 x 1536 4.32 -> 4.63 (kept).
     CukPlan kp;
-    if (M < 0x80000000u && fused_on_cuk(ctx, 2u * (uint64_t)M, K, 24u) &&
+    if (M < 0x80000000u && fused_on_cuk(ctx, 2u * (uint64_t)M, K, 20u) &&
         plan_cuk(ctx, Fmt::Q4_K, 2u * M, K, 1u, kp)) {
         void *kargs[] = {&Wg.data, &Wu.data, &x.data, &y.data, &M, &K};
         dim3 grid((2u * M + kp.rowsPerWg - 1u) / kp.rowsPerWg, 1, 1);

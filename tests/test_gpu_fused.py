@@ -64,7 +64,7 @@ def test_triple_shapes_match_oracle_and_single(gemv, rows, K):
 
 @pytest.mark.parametrize("M,K", [(3072, 1024), (10240, 2560), (33, 768),
                                  # 2M rows on the K-sliced kernels: 8, 4 and 2 rows per step
-                                 (3000, 4096), (1100, 8192), (1100, 14336),
+                                 (3000, 4096), (2560, 4096), (1100, 8192), (1100, 14336),
                                  # beyond the integer-dot kernels' 16384 weights: the fp32
                                  # pair kernel (encodeQ4KWeightsDualGeGLU takes any K % 256 == 0,
                                  # GEMVKernel.swift:930-976)
